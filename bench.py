@@ -1,0 +1,235 @@
+"""Benchmark of the exact SPLADE search path on one MI355X.
+
+Default workload (BASELINE.json's metric): config C3 -- 8.8M synthetic docs
+(~1.06e9 postings, fp16 posting weights, fp32 accumulation), batches of 512
+queries, k = 1000.  A step is one ``search`` of one 512-query batch: fused
+LDS-tile scoring with threshold selection, candidate selection, fp64 rescoring
+and the status check.  Inputs (index and query batch) are resident in HBM before
+the timed region.
+
+Prints one JSON line.  ``roofline`` is for the dominant kernel (the fused tile
+scoring kernel), timed with HIP events on its launch stream: algorithmic bytes =
+sum over queries and valid terms of the postings that launch streams x (4 B doc
+id + weight bytes).  ``cpu_baseline`` times the reference CPU path
+(cpu_sequential_score, restated in C) on a bounded sample of the same batch,
+pinned to C cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import resource
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "gpu-sparse_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "queries/s @8.8M docs k=1000 batch 512; scoring HBM GB/s as % of peak"
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="C3")
+    ap.add_argument("--n-docs", type=int, default=None, help="override the config's collection size")
+    ap.add_argument("--batch", type=int, default=512)
+    ap.add_argument("--k", type=int, default=1000)
+    ap.add_argument("--tile-log2", type=int, default=12)
+    ap.add_argument("--unroll", type=int, default=4)
+    ap.add_argument("--waves", type=int, default=0)
+    ap.add_argument("--cpu-queries-1", type=int, default=16, help="queries timed on one core")
+    ap.add_argument("--cpu-queries-all", type=int, default=64, help="queries timed on all cores")
+    ap.add_argument("--cpu-cores", type=int, default=16, help="cap on the cores of the all-core row")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--parity-queries", type=int, default=4)
+    ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
+    return ap.parse_args()
+
+
+def cpu_rows(index_h, ti, tw, k, n1, n_all, cap):
+    """Reference CPU path on one core and on `cap` cores: wall, CPU seconds,
+    CPU/wall and queries/s per row.  Pinned with sched_setaffinity (taskset's
+    syscall) and the thread-pool variables."""
+    from oracle import oracle as O
+    allowed = sorted(os.sched_getaffinity(0))
+    rows = []
+    for cores, nq in ((1, n1), (min(cap, len(allowed)), n_all)):
+        if nq <= 0:
+            continue
+        nq = min(nq, ti.shape[0])
+        pin = set(allowed[:cores])
+        for v in ("OMP_NUM_THREADS", "MKL_NUM_THREADS", "OPENBLAS_NUM_THREADS", "NUMEXPR_NUM_THREADS",
+                  "RAYON_NUM_THREADS"):
+            os.environ[v] = str(cores)
+        os.sched_setaffinity(0, pin)
+        try:
+            r0 = resource.getrusage(resource.RUSAGE_SELF)
+            t0 = time.perf_counter()
+            O.c_cpu_sequential(index_h, ti[:nq], tw[:nq], k, threads=cores)
+            wall = time.perf_counter() - t0
+            r1 = resource.getrusage(resource.RUSAGE_SELF)
+        finally:
+            os.sched_setaffinity(0, set(allowed))
+        cpu_s = (r1.ru_utime - r0.ru_utime) + (r1.ru_stime - r0.ru_stime)
+        ratio = cpu_s / wall if wall > 0 else 0.0
+        rows.append({"cores": cores, "queries": nq, "wall_s": round(wall, 3), "cpu_s": round(cpu_s, 3),
+                     "cpu_wall_ratio": round(ratio, 3), "qps": round(nq / wall, 3),
+                     "pinning_clean": bool(ratio < 1.35 * cores)})
+        log(f"cpu baseline cores={cores} queries={nq} wall={wall:.2f}s cpu/wall={ratio:.2f} "
+            f"q/s={nq / wall:.2f}")
+    return rows
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
+              "see DESIGN.md for how the index would shard.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import gpusparse as gs
+    from gpusparse import synth
+    from gpusparse.index import ensure_search_state
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    cfg = synth.CONFIGS[a.config]
+    if a.n_docs:
+        cfg = synth.scaled(cfg, n_docs=a.n_docs)
+    cfg = synth.scaled(cfg, n_queries=a.batch)
+
+    t0 = time.perf_counter()
+    docs, queries = synth.generate(cfg)
+    t_gen = time.perf_counter() - t0
+    log(f"generated {cfg.name}: {docs.shape[0]} docs, {docs.nnz} postings, {queries.shape[0]} queries "
+        f"in {t_gen:.1f}s")
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    index = gs.build_index(docs, dev)
+    torch.cuda.synchronize()
+    t_build = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    ensure_search_state(index, a.tile_log2)
+    torch.cuda.synchronize()
+    t_bounds = time.perf_counter() - t0
+    log(f"index built in {t_build:.2f}s (incl. H2D of the CSR), tile bounds {t_bounds:.3f}s")
+    qt, qw, T = gs.to_query_tensors(queries, dev)
+    B = qt.shape[0]
+    k = min(a.k, docs.shape[0])
+    del docs
+
+    def step(timing=None):
+        if a.path == "atomic":
+            return gs.atomic_fused_score(index, qt, qw, k)
+        return gs.search(index, (qt, qw), k, tile_log2=a.tile_log2, path=a.path, unroll=a.unroll,
+                         waves=a.waves, timing=timing)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    timing = {}
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        out = step(timing)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = 1000.0 * wall / a.steps
+    qps = B * a.steps / wall
+    log(f"{a.steps} steps: {ms_per_step:.2f} ms/step, {qps:.1f} queries/s, "
+        f"dense rows {timing.get('dense_rows', 0)}")
+
+    # ---- roofline of the fused tile-scoring kernel
+    wbytes = index.scores.element_size()
+    S = 0
+    roof = None
+    if a.path == "fused" and timing.get("score_kernel"):
+        kern_ms = [e0.elapsed_time(e1) for e0, e1 in timing["score_kernel"]]
+        call_ms = [e0.elapsed_time(e1) for e0, e1 in timing["search"]]
+        n_tiles = (index.num_docs + (1 << a.tile_log2) - 1) >> a.tile_log2
+        S = min(16, n_tiles)
+        tb = index.aux()[("tile_bounds", a.tile_log2)]
+        cols = tb[:, [S, n_tiles]].cpu().numpy().astype(np.int64)
+        per_term = cols[:, 1] - cols[:, 0]
+        all_term = index.lengths.cpu().numpy().astype(np.int64)
+        qt_h = qt.cpu().numpy()
+        valid = (qt_h >= 0) & (qt_h < index.vocab_size)
+        tq = np.where(valid, qt_h, 0)
+        post_launch = int((per_term[tq] * valid).sum())
+        post_all = int((all_term[tq] * valid).sum())
+        per_post = 4 + wbytes
+        bytes_launch = post_launch * per_post
+        avg_ms = float(np.mean(kern_ms))
+        achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": "k_score_tiles<emit> (fused LDS-tile scoring + threshold emission)",
+                "kernel_ms_avg": round(avg_ms, 3), "kernel_ms_min": round(float(np.min(kern_ms)), 3),
+                "scored_postings_per_launch": post_launch, "bytes_per_posting": per_post,
+                "algorithmic_bytes_per_launch": bytes_launch,
+                "search_call_ms_avg": round(float(np.mean(call_ms)), 3),
+                "batch_scored_postings": post_all,
+                "batch_gbs_algorithmic": round(post_all * per_post / (ms_per_step * 1e-3) / 1e9, 1)}
+        log(f"scoring kernel {avg_ms:.2f} ms avg: {achieved:.0f} GB/s algorithmic "
+            f"({100 * achieved / PEAK_HBM_GBS:.1f}% of {PEAK_HBM_GBS:.0f} GB/s); "
+            f"batch scored postings {post_all:.3e}")
+
+    # ---- parity sample at full size, and the CPU baseline
+    parity = None
+    cpu = None
+    need_host = a.parity_queries > 0 or not a.no_cpu
+    if need_host:
+        from gpusparse.index import to_host
+        from oracle import oracle as O
+        index_h = to_host(index)
+        ti_h, tw_h = qt.cpu().numpy(), qw.cpu().numpy()
+        if a.parity_queries > 0:
+            nq = min(a.parity_queries, B)
+            t0 = time.perf_counter()
+            vs, s64, vi = O.c_search(index_h, ti_h[:nq], tw_h[:nq], k, threads=min(16, os.cpu_count() or 1))
+            got_s, got_i = out[0][:nq].cpu().numpy(), out[1][:nq].cpu().numpy()
+            parity = {"queries_checked": nq, "ids_equal": bool(np.array_equal(got_i, vi)),
+                      "scores_equal": bool(np.array_equal(got_s, vs)),
+                      "max_abs_diff_vs_fp64": float(np.max(np.abs(got_s.astype(np.float64) - s64)))}
+            log(f"parity vs CPU oracle on {nq} queries: {parity} ({time.perf_counter() - t0:.1f}s)")
+        if not a.no_cpu:
+            rows = cpu_rows(index_h, ti_h, tw_h, k, a.cpu_queries_1, a.cpu_queries_all, a.cpu_cores)
+            best = rows[-1]
+            cpu = {"value": best["qps"], "unit": "queries/s", "cores": best["cores"], "kind": "port",
+                   "sample": f"first {best['queries']} queries of the batch over the full index "
+                             f"(reference CPU path cpu_sequential_score restated in C, fp32 accumulator)",
+                   "cpu_wall_ratio": best["cpu_wall_ratio"], "rows": rows}
+
+    n_docs = int(index.num_docs)
+    res = {
+        "metric": METRIC, "value": round(qps, 2), "unit": "queries/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32" if wbytes != 1 else "u32", "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: {cfg.description}", "n_docs": n_docs,
+                   "postings": int(index.lengths.sum().item()), "global_batch": B, "k": k, "max_query_terms": T,
+                   "weights": str(index.scores.dtype).replace("torch.", ""), "tile_docs": 1 << a.tile_log2,
+                   "path": a.path},
+        "roofline": roof, "cpu_baseline": cpu, "parity": parity,
+        "index_build_s": round(t_build, 3), "tile_bounds_s": round(t_bounds, 3), "generate_s": round(t_gen, 1),
+        "dense_rows": timing.get("dense_rows", 0),
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

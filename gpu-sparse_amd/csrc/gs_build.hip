@@ -1,0 +1,681 @@
+// Index construction and per-list checks/bounds for gfx950.
+//
+// The term-major layout is the reference's (lsr_benchmark_engine/
+// gpusparse_retrieval.py:81-115, src/run_correctness_verification.py:32-84):
+// postings of term t sit at [offsets[t], offsets[t] + lengths[t]), ascending in
+// doc id (a *stable* sort of the doc-major CSR by term), padded with (-1, 0) to a
+// multiple of 32 slots; offsets are the exclusive prefix sum of padded lengths.
+//
+// Here the transpose is a stable LSD radix sort over 8-bit digits of the term id
+// (two passes for a 30522-term vocabulary).  Each pass is
+//   histogram (per 4096-entry block, LDS)  ->  exclusive scan over (digit, block)
+//   ->  scatter with a stable in-block rank from 64-lane ballots,
+// and the last pass writes straight into the padded slot of each posting.
+#include <stdarg.h>
+
+#include "gs_common.h"
+
+static thread_local char g_err[512];
+
+void gs_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+extern "C" int gs_query_version(void) { return GS_ABI_VERSION; }
+extern "C" const char *gs_last_error(void) { return g_err; }
+
+namespace {
+
+constexpr int kLdsTermsMax = 40960;  // 160 KiB of uint32 counters
+constexpr int kRsThreads = 256;      // 4 waves
+constexpr int kRsRounds = 16;
+constexpr int kRsTile = kRsThreads * kRsRounds;  // entries per radix block
+constexpr int kScanTile = 4096;
+
+template <class T>
+__global__ void k_fill(T *p, int64_t n, T v) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// ------------------------------------------------------------------ block scan
+
+// Exclusive scan across the block (blockDim multiple of 64, <= 1024).
+template <class T>
+__device__ T block_excl_scan(T v, T *sh /* >= 16 */, T *total) {
+    const int lane = gs_lane(), wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    T x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        T o = __shfl_up(x, d, 64);
+        if (lane >= d) x += o;
+    }
+    if (lane == 63) sh[wave] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        T acc = 0;
+        for (int w = 0; w < nw; ++w) {
+            T s = sh[w];
+            sh[w] = acc;
+            acc += s;
+        }
+        sh[16] = acc;
+    }
+    __syncthreads();
+    T r = sh[wave] + x - v;
+    *total = sh[16];
+    __syncthreads();
+    return r;
+}
+
+// ------------------------------------------------------------------ term counts
+
+__global__ void __launch_bounds__(1024) k_term_count_lds(const int32_t *__restrict__ idx, int64_t nnz,
+                                                         int32_t V, int32_t *lengths,
+                                                         unsigned long long *n_bad) {
+    extern __shared__ uint32_t h[];
+    for (int i = threadIdx.x; i < V; i += blockDim.x) h[i] = 0;
+    __syncthreads();
+    uint32_t bad = 0;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nnz;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int32_t t = idx[i];
+        if ((uint32_t)t < (uint32_t)V)
+            atomicAdd(&h[t], 1u);
+        else
+            ++bad;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < V; i += blockDim.x)
+        if (h[i]) atomicAdd(reinterpret_cast<uint32_t *>(lengths) + i, h[i]);
+    if (bad) atomicAdd(n_bad, (unsigned long long)bad);
+}
+
+__global__ void k_term_count_global(const int32_t *__restrict__ idx, int64_t nnz, int32_t V,
+                                    int32_t *lengths, unsigned long long *n_bad) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nnz;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int32_t t = idx[i];
+        if ((uint32_t)t < (uint32_t)V)
+            atomicAdd(reinterpret_cast<uint32_t *>(lengths) + t, 1u);
+        else
+            atomicAdd(n_bad, 1ull);
+    }
+}
+
+// padded = ceil32(lengths); offsets = exclusive scan(padded); optionally
+// delta = offsets - exclusive scan(lengths).  Single block of 1024 threads.
+__global__ void __launch_bounds__(1024) k_term_scan(const int32_t *lengths, int32_t V, int32_t *padded,
+                                                    int64_t *offsets, int64_t *delta, int64_t *info,
+                                                    const unsigned long long *n_bad) {
+    __shared__ int64_t sh[17];
+    __shared__ int64_t sh2[17];
+    int64_t carry = 0, carry_seg = 0;
+    for (int base = 0; base < V; base += blockDim.x) {
+        int i = base + threadIdx.x;
+        int64_t len = i < V ? lengths[i] : 0;
+        int64_t pad = (len + 31) & ~int64_t(31);
+        int64_t tot, tot2;
+        int64_t ex = block_excl_scan<int64_t>(pad, sh, &tot);
+        int64_t ex2 = block_excl_scan<int64_t>(len, sh2, &tot2);
+        if (i < V) {
+            if (padded) padded[i] = (int32_t)pad;
+            if (offsets) offsets[i] = carry + ex;
+            if (delta) delta[i] = (carry + ex) - (carry_seg + ex2);
+        }
+        carry += tot;
+        carry_seg += tot2;
+    }
+    if (threadIdx.x == 0 && info) {
+        info[0] = carry;
+        info[1] = n_bad ? (int64_t)*n_bad : 0;
+    }
+}
+
+// ------------------------------------------------------------------ radix sort
+
+// Doc (row) id of every CSR entry: one wave per row.
+__global__ void k_row_ids(const int64_t *__restrict__ indptr, int64_t n_rows, uint32_t *__restrict__ row_of) {
+    const int lane = gs_lane();
+    const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    for (int64_t r = wave; r < n_rows; r += nwaves) {
+        int64_t b = indptr[r], e = indptr[r + 1];
+        for (int64_t i = b + lane; i < e; i += 64) row_of[i] = (uint32_t)r;
+    }
+}
+
+__device__ __forceinline__ uint32_t load_code(const void *p, int64_t i, int src_bytes) {
+    if (src_bytes == 4) return reinterpret_cast<const uint32_t *>(p)[i];
+    if (src_bytes == 2) return reinterpret_cast<const uint16_t *>(p)[i];
+    return reinterpret_cast<const uint8_t *>(p)[i];
+}
+
+__global__ void __launch_bounds__(kRsThreads) k_rs_hist(const uint32_t *__restrict__ key, int64_t n, int shift,
+                                                        uint32_t *__restrict__ hist, int64_t nblocks) {
+    __shared__ uint32_t h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const int64_t base = blockIdx.x * (int64_t)kRsTile;
+    for (int r = 0; r < kRsRounds; ++r) {
+        int64_t i = base + r * kRsThreads + threadIdx.x;
+        if (i < n) atomicAdd(&h[(key[i] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    hist[(int64_t)threadIdx.x * nblocks + blockIdx.x] = h[threadIdx.x];
+}
+
+// Device-wide exclusive scan of uint32 (three launches).
+__global__ void __launch_bounds__(1024) k_scan_reduce(const uint32_t *__restrict__ in, int64_t n,
+                                                      uint32_t *__restrict__ part) {
+    __shared__ uint32_t sh[17];
+    const int64_t base = blockIdx.x * (int64_t)kScanTile;
+    uint32_t s = 0;
+    for (int j = threadIdx.x; j < kScanTile; j += blockDim.x)
+        if (base + j < n) s += in[base + j];
+    s = gs_wave_sum(s);
+    if (gs_lane() == 0) sh[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += sh[w];
+        part[blockIdx.x] = t;
+    }
+}
+
+__global__ void __launch_bounds__(1024) k_scan_parts(uint32_t *part, int64_t nparts) {
+    __shared__ uint32_t sh[17];
+    uint32_t carry = 0;
+    for (int64_t b = 0; b < nparts; b += blockDim.x) {
+        int64_t i = b + threadIdx.x;
+        uint32_t v = i < nparts ? part[i] : 0, tot;
+        uint32_t ex = block_excl_scan<uint32_t>(v, sh, &tot);
+        if (i < nparts) part[i] = carry + ex;
+        carry += tot;
+    }
+}
+
+__global__ void __launch_bounds__(1024) k_scan_down(uint32_t *__restrict__ data, int64_t n,
+                                                    const uint32_t *__restrict__ part) {
+    __shared__ uint32_t sh[17];
+    const int64_t base = blockIdx.x * (int64_t)kScanTile;
+    uint32_t carry = part[blockIdx.x];
+    for (int j = 0; j < kScanTile; j += blockDim.x) {
+        int64_t i = base + j + threadIdx.x;
+        uint32_t v = i < n ? data[i] : 0, tot;
+        uint32_t ex = block_excl_scan<uint32_t>(v, sh, &tot);
+        if (i < n) data[i] = carry + ex;
+        carry += tot;
+    }
+}
+
+// Stable scatter of one 8-bit digit.  Entries of a block are taken in rounds of
+// 256 (wave w of round r owns entries r*256 + w*64 + lane), so the rank of an
+// entry among equal digits is: digits of earlier rounds + earlier waves of this
+// round + earlier lanes of this wave (from a 64-lane ballot match).
+template <bool FINAL, int WT>
+__global__ void __launch_bounds__(kRsThreads)
+    k_rs_scatter(const uint32_t *__restrict__ key_in, const uint32_t *__restrict__ doc_in,
+                 const void *__restrict__ code_in, int src_code_bytes, int64_t n, int shift, int bits,
+                 const uint32_t *__restrict__ scanned, int64_t nblocks, uint32_t *__restrict__ key_out,
+                 uint32_t *__restrict__ doc_out, uint32_t *__restrict__ code_out,
+                 const int64_t *__restrict__ delta, int32_t *__restrict__ final_doc,
+                 void *__restrict__ final_w) {
+    __shared__ uint32_t run[256];
+    __shared__ uint32_t wcnt[4][256];
+    const int tid = threadIdx.x, lane = gs_lane(), wave = tid >> 6;
+    run[tid] = scanned[(int64_t)tid * nblocks + blockIdx.x];
+    const int64_t base = blockIdx.x * (int64_t)kRsTile;
+    for (int r = 0; r < kRsRounds; ++r) {
+        wcnt[0][tid] = 0;
+        wcnt[1][tid] = 0;
+        wcnt[2][tid] = 0;
+        wcnt[3][tid] = 0;
+        __syncthreads();
+        const int64_t i = base + r * kRsThreads + tid;
+        const bool valid = i < n;
+        uint32_t k = 0, d = 0, c = 0, dig = 0;
+        if (valid) {
+            k = key_in[i];
+            d = doc_in[i];
+            c = load_code(code_in, i, src_code_bytes);
+            dig = (k >> shift) & 255u;
+        }
+        uint64_t peers = __ballot(valid);
+        for (int b = 0; b < bits; ++b) {
+            const bool bit = (dig >> b) & 1u;
+            const uint64_t m = __ballot(bit);
+            peers &= bit ? m : ~m;
+        }
+        const uint32_t rank = __popcll(peers & gs_lanemask_lt());
+        if (valid && rank == 0) wcnt[wave][dig] = __popcll(peers);
+        __syncthreads();
+        if (valid) {
+            uint32_t pos = run[dig] + rank;
+            for (int w = 0; w < wave; ++w) pos += wcnt[w][dig];
+            if (FINAL) {
+                const int64_t slot = (int64_t)pos + delta[k];
+                final_doc[slot] = (int32_t)d;
+                if (WT == GS_W_F32)
+                    reinterpret_cast<uint32_t *>(final_w)[slot] = c;
+                else if (WT == GS_W_F16)
+                    reinterpret_cast<uint16_t *>(final_w)[slot] = (uint16_t)c;
+                else
+                    reinterpret_cast<uint8_t *>(final_w)[slot] = (uint8_t)c;
+            } else {
+                key_out[pos] = k;
+                doc_out[pos] = d;
+                code_out[pos] = c;
+            }
+        }
+        __syncthreads();
+        run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+        __syncthreads();
+    }
+    (void)lane;
+}
+
+// Padding slots [offsets + lengths, offsets + padded) <- (-1, 0).
+template <int WT>
+__global__ void k_fill_pads(const int64_t *__restrict__ offsets, const int32_t *__restrict__ lengths,
+                            const int32_t *__restrict__ padded, int32_t V, int32_t *__restrict__ doc_ids,
+                            void *__restrict__ w) {
+    const int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t t = g >> 5;
+    const int j = (int)(g & 31);
+    if (t >= V) return;
+    const int64_t slot = offsets[t] + lengths[t] + j;
+    if (slot >= offsets[t] + padded[t]) return;
+    doc_ids[slot] = -1;
+    if (WT == GS_W_F32)
+        reinterpret_cast<float *>(w)[slot] = 0.0f;
+    else if (WT == GS_W_F16)
+        reinterpret_cast<uint16_t *>(w)[slot] = 0;
+    else
+        reinterpret_cast<uint8_t *>(w)[slot] = 0;
+}
+
+// ------------------------------------------------------------------ per-list scans
+
+constexpr int kListParts = 16;  // waves per list for the per-list passes
+
+template <int WT>
+__device__ __forceinline__ float weight_as_float(const void *w, int64_t i) {
+    if (WT == GS_W_F32) return reinterpret_cast<const float *>(w)[i];
+    if (WT == GS_W_F16) return (float)reinterpret_cast<const _Float16 *>(w)[i];
+    return (float)reinterpret_cast<const uint8_t *>(w)[i];
+}
+
+// max and max |w| per list, as monotone keys (max_key) and abs bits (max_abs_bits).
+template <int WT>
+__global__ void k_list_max(const void *__restrict__ w, const int64_t *__restrict__ offsets,
+                           const int32_t *__restrict__ lengths, int32_t V, uint32_t *max_key,
+                           uint32_t *max_abs_bits) {
+    const int lane = gs_lane();
+    const int64_t wv = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+    const int64_t t = wv / kListParts;
+    const int part = (int)(wv % kListParts);
+    if (t >= V) return;
+    const int64_t L = lengths[t], o = offsets[t];
+    const int64_t per = (L + kListParts - 1) / kListParts;
+    const int64_t b = part * per, e = b + per < L ? b + per : L;
+    if (b >= e) return;
+    uint32_t mk = 0, ma = 0;
+    for (int64_t i = b + lane; i < e; i += 64) {
+        float v = weight_as_float<WT>(w, o + i);
+        uint32_t k = gs_key_f32(v), a = __float_as_uint(fabsf(v));
+        mk = k > mk ? k : mk;
+        ma = a > ma ? a : ma;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        uint32_t o1 = __shfl_xor(mk, d, 64), o2 = __shfl_xor(ma, d, 64);
+        mk = o1 > mk ? o1 : mk;
+        ma = o2 > ma ? o2 : ma;
+    }
+    if (lane == 0) {
+        atomicMax(max_key + t, mk);
+        atomicMax(max_abs_bits + t, ma);
+    }
+}
+
+__global__ void k_list_max_final(const uint32_t *max_key, const uint32_t *max_abs_bits,
+                                 const int32_t *lengths, int32_t V, float *max_scores, float *max_abs) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= V) return;
+    const bool nz = lengths[t] > 0;
+    if (max_scores) max_scores[t] = nz ? gs_unkey_f32(max_key[t]) : 0.0f;
+    if (max_abs) max_abs[t] = nz ? __uint_as_float(max_abs_bits[t]) : 0.0f;
+}
+
+// Non-ascending flag and count of equal neighbours per list.
+__global__ void k_check_lists(const int32_t *__restrict__ doc, const int64_t *__restrict__ offsets,
+                              const int32_t *__restrict__ lengths, int32_t V, int32_t *bad, int32_t *dup) {
+    const int lane = gs_lane();
+    const int64_t wv = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+    const int64_t t = wv / kListParts;
+    const int part = (int)(wv % kListParts);
+    if (t >= V) return;
+    const int64_t L = lengths[t], o = offsets[t];
+    const int64_t per = (L + kListParts - 1) / kListParts;
+    int64_t b = part * per;
+    const int64_t e = b + per < L ? b + per : L;
+    if (b < 1) b = 1;
+    if (b >= e) return;
+    uint32_t nbad = 0, ndup = 0;
+    for (int64_t i = b + lane; i < e; i += 64) {
+        int32_t cur = doc[o + i], prev = doc[o + i - 1];
+        nbad += cur < prev;
+        ndup += cur == prev;
+    }
+    nbad = gs_wave_sum(nbad);
+    ndup = gs_wave_sum(ndup);
+    if (lane == 0) {
+        if (nbad) atomicOr(reinterpret_cast<uint32_t *>(bad) + t, 1u);
+        if (ndup) atomicAdd(reinterpret_cast<uint32_t *>(dup) + t, ndup);
+    }
+}
+
+__global__ void __launch_bounds__(1024) k_count_flags(const int32_t *flags, int32_t V, int64_t *out) {
+    __shared__ uint32_t sh[17];
+    uint32_t c = 0;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) c += flags[i] != 0;
+    c = gs_wave_sum(c);
+    if (gs_lane() == 0) sh[threadIdx.x >> 6] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += sh[w];
+        out[0] = t;
+    }
+}
+
+__device__ __forceinline__ int64_t lower_bound_i32(const int32_t *a, int64_t n, int64_t x) {
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        int64_t mid = (lo + hi) >> 1;
+        if ((int64_t)a[mid] < x)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+__global__ void k_chunk_bounds(const int32_t *__restrict__ doc, const int64_t *__restrict__ offsets,
+                               const int32_t *__restrict__ lengths, int32_t V, int64_t n_docs,
+                               int64_t chunk, int64_t n_chunks, int64_t *__restrict__ bounds) {
+    const int64_t total = (n_chunks + 1) * (int64_t)V;
+    for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < total;
+         g += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t c = g / V, t = g % V;
+        const int64_t edge = c < n_chunks ? c * chunk : n_docs;
+        const int64_t o = offsets[t];
+        bounds[g] = o + lower_bound_i32(doc + o, lengths[t], edge);
+    }
+}
+
+__global__ void k_tile_bounds(const int32_t *__restrict__ doc, const int64_t *__restrict__ offsets,
+                              const int32_t *__restrict__ lengths, int32_t V, int32_t tile_log2,
+                              int64_t n_tiles, int32_t *__restrict__ bounds) {
+    const int64_t row = n_tiles + 1;
+    const int64_t total = row * (int64_t)V;
+    for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < total;
+         g += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = g / row, j = g % row;
+        const int64_t o = offsets[t];
+        bounds[g] = (int32_t)lower_bound_i32(doc + o, lengths[t], j << tile_log2);
+    }
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" int gs_index_count(const int32_t *indices_d, int64_t nnz, int32_t vocab, int32_t *lengths_d,
+                              int32_t *padded_d, int64_t *offsets_d, int64_t *info_d, void *stream) {
+    GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
+    GS_REQUIRE(nnz >= 0 && nnz < 0xFFFFFFFFll, "nnz %lld outside [0, 2^32-1)", (long long)nnz);
+    GS_REQUIRE(lengths_d && padded_d && offsets_d && info_d, "null output pointer");
+    GS_REQUIRE(nnz == 0 || indices_d, "null indices");
+    hipStream_t s = gs_stream(stream);
+    // info_d doubles as the 64-bit bad-entry counter until the scan writes it.
+    unsigned long long *n_bad = reinterpret_cast<unsigned long long *>(info_d + 1);
+    k_fill<int32_t><<<gs_blocks(vocab, 256), 256, 0, s>>>(lengths_d, vocab, 0);
+    k_fill<int64_t><<<1, 64, 0, s>>>(info_d, 2, 0);
+    GS_CHECK_LAUNCH();
+    if (nnz > 0) {
+        if (vocab <= kLdsTermsMax) {
+            size_t lds = sizeof(uint32_t) * (size_t)vocab;
+            GS_CHECK_HIP(hipFuncSetAttribute((const void *)k_term_count_lds,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            unsigned blocks = gs_blocks(nnz, 1024 * 64, 512);
+            k_term_count_lds<<<blocks, 1024, lds, s>>>(indices_d, nnz, vocab, lengths_d, n_bad);
+        } else {
+            k_term_count_global<<<gs_blocks(nnz, 256, 65536), 256, 0, s>>>(indices_d, nnz, vocab,
+                                                                          lengths_d, n_bad);
+        }
+        GS_CHECK_LAUNCH();
+    }
+    k_term_scan<<<1, 1024, 0, s>>>(lengths_d, vocab, padded_d, offsets_d, nullptr, info_d, n_bad);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+namespace {
+struct FillPlan {
+    int passes;
+    int64_t nblocks;
+    int64_t hist_n;
+    int64_t nparts;
+};
+FillPlan fill_plan(int64_t nnz, int32_t vocab) {
+    FillPlan p;
+    int bits = 0;
+    while (bits < 31 && (1ll << bits) < (int64_t)vocab) ++bits;
+    p.passes = bits <= 8 ? 1 : (bits + 7) / 8;
+    p.nblocks = (nnz + kRsTile - 1) / kRsTile;
+    if (p.nblocks < 1) p.nblocks = 1;
+    p.hist_n = 256 * p.nblocks;
+    p.nparts = (p.hist_n + kScanTile - 1) / kScanTile;
+    return p;
+}
+size_t fill_layout(int64_t nnz, int32_t vocab, gs_arena &a, uint32_t **row_of, uint32_t *kb[2],
+                   uint32_t *db[2], uint32_t *cb[2], uint32_t **hist, uint32_t **parts, int64_t **delta,
+                   uint32_t **mk, uint32_t **ma) {
+    FillPlan p = fill_plan(nnz, vocab);
+    *row_of = a.take<uint32_t>(nnz);
+    int nbuf = p.passes >= 3 ? 2 : (p.passes == 2 ? 1 : 0);
+    for (int b = 0; b < 2; ++b) {
+        kb[b] = b < nbuf ? a.take<uint32_t>(nnz) : nullptr;
+        db[b] = b < nbuf ? a.take<uint32_t>(nnz) : nullptr;
+        cb[b] = b < nbuf ? a.take<uint32_t>(nnz) : nullptr;
+    }
+    *hist = a.take<uint32_t>(p.hist_n);
+    *parts = a.take<uint32_t>(p.nparts);
+    *delta = a.take<int64_t>(vocab);
+    *mk = a.take<uint32_t>(vocab);
+    *ma = a.take<uint32_t>(vocab);
+    return a.used;
+}
+}  // namespace
+
+extern "C" size_t gs_index_fill_workspace(int64_t nnz, int32_t vocab) {
+    gs_arena a{nullptr, 0, 0};
+    uint32_t *r, *kb[2], *db[2], *cb[2], *h, *pp, *mk, *ma;
+    int64_t *dl;
+    return fill_layout(nnz, vocab, a, &r, kb, db, cb, &h, &pp, &dl, &mk, &ma) + 256;
+}
+
+template <int WT>
+static int index_fill_impl(const int64_t *indptr_d, const int32_t *indices_d, const void *data_d,
+                           int64_t n_docs, int64_t nnz, int32_t vocab, const int64_t *offsets_d,
+                           const int32_t *lengths_d, const int32_t *padded_d, int32_t *doc_ids_d,
+                           void *weights_d, float *max_scores_d, float *max_abs_d, void *ws,
+                           size_t ws_bytes, hipStream_t s) {
+    gs_arena a{reinterpret_cast<char *>(ws), 0, ws_bytes};
+    uint32_t *row_of, *kb[2], *db[2], *cb[2], *hist, *parts, *mk, *ma;
+    int64_t *delta;
+    fill_layout(nnz, vocab, a, &row_of, kb, db, cb, &hist, &parts, &delta, &mk, &ma);
+    if (!a.ok()) {
+        gs_set_error("index_fill workspace too small: need %zu bytes, got %zu", a.used, ws_bytes);
+        return GS_ENOSPC;
+    }
+    const FillPlan p = fill_plan(nnz, vocab);
+    const int src_bytes = WT == GS_W_F32 ? 4 : (WT == GS_W_F16 ? 2 : 1);
+
+    // per-term delta = offsets - exclusive scan(lengths): padded slot of a sorted position
+    k_term_scan<<<1, 1024, 0, s>>>(lengths_d, vocab, nullptr, nullptr, delta, nullptr, nullptr);
+    k_fill_pads<WT><<<gs_blocks((int64_t)vocab * 32, 256), 256, 0, s>>>(offsets_d, lengths_d, padded_d,
+                                                                        vocab, doc_ids_d, weights_d);
+    GS_CHECK_LAUNCH();
+    if (nnz > 0) {
+        k_row_ids<<<gs_blocks(n_docs * 64, 256, 65536), 256, 0, s>>>(indptr_d, n_docs, row_of);
+        GS_CHECK_LAUNCH();
+        const uint32_t *key_in = reinterpret_cast<const uint32_t *>(indices_d);
+        const uint32_t *doc_in = row_of;
+        const void *code_in = data_d;
+        int code_bytes = src_bytes;
+        int cur = 0;
+        for (int pass = 0; pass < p.passes; ++pass) {
+            const int shift = 8 * pass;
+            const bool last = pass == p.passes - 1;
+            int bits = 8;
+            {
+                int total_bits = 0;
+                while (total_bits < 31 && (1ll << total_bits) < (int64_t)vocab) ++total_bits;
+                if (total_bits < 1) total_bits = 1;
+                int rem = total_bits - shift;
+                bits = rem < 8 ? rem : 8;
+                if (bits < 1) bits = 1;
+            }
+            k_rs_hist<<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(key_in, nnz, shift, hist, p.nblocks);
+            k_scan_reduce<<<(unsigned)p.nparts, 1024, 0, s>>>(hist, p.hist_n, parts);
+            k_scan_parts<<<1, 1024, 0, s>>>(parts, p.nparts);
+            k_scan_down<<<(unsigned)p.nparts, 1024, 0, s>>>(hist, p.hist_n, parts);
+            GS_CHECK_LAUNCH();
+            if (last) {
+                k_rs_scatter<true, WT><<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(
+                    key_in, doc_in, code_in, code_bytes, nnz, shift, bits, hist, p.nblocks, nullptr, nullptr,
+                    nullptr, delta, doc_ids_d, weights_d);
+            } else {
+                k_rs_scatter<false, WT><<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(
+                    key_in, doc_in, code_in, code_bytes, nnz, shift, bits, hist, p.nblocks, kb[cur], db[cur],
+                    cb[cur], nullptr, nullptr, nullptr);
+                key_in = kb[cur];
+                doc_in = db[cur];
+                code_in = cb[cur];
+                code_bytes = 4;
+                cur ^= 1;
+            }
+            GS_CHECK_LAUNCH();
+        }
+    }
+    // max_scores / max_abs
+    k_fill<uint32_t><<<gs_blocks(vocab, 256), 256, 0, s>>>(mk, vocab, 0u);
+    k_fill<uint32_t><<<gs_blocks(vocab, 256), 256, 0, s>>>(ma, vocab, 0u);
+    k_list_max<WT><<<gs_blocks((int64_t)vocab * kListParts * 64, 256), 256, 0, s>>>(
+        weights_d, offsets_d, lengths_d, vocab, mk, ma);
+    k_list_max_final<<<gs_blocks(vocab, 256), 256, 0, s>>>(mk, ma, lengths_d, vocab, max_scores_d,
+                                                          max_abs_d);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+extern "C" int gs_index_fill(const int64_t *indptr_d, const int32_t *indices_d, const void *data_d,
+                             int32_t wtype, int64_t n_docs, int64_t nnz, int32_t vocab,
+                             const int64_t *offsets_d, const int32_t *lengths_d, const int32_t *padded_d,
+                             int64_t n_slots, int32_t *doc_ids_d, void *weights_d, float *max_scores_d,
+                             float *max_abs_d, void *workspace_d, size_t workspace_bytes, void *stream) {
+    GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
+    GS_REQUIRE(n_docs >= 0 && n_docs < 0x7FFFFFFFll, "n_docs %lld outside [0, 2^31-1)", (long long)n_docs);
+    GS_REQUIRE(nnz >= 0 && nnz < 0xFFFFFFFFll, "nnz %lld outside [0, 2^32-1)", (long long)nnz);
+    GS_REQUIRE(n_slots >= nnz, "n_slots %lld < nnz %lld", (long long)n_slots, (long long)nnz);
+    GS_REQUIRE(indptr_d && offsets_d && lengths_d && padded_d, "null input pointer");
+    GS_REQUIRE(nnz == 0 || (indices_d && data_d), "null CSR arrays");
+    GS_REQUIRE(n_slots == 0 || (doc_ids_d && weights_d), "null output arrays");
+    hipStream_t s = gs_stream(stream);
+    switch (wtype) {
+        case GS_W_F32:
+            return index_fill_impl<GS_W_F32>(indptr_d, indices_d, data_d, n_docs, nnz, vocab, offsets_d,
+                                             lengths_d, padded_d, doc_ids_d, weights_d, max_scores_d,
+                                             max_abs_d, workspace_d, workspace_bytes, s);
+        case GS_W_F16:
+            return index_fill_impl<GS_W_F16>(indptr_d, indices_d, data_d, n_docs, nnz, vocab, offsets_d,
+                                             lengths_d, padded_d, doc_ids_d, weights_d, max_scores_d,
+                                             max_abs_d, workspace_d, workspace_bytes, s);
+        case GS_W_U8:
+            return index_fill_impl<GS_W_U8>(indptr_d, indices_d, data_d, n_docs, nnz, vocab, offsets_d,
+                                            lengths_d, padded_d, doc_ids_d, weights_d, max_scores_d,
+                                            max_abs_d, workspace_d, workspace_bytes, s);
+        default:
+            gs_set_error("unknown weight type %d", wtype);
+            return GS_EINVAL;
+    }
+}
+
+extern "C" int gs_check_lists(const int32_t *doc_ids_d, const int64_t *offsets_d, const int32_t *lengths_d,
+                              int32_t vocab, int32_t *bad_d, int32_t *dup_d, int64_t *info_d, void *stream) {
+    GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
+    GS_REQUIRE(offsets_d && lengths_d && bad_d && dup_d && info_d, "null pointer");
+    hipStream_t s = gs_stream(stream);
+    k_fill<int32_t><<<gs_blocks(vocab, 256), 256, 0, s>>>(bad_d, vocab, 0);
+    k_fill<int32_t><<<gs_blocks(vocab, 256), 256, 0, s>>>(dup_d, vocab, 0);
+    k_check_lists<<<gs_blocks((int64_t)vocab * kListParts * 64, 256), 256, 0, s>>>(
+        doc_ids_d, offsets_d, lengths_d, vocab, bad_d, dup_d);
+    k_count_flags<<<1, 1024, 0, s>>>(bad_d, vocab, info_d);
+    k_count_flags<<<1, 1024, 0, s>>>(lengths_d, vocab, info_d + 1);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+extern "C" int gs_list_max(const void *weights_d, int32_t wtype, const int64_t *offsets_d, const int32_t *lengths_d,
+                           int32_t vocab, float *max_scores_d, float *max_abs_d, void *workspace_d,
+                           size_t workspace_bytes, void *stream) {
+    GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
+    GS_REQUIRE(weights_d && offsets_d && lengths_d && workspace_d, "null pointer");
+    GS_REQUIRE(workspace_bytes >= 2 * sizeof(uint32_t) * (size_t)vocab, "list_max workspace too small");
+    hipStream_t s = gs_stream(stream);
+    uint32_t *mk = reinterpret_cast<uint32_t *>(workspace_d), *ma = mk + vocab;
+    k_fill<uint32_t><<<gs_blocks(2 * (int64_t)vocab, 256), 256, 0, s>>>(mk, 2 * (int64_t)vocab, 0u);
+    const unsigned g = gs_blocks((int64_t)vocab * kListParts * 64, 256);
+    switch (wtype) {
+        case GS_W_F32: k_list_max<GS_W_F32><<<g, 256, 0, s>>>(weights_d, offsets_d, lengths_d, vocab, mk, ma); break;
+        case GS_W_F16: k_list_max<GS_W_F16><<<g, 256, 0, s>>>(weights_d, offsets_d, lengths_d, vocab, mk, ma); break;
+        case GS_W_U8: k_list_max<GS_W_U8><<<g, 256, 0, s>>>(weights_d, offsets_d, lengths_d, vocab, mk, ma); break;
+        default: gs_set_error("unknown weight type %d", wtype); return GS_EINVAL;
+    }
+    k_list_max_final<<<gs_blocks(vocab, 256), 256, 0, s>>>(mk, ma, lengths_d, vocab, max_scores_d, max_abs_d);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+extern "C" int gs_chunk_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d, const int32_t *lengths_d,
+                               int32_t vocab, int64_t n_docs, int64_t doc_chunk, int64_t *bounds_d,
+                               void *stream) {
+    GS_REQUIRE(vocab > 0 && n_docs >= 0, "bad sizes");
+    GS_REQUIRE(doc_chunk > 0, "doc_chunk must be positive, got %lld", (long long)doc_chunk);
+    const int64_t n_chunks = (n_docs + doc_chunk - 1) / doc_chunk;
+    const int64_t total = (n_chunks + 1) * (int64_t)vocab;
+    k_chunk_bounds<<<gs_blocks(total, 256, 1 << 16), 256, 0, gs_stream(stream)>>>(
+        doc_ids_d, offsets_d, lengths_d, vocab, n_docs, doc_chunk, n_chunks, bounds_d);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+extern "C" int gs_tile_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d, const int32_t *lengths_d,
+                              int32_t vocab, int64_t n_docs, int32_t tile_log2, int32_t *bounds_d,
+                              void *stream) {
+    GS_REQUIRE(vocab > 0 && n_docs >= 0, "bad sizes");
+    GS_REQUIRE(tile_log2 >= 6 && tile_log2 <= 16, "tile_log2 %d outside [6, 16]", tile_log2);
+    const int64_t n_tiles = (n_docs + (1ll << tile_log2) - 1) >> tile_log2;
+    const int64_t total = (n_tiles + 1) * (int64_t)vocab;
+    k_tile_bounds<<<gs_blocks(total, 256, 1 << 16), 256, 0, gs_stream(stream)>>>(
+        doc_ids_d, offsets_d, lengths_d, vocab, tile_log2, n_tiles, bounds_d);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}

@@ -1,0 +1,136 @@
+// Internal helpers shared by the gfx950 kernels of libgpusparse.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "gpusparse.h"
+
+// ------------------------------------------------------------------ errors
+
+void gs_set_error(const char *fmt, ...);
+
+#define GS_CHECK_HIP(expr)                                                               \
+    do {                                                                                 \
+        hipError_t _e = (expr);                                                          \
+        if (_e != hipSuccess) {                                                          \
+            gs_set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__, \
+                         __LINE__);                                                      \
+            return GS_EHIP;                                                              \
+        }                                                                                \
+    } while (0)
+
+#define GS_CHECK_LAUNCH() GS_CHECK_HIP(hipGetLastError())
+
+#define GS_REQUIRE(cond, ...)         \
+    do {                              \
+        if (!(cond)) {                \
+            gs_set_error(__VA_ARGS__); \
+            return GS_EINVAL;         \
+        }                             \
+    } while (0)
+
+static inline hipStream_t gs_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+static inline unsigned gs_blocks(int64_t n, int per_block, int64_t cap = 1 << 20) {
+    int64_t b = (n + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > cap) b = cap;
+    return (unsigned)b;
+}
+
+// 256-byte aligned bump allocator over a caller workspace.
+struct gs_arena {
+    char *base;
+    size_t used;
+    size_t cap;
+    template <class T>
+    T *take(size_t n) {
+        size_t off = (used + 255) & ~size_t(255);
+        used = off + n * sizeof(T);
+        return reinterpret_cast<T *>(base ? base + off : nullptr);
+    }
+    bool ok() const { return used <= cap; }
+};
+
+// ------------------------------------------------------------------ device helpers
+
+constexpr int GS_WAVE = 64;
+
+__device__ __forceinline__ int gs_lane() { return (int)(threadIdx.x & (GS_WAVE - 1)); }
+
+__device__ __forceinline__ uint64_t gs_lanemask_lt() {
+    return (1ull << gs_lane()) - 1ull;
+}
+
+__device__ __forceinline__ int gs_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Order-preserving maps of scores onto unsigned integers (larger score -> larger key).
+__device__ __forceinline__ uint32_t gs_key_f32(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float gs_unkey_f32(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+__device__ __forceinline__ uint64_t gs_key_f64(double d) {
+    uint64_t u = (uint64_t)__double_as_longlong(d);
+    return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+}
+__device__ __forceinline__ double gs_unkey_f64(uint64_t k) {
+    uint64_t u = (k & 0x8000000000000000ull) ? (k & 0x7FFFFFFFFFFFFFFFull) : ~k;
+    return __longlong_as_double((long long)u);
+}
+
+// Weight decoding by storage type.
+template <int WT>
+struct gs_weight;
+template <>
+struct gs_weight<GS_W_F32> {
+    using store_t = float;
+    using acc_t = float;
+    using qw_t = float;
+    __device__ __forceinline__ static float decode(float w) { return w; }
+};
+template <>
+struct gs_weight<GS_W_F16> {
+    using store_t = _Float16;
+    using acc_t = float;
+    using qw_t = float;
+    __device__ __forceinline__ static float decode(_Float16 w) { return (float)w; }
+};
+template <>
+struct gs_weight<GS_W_U8> {
+    using store_t = uint8_t;
+    using acc_t = uint32_t;
+    using qw_t = uint8_t;
+    __device__ __forceinline__ static uint32_t decode(uint8_t w) { return (uint32_t)w; }
+};
+
+// Histogram bin of a positive score: bits of its fp32 value >> 20 (exponent and
+// three mantissa bits, ~9% wide bins), 2048 bins cover every positive float.
+constexpr int GS_HIST_BINS = 2048;
+__device__ __forceinline__ uint32_t gs_bin_of(float v) { return __float_as_uint(v) >> 20; }
+__device__ __forceinline__ float gs_bin_edge(uint32_t b) { return __uint_as_float(b << 20); }
+
+// Wave-wide inclusive prefix sum of 32-bit values (lane order).
+__device__ __forceinline__ uint32_t gs_wave_incl_scan(uint32_t v) {
+#pragma unroll
+    for (int d = 1; d < GS_WAVE; d <<= 1) {
+        uint32_t o = __shfl_up(v, d, GS_WAVE);
+        if (gs_lane() >= d) v += o;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t gs_wave_sum(uint32_t v) {
+#pragma unroll
+    for (int d = GS_WAVE / 2; d >= 1; d >>= 1) v += __shfl_xor(v, d, GS_WAVE);
+    return v;
+}
+
+// Relaxed device-scope loads/stores of shared counters (bypass the per-CU cache).
+__device__ __forceinline__ uint32_t gs_load_relaxed(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}

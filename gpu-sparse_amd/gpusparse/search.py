@@ -1,0 +1,254 @@
+"""Batched exact search and the reference's scoring entry points.
+
+``search(index, query_batch, k)`` is the batched retrieval call: scores and doc
+ids of the k best documents per query, ordered by score descending, ties by doc
+id ascending.  ``triton_fused_score`` (src/triton_kernel.py:159-200) keeps the
+reference's name and signature.  Both run the fused LDS-tile pipeline of
+``gs_search`` and finish the rare rows it flags with the dense path
+(``gs_search_dense``), or run the dense path directly when the full
+``[B, num_docs]`` score rows are small.
+
+Float indexes return float32 scores equal to the fp64 scatter-add rounded to
+float32; uint8 indexes return the exact uint32 sums as int32.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+from .index import DEFAULT_TILE_LOG2, gs_index_struct, _device_of
+
+MAX_K = 8192
+DEFAULT_DENSE_BUDGET = 1 << 30   # bytes of [B, N] score rows below which the dense path is used
+
+
+def _check_pow2(block_pl: int) -> None:
+    # same check as src/triton_kernel.py:175-176
+    assert block_pl > 0 and (block_pl & (block_pl - 1)) == 0, \
+        f"block_pl must be a positive power of 2, got {block_pl}"
+
+
+def query_tensors(index, query_batch):
+    """(term ids int32 [B, T], weights [B, T]) on the index device, from a tuple of
+    tensors/arrays or from a query CSR (no truncation, as to_query_tensors)."""
+    dev = _device_of(index)
+    if isinstance(query_batch, tuple) and len(query_batch) in (2, 3) and not hasattr(query_batch, "indptr"):
+        qt, qw = query_batch[0], query_batch[1]
+    else:
+        from .engine import to_query_tensors
+        qt, qw, _ = to_query_tensors(query_batch, dev)
+    qt = torch.as_tensor(qt).to(dev)
+    qw = torch.as_tensor(qw).to(dev)
+    if qt.dim() != 2 or qw.shape != qt.shape:
+        raise ValueError(f"query term ids {tuple(qt.shape)} and weights {tuple(qw.shape)} must be the same [B, T]")
+    if qt.dtype != torch.int32:
+        qt = qt.to(torch.int32)
+    want = torch.uint8 if index.scores.dtype == torch.uint8 else torch.float32
+    if qw.dtype != want:
+        if want == torch.uint8:
+            raise ValueError("a uint8 index takes uint8 query weights")
+        qw = qw.to(want)
+    return qt.contiguous(), qw.contiguous()
+
+
+def _workspace(index, nbytes: int) -> torch.Tensor:
+    a = index.aux()
+    ws = a.get("workspace")
+    if ws is None or ws.numel() < nbytes:
+        a.pop("workspace", None)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=_device_of(index))
+        a["workspace"] = ws
+    return ws
+
+
+def _dense_rows(index, gidx, qt, qw, k, rows, out_s, out_i, dense_budget):
+    """Runs gs_search_dense for `rows` (int32 device tensor or None = all)."""
+    L = _lib.lib()
+    dev = _device_of(index)
+    B, T = qt.shape
+    R = B if rows is None else int(rows.numel())
+    if R == 0:
+        return
+    one = _lib.C.c_size_t()
+    _lib.check(L.gs_search_dense_workspace(_lib.C.byref(gidx), 1, _lib.C.byref(one)), "gs_search_dense_workspace")
+    per_row = max(int(one.value), 1)
+    rows_per_pass = max(1, min(R, dense_budget // per_row))
+    ws = torch.empty(rows_per_pass * per_row, dtype=torch.uint8, device=dev)
+    _lib.check(L.gs_search_dense(_lib.C.byref(gidx), _lib.ptr(qt), _lib.ptr(qw), B, T, k, _lib.ptr(rows), R,
+                                 _lib.ptr(out_s), _lib.ptr(out_i), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev)),
+               "gs_search_dense")
+
+
+def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG2, path: str = "auto",
+           sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 4, waves: int = 0,
+           dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None):
+    """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
+
+    path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense".
+    timing: optional dict; receives event pairs on the launch stream bracketing the
+    fused scoring kernel ("score_kernel") and the whole gs_search call ("search"),
+    and the number of rows finished by the dense path ("dense_rows")."""
+    dev = _lib.require_gpu(_device_of(index))
+    N = int(index.num_docs)
+    kk = min(int(k), N)
+    if kk < 1:
+        raise ValueError(f"k must be >= 1, got {k}")
+    if kk > MAX_K:
+        raise ValueError(f"k={kk} exceeds the supported maximum {MAX_K}")
+    qt, qw = query_tensors(index, query_batch)
+    B, T = qt.shape
+    out_dtype = torch.int32 if index.scores.dtype == torch.uint8 else torch.float32
+    out_s = torch.empty((B, kk), dtype=out_dtype, device=dev)
+    out_i = torch.empty((B, kk), dtype=torch.int64, device=dev)
+    if B == 0:
+        return out_s, out_i
+    if T == 0:
+        qt = torch.full((B, 1), -1, dtype=torch.int32, device=dev)
+        qw = torch.zeros((B, 1), dtype=qw.dtype, device=dev)
+        T = 1
+    gidx = gs_index_struct(index, tile_log2)
+    L = _lib.lib()
+    acc_bytes = 4 if index.scores.dtype == torch.uint8 else 8
+    dense_bytes = B * gidx.n_tiles * (1 << tile_log2) * acc_bytes
+    if path not in ("auto", "fused", "dense"):
+        raise ValueError(f"unknown path {path!r}")
+    use_dense = path == "dense" or (path == "auto" and dense_bytes <= dense_budget)
+    if use_dense:
+        _dense_rows(index, gidx, qt, qw, kk, None, out_s, out_i, max(dense_budget, 1))
+        return out_s, out_i
+    opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, waves, None, None)
+    need = _lib.C.c_size_t()
+    _lib.check(L.gs_search_workspace(_lib.C.byref(gidx), B, T, kk, _lib.C.byref(opts), _lib.C.byref(need)),
+               "gs_search_workspace")
+    ws = _workspace(index, int(need.value))
+    status = torch.empty(B, dtype=torch.int32, device=dev)
+    s = _lib.stream_ptr(dev)
+    if timing is not None:
+        # events recorded by gs_search itself around the fused scoring kernel, and
+        # around the whole gs_search call, on the launch stream
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        for e in evs:
+            e.record()
+        opts.ev_score_begin, opts.ev_score_end = evs[0].cuda_event, evs[1].cuda_event
+        evs[2].record()
+    _lib.check(L.gs_search(_lib.C.byref(gidx), _lib.ptr(qt), _lib.ptr(qw), B, T, kk, _lib.C.byref(opts),
+                           _lib.ptr(out_s), _lib.ptr(out_i), _lib.ptr(status), _lib.ptr(ws), ws.numel(), s),
+               "gs_search")
+    if timing is not None:
+        evs[3].record()
+        timing.setdefault("score_kernel", []).append((evs[0], evs[1]))
+        timing.setdefault("search", []).append((evs[2], evs[3]))
+    st = status.cpu().numpy()
+    bad = np.nonzero(st != _lib.GS_ROW_DONE)[0]
+    if timing is not None:
+        timing["dense_rows"] = timing.get("dense_rows", 0) + int(bad.size)
+    if bad.size:
+        rows = torch.from_numpy(bad.astype(np.int32)).to(dev)
+        _dense_rows(index, gidx, qt, qw, kk, rows, out_s, out_i, max(dense_budget, 1))
+    return out_s, out_i
+
+
+def triton_fused_score(index, query_term_ids: torch.Tensor, query_term_scores: torch.Tensor, top_k: int = 10,
+                       block_pl: int = 128):
+    """Drop-in for triton_fused_score (src/triton_kernel.py:159-200): exact top-k,
+    (scores [B, k] desc, ids [B, k] int64).  block_pl sets the posting loads in
+    flight per lane (block_pl / 64, clamped to 1..8)."""
+    _check_pow2(block_pl)
+    unroll = max(1, min(8, block_pl // 64))
+    return search(index, (query_term_ids, query_term_scores), top_k, unroll=unroll)
+
+
+def compacted_topk(scores: torch.Tensor, tau: torch.Tensor, k: int, max_cand: int = 8192, block: int = 1024):
+    """Drop-in for compacted_topk (src/fused_topk.py:71-103): top-k of `scores`
+    [B, L] among entries >= tau[B]; (values [B, kk], chunk-local indices [B, kk]),
+    missing slots (-inf, 0).  Rows with more than max_cand candidates are selected
+    from the full row.  `block` is accepted for signature compatibility."""
+    if scores.dim() != 2:
+        raise ValueError("scores must be [B, L]")
+    dev = _lib.require_gpu(scores.device)
+    B, Lc = scores.shape
+    kk = min(int(k), Lc)
+    if kk > MAX_K:
+        raise ValueError(f"k={kk} exceeds the supported maximum {MAX_K}")
+    max_cand = max(int(max_cand), kk)
+    if scores.dtype != torch.float32 or scores.stride(1) != 1:
+        scores = scores.float().contiguous()
+    tau_d = None
+    if tau is not None:
+        tau_d = torch.as_tensor(tau, dtype=torch.float32, device=dev).contiguous()
+    out_v = torch.empty((B, kk), dtype=torch.float32, device=dev)
+    out_i = torch.empty((B, kk), dtype=torch.int64, device=dev)
+    if B == 0:
+        return out_v, out_i
+    counts = torch.empty(B, dtype=torch.int32, device=dev)
+    L = _lib.lib()
+    ws = torch.empty(L.gs_compacted_topk_workspace(B, max_cand), dtype=torch.uint8, device=dev)
+    _lib.check(L.gs_compacted_topk(_lib.ptr(scores), scores.stride(0), B, Lc, _lib.ptr(tau_d), kk, max_cand,
+                                   _lib.ptr(out_v), _lib.ptr(out_i), _lib.ptr(counts), _lib.ptr(ws), ws.numel(),
+                                   _lib.stream_ptr(dev)), "gs_compacted_topk")
+    return out_v, out_i
+
+
+def topk_rows(scores: torch.Tensor, k: int):
+    """Exact top-k of each row (torch.topk semantics on [B, L]; ties: lower column first)."""
+    return compacted_topk(scores, None, k, max_cand=max(k, 1))
+
+
+def scatter_add(index, query_term_ids, query_term_scores, out: torch.Tensor, lo=None, hi=None, chunk_start: int = 0,
+                chunk_len: int | None = None, block_pl: int = 128) -> torch.Tensor:
+    """The reference kernel on this GPU: per (query, term) program, global atomic
+    adds of q*w into `out` (pre-zeroed, [B, >= chunk_len], row stride out.stride(0)).
+    lo/hi: int64 [V] posting bounds of one chunk (_chunked_scatter_add_kernel,
+    src/triton_kernel_chunked.py:34-80) or None for whole lists
+    (_fast_scatter_add_kernel, src/triton_kernel.py:93-156)."""
+    _check_pow2(block_pl)
+    dev = _lib.require_gpu(_device_of(index))
+    qt, qw = query_tensors(index, (query_term_ids, query_term_scores))
+    B, T = qt.shape
+    clen = int(index.num_docs) if chunk_len is None else int(chunk_len)
+    gidx = _lib.GsIndex()
+    gidx.doc_ids_d = index.doc_ids.data_ptr()
+    gidx.weights_d = index.scores.data_ptr()
+    gidx.offsets_d = index.offsets.data_ptr()
+    gidx.lengths_d = index.lengths.data_ptr()
+    gidx.n_docs = int(index.num_docs)
+    gidx.vocab = int(index.vocab_size)
+    gidx.wtype = index.wtype
+    want = torch.int32 if index.scores.dtype == torch.uint8 else torch.float32
+    if out.dtype != want or out.dim() != 2 or out.stride(1) != 1 or out.device != dev:
+        raise ValueError(f"out must be a row-contiguous [B, L] {want} tensor on {dev}")
+    if out.shape[0] < B or out.shape[1] < clen:
+        raise ValueError(f"out {tuple(out.shape)} is smaller than [{B}, {clen}]")
+    V = int(index.vocab_size)
+    for b in (lo, hi):
+        if b is not None and (b.dtype != torch.int64 or b.numel() != V or b.device != dev):
+            raise ValueError(f"chunk bounds must be int64 [{V}] tensors on {dev}")
+    if (lo is None) != (hi is None):
+        raise ValueError("lo and hi must both be given or both be None")
+    if B == 0 or T == 0:
+        return out
+    lo = None if lo is None else lo.contiguous()
+    hi = None if hi is None else hi.contiguous()
+    _lib.check(_lib.lib().gs_scatter_add(_lib.C.byref(gidx), _lib.ptr(lo), _lib.ptr(hi), _lib.ptr(qt), _lib.ptr(qw),
+                                         B, T, _lib.ptr(out), int(chunk_start), clen, out.stride(0), block_pl,
+                                         _lib.stream_ptr(dev)), "gs_scatter_add")
+    return out
+
+
+def atomic_fused_score(index, query_term_ids, query_term_scores, top_k: int = 10, block_pl: int = 128):
+    """The reference's monolithic algorithm on this GPU (zeroed [B, N] fp32
+    accumulator, global-atomic scatter-add, exact row top-k): the baseline the
+    LDS-tile path is compared against.  Scores are fp32 sums in atomic order."""
+    dev = _lib.require_gpu(_device_of(index))
+    qt, qw = query_tensors(index, (query_term_ids, query_term_scores))
+    B = qt.shape[0]
+    N = int(index.num_docs)
+    dt = torch.int32 if index.scores.dtype == torch.uint8 else torch.float32
+    out = torch.zeros((B, N), dtype=dt, device=dev)
+    scatter_add(index, qt, qw, out, block_pl=block_pl)
+    if dt == torch.int32:
+        # uint8 sums stay below 2^24 for queries of <= 258 terms, where fp32 is exact
+        v, i = topk_rows(out.to(torch.float32), top_k)
+        return v.to(torch.int32), i
+    return topk_rows(out, top_k)

@@ -1,0 +1,192 @@
+/*
+ * gpusparse.h - C ABI of the MI355X (gfx950) exact SPLADE scoring library.
+ *
+ * The reference (ashutoshuiuc/gpu-sparse) has no native library: its only "FFI"
+ * is the Triton JIT launch `kernel[grid](ptrs..., BLOCK_PL=...)`.  Each entry
+ * point below replaces one such launch, or a numpy / torch step on the same
+ * path, and names the reference code it stands in for.
+ *
+ * Conventions
+ *  - Every pointer argument named *_d is a device pointer (hipMalloc / torch).
+ *  - `stream` is a hipStream_t passed as void*; NULL means the null stream.
+ *  - No entry point allocates device memory or synchronises the host: scratch
+ *    memory is a caller-provided workspace whose size the matching
+ *    *_workspace() call reports, and results are produced asynchronously.
+ *  - Return value: GS_OK, or an error code with a message from gs_last_error()
+ *    (thread-local).  GS_EINVAL maps to ValueError, GS_EHIP to RuntimeError.
+ */
+#ifndef GPUSPARSE_H
+#define GPUSPARSE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_ABI_VERSION 1
+
+#define GS_OK 0
+#define GS_EINVAL 1   /* bad argument or layout */
+#define GS_EHIP 2     /* HIP runtime error */
+#define GS_ENOSPC 3   /* workspace smaller than the *_workspace() size */
+
+/* posting-weight storage types */
+#define GS_W_F32 0    /* fp32 weights, fp32 query weights, fp32 tiles, fp64-exact output */
+#define GS_W_F16 1    /* IEEE binary16 weights, otherwise as GS_W_F32 */
+#define GS_W_U8 2     /* uint8 impacts and uint8 query weights, exact uint32 sums */
+
+/* Per-query status written by gs_search. */
+#define GS_ROW_DONE 0
+#define GS_ROW_DENSE 1  /* row must be finished by gs_search_dense (rare: overflow or < k positive scores) */
+
+/*
+ * Device-resident term-major inverted index: the layout of the reference's
+ * GPUInvertedIndex (src/gpu_inverted_index.py:21-35) plus the per-(term, doc
+ * tile) posting bounds this library schedules by.
+ */
+typedef struct gs_index {
+    const int32_t *doc_ids_d;     /* [n_slots] doc ids, ascending within each list, -1 padding */
+    const void *weights_d;        /* [n_slots] weights in `wtype`, 0 padding */
+    const int64_t *offsets_d;     /* [vocab] first slot of each list */
+    const int32_t *lengths_d;     /* [vocab] postings per list (before padding) */
+    const float *max_abs_d;       /* [vocab] max |weight| per list (0 for empty lists) */
+    const int32_t *dup_d;         /* [vocab] equal adjacent doc ids per list (0 when canonical) */
+    const int32_t *tile_bounds_d; /* [vocab][n_tiles + 1] list-relative first posting of each doc tile */
+    int64_t n_slots;
+    int64_t n_docs;
+    int32_t vocab;
+    int32_t wtype;                /* GS_W_* */
+    int32_t tile_log2;            /* docs per tile = 1 << tile_log2 */
+    int32_t n_tiles;              /* ceil(n_docs / tile) */
+} gs_index;
+
+/* Tuning knobs of gs_search; zero selects the default. */
+typedef struct gs_search_opts {
+    int32_t sample_tiles;  /* doc tiles scored densely to seed the k-th-score threshold (default 16) */
+    int32_t cand_cap;      /* candidates kept per query before the dense fallback (default 65536) */
+    int32_t unroll;        /* posting loads in flight per lane: block_pl / 64, 1..8 (default 4) */
+    int32_t waves;         /* queries per tile workgroup: 4 or 8 (default: 8 if the tile fits) */
+    void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
+    void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
+} gs_search_opts;
+
+int gs_query_version(void);
+const char *gs_last_error(void);
+
+/* ------------------------------------------------------------ index build
+ * Replaces the host numpy builders build_index
+ * (lsr_benchmark_engine/gpusparse_retrieval.py:81-115) and
+ * build_gpu_index_from_csr (src/run_correctness_verification.py:32-84):
+ * stable term-major transpose of a doc-major CSR, lists padded to 32 slots.
+ *
+ * Step 1, gs_index_count: lengths, padded lengths, exclusive offsets.
+ *   info_d[0] <- n_slots (= offsets[V-1] + padded[V-1]),
+ *   info_d[1] <- entries whose term id is outside [0, vocab) (build must not proceed).
+ * Step 2, gs_index_fill: stable LSD radix sort of (term; doc, weight) by term,
+ *   scattered into the padded layout; also max_scores (signed max per list, 0 if
+ *   empty: run_correctness_verification.py:63,71) and max_abs.
+ */
+int gs_index_count(const int32_t *indices_d, int64_t nnz, int32_t vocab, int32_t *lengths_d,
+                   int32_t *padded_d, int64_t *offsets_d, int64_t *info_d, void *stream);
+size_t gs_index_fill_workspace(int64_t nnz, int32_t vocab);
+int gs_index_fill(const int64_t *indptr_d, const int32_t *indices_d, const void *data_d, int32_t wtype,
+                  int64_t n_docs, int64_t nnz, int32_t vocab, const int64_t *offsets_d,
+                  const int32_t *lengths_d, const int32_t *padded_d, int64_t n_slots,
+                  int32_t *doc_ids_d, void *weights_d, float *max_scores_d, float *max_abs_d,
+                  void *workspace_d, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------ list checks and bounds
+ * gs_check_lists replaces the ascending-doc-id validation of
+ * build_chunk_boundaries (src/triton_kernel_chunked.py:96-108) and the invariant
+ * check of src/remeasure_2026_09.py:261-299:
+ *   bad_d[t] <- 1 if list t has doc[i] < doc[i-1], dup_d[t] <- #(doc[i] == doc[i-1]),
+ *   info_d[0] <- number of non-ascending lists, info_d[1] <- number of non-empty lists.
+ */
+int gs_check_lists(const int32_t *doc_ids_d, const int64_t *offsets_d, const int32_t *lengths_d,
+                   int32_t vocab, int32_t *bad_d, int32_t *dup_d, int64_t *info_d, void *stream);
+
+/* Per-list max weight (max_scores of run_correctness_verification.py:63,71: signed
+ * max, 0 for empty lists) and max |weight|, for indexes assembled outside
+ * gs_index_fill.  Workspace: 8 * vocab bytes. */
+int gs_list_max(const void *weights_d, int32_t wtype, const int64_t *offsets_d, const int32_t *lengths_d,
+                int32_t vocab, float *max_scores_d, float *max_abs_d, void *workspace_d,
+                size_t workspace_bytes, void *stream);
+
+/* Replaces build_chunk_boundaries (src/triton_kernel_chunked.py:110-122):
+ *   bounds_d[c][t] = offsets[t] + lower_bound(list t, edge_c), edges = c*doc_chunk
+ *   (c < n_chunks) and n_docs; shape [n_chunks + 1][vocab], int64.
+ * Lists must be ascending (gs_check_lists). */
+int gs_chunk_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d, const int32_t *lengths_d,
+                    int32_t vocab, int64_t n_docs, int64_t doc_chunk, int64_t *bounds_d, void *stream);
+
+/* Per-(term, doc tile) bounds used by gs_search: bounds_d[t][j] = lower_bound(list t,
+ * j << tile_log2) relative to offsets[t], j = 0..n_tiles; shape [vocab][n_tiles + 1].
+ * The reference's per-(term, chunk) sub-ranges at LDS-tile granularity. */
+int gs_tile_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d, const int32_t *lengths_d,
+                   int32_t vocab, int64_t n_docs, int32_t tile_log2, int32_t *bounds_d, void *stream);
+
+/* ------------------------------------------------------------ search
+ * Replaces triton_fused_score (src/triton_kernel.py:159-200) and
+ * triton_chunked_score_fused (src/fused_topk.py:106-160): exact top-k of
+ *   score[q, d] = sum_j q_weights[q, j] * w(q_terms[q, j], d)
+ * over valid terms (0 <= term < vocab; others are skipped as in
+ * triton_kernel.py:126-128), ordered by score descending then doc id ascending.
+ *   q_terms_d   int32 [B][T] (-1 padding), q_weights_d float32 (or uint8 for GS_W_U8) [B][T]
+ *   out_scores_d float32 [B][k] (int32 for GS_W_U8), out_ids_d int64 [B][k]
+ *   status_d    int32 [B]: GS_ROW_DONE, or GS_ROW_DENSE when the row has to be
+ *               recomputed with gs_search_dense (its outputs are then undefined).
+ * Float indexes accumulate fp32 in LDS doc tiles and rescore the selected
+ * candidates in fp64 in query-term order, so scores equal the fp64 scatter-add
+ * rounded to fp32.  1 <= k <= min(n_docs, 8192). */
+int gs_search_workspace(const gs_index *index, int32_t B, int32_t T, int32_t k,
+                        const gs_search_opts *opts, size_t *bytes);
+int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d, int32_t B,
+              int32_t T, int32_t k, const gs_search_opts *opts, void *out_scores_d,
+              int64_t *out_ids_d, int32_t *status_d, void *workspace_d, size_t workspace_bytes,
+              void *stream);
+
+/* Monolithic exact path (the reference's [B, N] accumulator, triton_kernel.py:182-199):
+ * rows listed in rows_d (int32 [R], or NULL for rows 0..B-1) are scored densely
+ * over all documents (fp64 or uint32 tiles written to a dense row buffer) and
+ * selected exactly; results go to the same rows of out_*.  The workspace bounds
+ * how many rows are processed per pass (at least one row must fit). */
+int gs_search_dense_workspace(const gs_index *index, int32_t rows_per_pass, size_t *bytes);
+int gs_search_dense(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d,
+                    int32_t B, int32_t T, int32_t k, const int32_t *rows_d, int32_t R,
+                    void *out_scores_d, int64_t *out_ids_d, void *workspace_d,
+                    size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------ dense-row selection
+ * Replaces compacted_topk (src/fused_topk.py:71-103) and its
+ * _compact_above_threshold_kernel (:33-68): entries of scores_d[B][L] (row stride
+ * ld) with value >= tau_d[b] are compacted into a [B][max_cand] candidate buffer,
+ * then the top kk = min(k, L) are returned sorted descending (ties: lower column
+ * first); missing slots are (-inf, 0).  Rows with more than max_cand candidates
+ * are selected from the full row, as the reference's overflow path does.
+ * tau_d may be NULL (plain torch.topk semantics on the row).  counts_d int32 [B]
+ * receives the per-row candidate count. */
+size_t gs_compacted_topk_workspace(int32_t B, int32_t max_cand);
+int gs_compacted_topk(const float *scores_d, int64_t ld, int32_t B, int64_t L, const float *tau_d,
+                      int32_t k, int32_t max_cand, float *out_values_d, int64_t *out_idx_d,
+                      int32_t *counts_d, void *workspace_d, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------ atomic scatter-add
+ * The reference's scoring kernel itself: _fast_scatter_add_kernel
+ * (src/triton_kernel.py:93-156) when lo_d/hi_d are NULL, and
+ * _chunked_scatter_add_kernel (src/triton_kernel_chunked.py:34-80) when they are
+ * the [vocab] posting bounds of one chunk.  One program per (query, term) streams
+ * the postings and adds q*w into out_d[q*out_stride + doc - chunk_start] with
+ * global fp32 atomics (uint32 for GS_W_U8); docs outside [chunk_start,
+ * chunk_start + chunk_len) and padding are skipped.  out_d must be pre-zeroed. */
+int gs_scatter_add(const gs_index *index, const int64_t *lo_d, const int64_t *hi_d,
+                   const int32_t *q_terms_d, const void *q_weights_d, int32_t B, int32_t T,
+                   void *out_d, int64_t chunk_start, int64_t chunk_len, int64_t out_stride,
+                   int32_t block_pl, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GPUSPARSE_H */

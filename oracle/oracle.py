@@ -1,0 +1,322 @@
+"""CPU oracle for the exact SPLADE scoring path.  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module or the C library next to it (liboracle.so), and only as the checker
+or as the timed CPU baseline -- never as part of the product path.
+
+Each function restates one piece of the reference (ashutoshuiuc/gpu-sparse) in
+plain numpy, citing the file:line it follows.  The reference has no test suite
+and no golden vectors; every function here is pinned in tests/test_oracle.py
+against an independent computation (brute force over Python lists, dense matrix
+products, exhaustive sorting, closed forms):
+
+  build_index            pinned: dict-of-lists builder + layout invariants
+  chunk_bounds           pinned: linear scan per list + partition invariant
+  scores_f64 / _u32      pinned: dense Q @ D^T (float64 / int64) on small inputs
+  scores_f32_sequential  pinned: scalar float32 loop of gpu_scoring.py:246-251
+  topk                   pinned: Python sorted() with the same key
+  compacted_topk         pinned: topk of the thresholded row
+  to_query_tensors       pinned: explicit per-row loop
+  fp16 / u8 codes        pinned: numpy float16 cast / closed-form values
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+BLOCK = 32
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+
+# ------------------------------------------------------------------ index build
+
+
+def build_index(indptr, indices, data, n_docs: int, vocab: int) -> dict:
+    """Term-major padded index of a doc-major CSR.
+
+    Follows lsr_benchmark_engine/gpusparse_retrieval.py:81-115 (stable argsort of
+    the COO column, bincount lengths, padding to 32, exclusive cumsum offsets,
+    copy of each list, pads -1 / 0) and adds max_scores as
+    src/run_correctness_verification.py:63,71 does (per-list max, 0 if empty)."""
+    indptr = np.asarray(indptr, dtype=np.int64)
+    cols = np.asarray(indices, dtype=np.int64)
+    vals = np.asarray(data)
+    rows = np.repeat(np.arange(n_docs, dtype=np.int64), np.diff(indptr))
+    if cols.size and (cols.min() < 0 or cols.max() >= vocab):
+        raise IndexError(f"term id outside [0, {vocab})")
+    order = np.argsort(cols, kind="stable")
+    terms, docs, scores = cols[order], rows[order], vals[order]
+    lengths = np.bincount(terms, minlength=vocab).astype(np.int32)
+    padded = ((lengths + BLOCK - 1) // BLOCK) * BLOCK
+    offsets = np.zeros(vocab, dtype=np.int64)
+    if vocab > 1:
+        np.cumsum(padded[:-1], out=offsets[1:])
+    total = int(offsets[-1] + padded[-1])
+    all_docs = np.full(total, -1, dtype=np.int32)
+    all_scores = np.zeros(total, dtype=vals.dtype)
+    max_scores = np.zeros(vocab, dtype=np.float32)
+    pos = 0
+    for t in np.nonzero(lengths)[0]:
+        L = int(lengths[t])
+        o = int(offsets[t])
+        all_docs[o:o + L] = docs[pos:pos + L]
+        all_scores[o:o + L] = scores[pos:pos + L]
+        max_scores[t] = scores[pos:pos + L].astype(np.float32).max()
+        pos += L
+    return {"doc_ids": all_docs, "scores": all_scores, "offsets": offsets, "lengths": lengths,
+            "padded_lengths": padded.astype(np.int32), "max_scores": max_scores,
+            "num_docs": int(n_docs), "vocab_size": int(vocab)}
+
+
+def chunk_bounds(doc_ids, offsets, lengths, vocab: int, n_docs: int, doc_chunk: int) -> np.ndarray:
+    """[n_chunks + 1, vocab] posting bounds, src/triton_kernel_chunked.py:89-122,
+    including its ValueError for non-ascending lists (:99-108)."""
+    n_chunks = (n_docs + doc_chunk - 1) // doc_chunk
+    n_bad = 0
+    for t in np.nonzero(lengths)[0]:
+        seg = doc_ids[offsets[t]: offsets[t] + lengths[t]]
+        if np.any(np.diff(seg) < 0):
+            n_bad += 1
+    if n_bad:
+        raise ValueError(
+            f"{n_bad} of {int((lengths > 0).sum())} posting lists are not ascending in "
+            f"doc_id. Chunked scoring requires ascending lists (build the index with "
+            f"np.argsort(..., kind='stable')); otherwise results are silently wrong.")
+    bounds = np.zeros((n_chunks + 1, vocab), dtype=np.int64)
+    edges = [c * doc_chunk for c in range(n_chunks)] + [n_docs]
+    for t in range(vocab):
+        L = int(lengths[t])
+        if L == 0:
+            bounds[:, t] = offsets[t]
+            continue
+        seg = doc_ids[offsets[t]: offsets[t] + L]
+        first = int(np.searchsorted(seg, 0, side="left"))
+        rel = np.searchsorted(seg[first:], edges, side="left")
+        bounds[:, t] = offsets[t] + first + rel
+    return bounds
+
+
+# ------------------------------------------------------------------ scoring
+
+
+def decode_weights(scores: np.ndarray) -> np.ndarray:
+    """Stored weights as float64 (fp16 and uint8 decode exactly)."""
+    return scores.astype(np.float64)
+
+
+def _postings(index, t):
+    o = int(index["offsets"][t])
+    L = int(index["lengths"][t])
+    return index["doc_ids"][o:o + L], index["scores"][o:o + L]
+
+
+def scores_f64(index: dict, q_terms: np.ndarray, q_weights: np.ndarray) -> np.ndarray:
+    """Exhaustive fp64 scatter-add, query terms in order and postings in list order:
+    the sum of src/triton_kernel.py:142-156 (out[q, doc] += wq * w) accumulated in
+    float64 (products of fp32/fp16/u8 values are exact in float64).  [B, N]."""
+    B, T = q_terms.shape
+    N, V = index["num_docs"], index["vocab_size"]
+    out = np.zeros((B, N), dtype=np.float64)
+    for q in range(B):
+        acc = out[q]
+        for j in range(T):
+            t = int(q_terms[q, j])
+            if t < 0 or t >= V:          # skipped as in triton_kernel.py:126-128
+                continue
+            d, w = _postings(index, t)
+            np.add.at(acc, d, float(q_weights[q, j]) * decode_weights(w))
+    return out
+
+
+def scores_u32(index: dict, q_terms: np.ndarray, q_weights: np.ndarray) -> np.ndarray:
+    """Integer scatter-add of uint8 impacts and uint8 query weights, [B, N] uint32."""
+    B, T = q_terms.shape
+    N, V = index["num_docs"], index["vocab_size"]
+    out = np.zeros((B, N), dtype=np.uint64)
+    for q in range(B):
+        for j in range(T):
+            t = int(q_terms[q, j])
+            if t < 0 or t >= V:
+                continue
+            d, w = _postings(index, t)
+            np.add.at(out[q], d, np.uint64(q_weights[q, j]) * w.astype(np.uint64))
+    assert out.max(initial=0) < 2 ** 32
+    return out.astype(np.uint32)
+
+
+def scores_f32_sequential(index: dict, q_terms: np.ndarray, q_weights: np.ndarray) -> np.ndarray:
+    """The reference CPU path's accumulation (src/gpu_scoring.py:241-251): float32
+    accumulator per query, doc_scores[doc] += q * w in query-term then posting order."""
+    B, T = q_terms.shape
+    N, V = index["num_docs"], index["vocab_size"]
+    out = np.zeros((B, N), dtype=np.float32)
+    for q in range(B):
+        for j in range(T):
+            t = int(q_terms[q, j])
+            if t < 0 or t >= V:
+                continue
+            d, w = _postings(index, t)
+            prod = (np.float32(q_weights[q, j]) * w.astype(np.float32)).astype(np.float32)
+            np.add.at(out[q], d, prod)
+    return out
+
+
+def topk(scores: np.ndarray, k: int):
+    """Top-k of each row ordered by score descending, then doc id ascending:
+    the tie rule of this implementation (torch.topk's tie order is unspecified).
+    Returns (values [B, k] in the input dtype, ids [B, k] int64)."""
+    B, N = scores.shape
+    k = min(k, N)
+    ids = np.empty((B, k), dtype=np.int64)
+    for q in range(B):
+        order = np.lexsort((np.arange(N), -scores[q].astype(np.float64) if scores.dtype != np.uint32
+                            else -scores[q].astype(np.int64)))
+        ids[q] = order[:k]
+    vals = np.take_along_axis(scores, ids, axis=1)
+    return vals, ids
+
+
+def search(index: dict, q_terms: np.ndarray, q_weights: np.ndarray, k: int):
+    """Exact top-k of the scatter-add: float indexes -> (fp32 of the fp64 score,
+    ids); uint8 indexes -> (int32 uint32-sum, ids)."""
+    if index["scores"].dtype == np.uint8:
+        s = scores_u32(index, q_terms, q_weights)
+        v, i = topk(s, k)
+        return v.astype(np.int32), i
+    s = scores_f64(index, q_terms, q_weights)
+    v, i = topk(s, k)
+    return v.astype(np.float32), i
+
+
+def compacted_topk(scores: np.ndarray, tau, k: int, max_cand: int = 8192):
+    """src/fused_topk.py:71-103: top kk = min(k, L) of the entries >= tau[b] (all
+    entries when tau is None), descending, missing slots (-inf, 0); the result
+    does not depend on max_cand (overflow rows are redone in full, :96-102)."""
+    B, L = scores.shape
+    kk = min(k, L)
+    vals = np.full((B, kk), -np.inf, dtype=np.float32)
+    idx = np.zeros((B, kk), dtype=np.int64)
+    for b in range(B):
+        row = scores[b]
+        cand = np.arange(L) if tau is None else np.nonzero(row >= tau[b])[0]
+        order = cand[np.lexsort((cand, -row[cand].astype(np.float64)))][:kk]
+        vals[b, :order.size] = row[order]
+        idx[b, :order.size] = order
+    return vals, idx
+
+
+def cpu_sequential_score(doc_term_ids, doc_term_scores, query_term_ids_list, query_term_scores_list,
+                         num_docs, top_k=10):
+    """src/gpu_scoring.py:221-259 restated: dict inverted index, float32 per-query
+    accumulator, argpartition + argsort top-k.  Pure Python: small inputs only."""
+    inv = {}
+    for doc_id in range(num_docs):
+        for term_id, score in zip(doc_term_ids[doc_id], doc_term_scores[doc_id]):
+            inv.setdefault(term_id, []).append((doc_id, score))
+    all_s, all_i = [], []
+    for q_terms, q_scores in zip(query_term_ids_list, query_term_scores_list):
+        acc = np.zeros(num_docs, dtype=np.float32)
+        for term_id, q_score in zip(q_terms, q_scores):
+            for doc_id, d_score in inv.get(term_id, ()):
+                acc[doc_id] += q_score * d_score
+        top = np.argpartition(acc, -top_k)[-top_k:]
+        top = top[np.argsort(acc[top])[::-1]]
+        all_s.append(acc[top].tolist())
+        all_i.append(top.tolist())
+    return all_s, all_i
+
+
+# ------------------------------------------------------------------ host formatting
+
+
+def to_query_tensors(indptr, indices, data):
+    """Dense [nq, max_nnz] ids (-1 pad) and weights (0 pad): gpusparse_retrieval.py:118-132."""
+    nq = len(indptr) - 1
+    max_nnz = int(np.diff(indptr).max()) if nq else 1
+    ti = np.full((nq, max_nnz), -1, dtype=np.int32)
+    ts = np.zeros((nq, max_nnz), dtype=np.uint8 if np.asarray(data).dtype == np.uint8 else np.float32)
+    for i in range(nq):
+        s, e = indptr[i], indptr[i + 1]
+        ti[i, :e - s] = indices[s:e]
+        ts[i, :e - s] = data[s:e]
+    return ti, ts, max_nnz
+
+
+def rankings(q_ids, scores, ids, doc_ids, k):
+    """Per-query [(qid, score, docno)] keeping score > 0 (gpusparse_retrieval.py:168-171)."""
+    out = []
+    for r in range(scores.shape[0]):
+        out.append([(q_ids[r], float(scores[r, j]), doc_ids[ids[r, j]]) for j in range(min(k, scores.shape[1]))
+                    if scores[r, j] > 0])
+    return out
+
+
+# ------------------------------------------------------------------ C scorer
+
+
+_clib = None
+
+
+def clib():
+    """liboracle.so (oracle/oracle_score.c), built by oracle/Makefile."""
+    global _clib
+    if _clib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run make -C oracle")
+        L = C.CDLL(LIB_PATH)
+        P, I32, I64 = C.c_void_p, C.c_int32, C.c_int64
+        L.orc_search.restype = C.c_int
+        L.orc_search.argtypes = [P, P, C.c_int, P, P, I32, I64, P, P, I32, I32, I32, P, P, P, C.c_int]
+        L.orc_cpu_sequential.restype = C.c_int
+        L.orc_cpu_sequential.argtypes = [P, P, C.c_int, P, P, I32, I64, P, P, I32, I32, I32, P, P, C.c_int]
+        _clib = L
+    return _clib
+
+
+_WT = {np.dtype(np.float32): 0, np.dtype(np.float16): 1, np.dtype(np.uint8): 2}
+
+
+def _c_args(index, q_terms, q_weights):
+    doc = np.ascontiguousarray(index["doc_ids"], dtype=np.int32)
+    w = np.ascontiguousarray(index["scores"])
+    off = np.ascontiguousarray(index["offsets"], dtype=np.int64)
+    ln = np.ascontiguousarray(index["lengths"], dtype=np.int32)
+    qt = np.ascontiguousarray(q_terms, dtype=np.int32)
+    qw = np.ascontiguousarray(q_weights, dtype=np.uint8 if w.dtype == np.uint8 else np.float32)
+    return doc, w, off, ln, qt, qw
+
+
+def c_search(index: dict, q_terms, q_weights, k: int, threads: int = 0):
+    """C version of :func:`search` (same definition; OpenMP over queries).
+    Returns (scores f32 or int32 [B, k], fp64 scores [B, k], ids int64 [B, k])."""
+    doc, w, off, ln, qt, qw = _c_args(index, q_terms, q_weights)
+    B, T = qt.shape
+    k = min(k, index["num_docs"])
+    s64 = np.empty((B, k), dtype=np.float64)
+    ids = np.empty((B, k), dtype=np.int64)
+    rc = clib().orc_search(doc.ctypes.data, w.ctypes.data, _WT[w.dtype], off.ctypes.data, ln.ctypes.data,
+                           int(index["vocab_size"]), int(index["num_docs"]), qt.ctypes.data, qw.ctypes.data, B, T,
+                           k, s64.ctypes.data, ids.ctypes.data, None, int(threads))
+    if rc:
+        raise RuntimeError(f"orc_search failed ({rc})")
+    vals = s64.astype(np.int32) if w.dtype == np.uint8 else s64.astype(np.float32)
+    return vals, s64, ids
+
+
+def c_cpu_sequential(index: dict, q_terms, q_weights, k: int, threads: int = 1):
+    """The reference CPU path (float32 accumulator per query, cpu_sequential_score
+    src/gpu_scoring.py:221-259) in C; the timed CPU baseline."""
+    doc, w, off, ln, qt, qw = _c_args(index, q_terms, q_weights)
+    B, T = qt.shape
+    k = min(k, index["num_docs"])
+    vals = np.empty((B, k), dtype=np.float32)
+    ids = np.empty((B, k), dtype=np.int64)
+    rc = clib().orc_cpu_sequential(doc.ctypes.data, w.ctypes.data, _WT[w.dtype], off.ctypes.data, ln.ctypes.data,
+                                   int(index["vocab_size"]), int(index["num_docs"]), qt.ctypes.data,
+                                   qw.ctypes.data, B, T, k, vals.ctypes.data, ids.ctypes.data, int(threads))
+    if rc:
+        raise RuntimeError(f"orc_cpu_sequential failed ({rc})")
+    return vals, ids

@@ -1,0 +1,307 @@
+"""GPU parity: the HIP path against the CPU oracle on the same seeded inputs.
+
+Bar: index arrays, chunk bounds and uint8 results bit-exact; float results with
+identical ids and scores equal to the oracle's fp64 scatter-add rounded to fp32
+(bit-exact, which is stricter than the |diff| <= 1e-5 tolerance of the task)."""
+import numpy as np
+import pytest
+import torch
+
+import gpusparse as gs
+from gpusparse import synth
+from gpusparse.index import CSR, GPUInvertedIndex
+from helpers import random_csr, random_queries
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+FIELDS = ("doc_ids", "scores", "offsets", "lengths", "padded_lengths", "max_scores")
+
+
+def oracle_index(csr: CSR, vocab=None):
+    return O.build_index(csr.indptr, csr.indices, csr.data, csr.shape[0], csr.shape[1] if vocab is None else vocab)
+
+
+def assert_index_equal(ix, ref):
+    for f in FIELDS:
+        got = getattr(ix, f).cpu().numpy()
+        want = ref[f]
+        assert got.dtype == want.dtype, f
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), f
+    assert ix.num_docs == ref["num_docs"] and ix.vocab_size == ref["vocab_size"]
+
+
+def assert_search_equal(ix, ref, ti, tw, k, **opts):
+    s, i = gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), k, **opts)
+    vs, s64, vi = O.c_search(ref, ti, tw, k, threads=8)
+    s, i = s.cpu().numpy(), i.cpu().numpy()
+    assert np.array_equal(i, vi)
+    assert s.dtype == vs.dtype and np.array_equal(s, vs)
+    if s.dtype == np.float32:
+        assert np.max(np.abs(s.astype(np.float64) - s64), initial=0.0) <= 1e-5
+    return s, i
+
+
+# ------------------------------------------------------------------ index build
+
+
+@pytest.mark.parametrize("seed,n_docs,vocab,dtype,dup", [
+    (0, 500, 300, np.float32, 0.0), (1, 2000, 9, np.float32, 0.2), (2, 300, 1, np.float32, 0.0),
+    (3, 1000, 700, np.float16, 0.05), (4, 700, 250, np.uint8, 0.0), (5, 1, 3, np.float32, 0.0),
+    (6, 400, 70000, np.float32, 0.0)])
+def test_build_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
+    print(f"build case seed={seed} n_docs={n_docs} vocab={vocab} dtype={dtype.__name__}", flush=True)
+    csr = random_csr(np.random.default_rng(seed), n_docs, vocab, dtype=dtype, dup_rate=dup)
+    ix = gs.build_index(csr, device)
+    assert_index_equal(ix, oracle_index(csr))
+
+
+def test_build_generated_c1(device):
+    docs, _ = synth.generate("C1")
+    ix = gs.build_index(docs, device)
+    assert_index_equal(ix, oracle_index(docs))
+
+
+def test_build_harness_vocab_and_range_check(device):
+    csr = random_csr(np.random.default_rng(8), 300, 500)
+    ix = gs.build_gpu_index_from_csr(csr, device)
+    assert ix.vocab_size == 30522
+    assert_index_equal(ix, oracle_index(csr, vocab=30522))
+    big = CSR(csr.indptr, csr.indices + 30100, csr.data, (300, 31000))
+    with pytest.raises(IndexError):
+        gs.build_gpu_index_from_csr(big, device)
+
+
+def test_build_from_lists_and_torch_sparse(device):
+    rng = np.random.default_rng(9)
+    csr = random_csr(rng, 200, 60, dup_rate=0.1)
+    terms = [csr.indices[csr.indptr[d]:csr.indptr[d + 1]].tolist() for d in range(200)]
+    ws = [csr.data[csr.indptr[d]:csr.indptr[d + 1]].tolist() for d in range(200)]
+    ix = gs.build_gpu_inverted_index(terms, ws, 60, device)
+    assert_index_equal(ix, oracle_index(csr))
+    # torch sparse COO: duplicates coalesce (summed) and zeros drop, as the dense
+    # round trip of gpu_inverted_index.py:121-132 does
+    canon = random_csr(rng, 150, 40, sort_rows=True)
+    rows = np.repeat(np.arange(150), np.diff(canon.indptr))
+    coo = torch.sparse_coo_tensor(np.stack([rows, canon.indices]), canon.data, (150, 40))
+    ix2 = gs.build_gpu_inverted_index_from_sparse(coo, device)
+    assert_index_equal(ix2, oracle_index(canon))
+    ix3 = gs.build_gpu_inverted_index_from_sparse(coo.to_dense(), device)
+    assert_index_equal(ix3, oracle_index(canon))
+
+
+def test_chunk_bounds_and_ascending_check(device):
+    csr = random_csr(np.random.default_rng(10), 3000, 120, dup_rate=0.02)
+    ix = gs.build_index(csr, device)
+    ref = oracle_index(csr)
+    for chunk in (1, 100, 1024, 2999, 5000):
+        b = gs.build_chunk_boundaries(ix, chunk).cpu().numpy()
+        assert np.array_equal(b, O.chunk_bounds(ref["doc_ids"], ref["offsets"], ref["lengths"], 120, 3000, chunk))
+    # a plug-in style index (built through __new__, no cached checks) with one list
+    # made non-ascending must be rejected with the reference's message
+    bad = GPUInvertedIndex.__new__(GPUInvertedIndex)
+    doc = ix.doc_ids.clone()
+    t = int(torch.argmax(ix.lengths).item())
+    o = int(ix.offsets[t].item())
+    doc[o], doc[o + 1] = ix.doc_ids[o + 1], ix.doc_ids[o]
+    bad.doc_ids, bad.scores, bad.offsets, bad.lengths = doc, ix.scores, ix.offsets, ix.lengths
+    bad.num_docs, bad.vocab_size, bad.device = ix.num_docs, ix.vocab_size, ix.device
+    n_nonempty = int((ref["lengths"] > 0).sum())
+    with pytest.raises(ValueError, match=f"1 of {n_nonempty} posting lists are not ascending"):
+        gs.build_chunk_boundaries(bad, 1000)
+    with pytest.raises(ValueError):
+        gs.search(bad, (torch.zeros((1, 1), dtype=torch.int32), torch.ones((1, 1))), 5)
+
+
+# ------------------------------------------------------------------ search
+
+
+@pytest.fixture(scope="module")
+def c1(device):
+    docs, queries = synth.generate("C1")
+    ix = gs.build_index(docs, device)
+    ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
+    return ix, oracle_index(docs), ti, tw
+
+
+@pytest.mark.parametrize("path", ["fused", "dense"])
+@pytest.mark.parametrize("k", [10, 1000])
+def test_search_c1(c1, path, k):
+    ix, ref, ti, tw = c1
+    print(f"search C1 path={path} k={k}", flush=True)
+    assert_search_equal(ix, ref, ti, tw, k, path=path)
+
+
+@pytest.mark.parametrize("tile_log2", [8, 10, 13])
+def test_search_c1_tile_sizes(c1, tile_log2):
+    ix, ref, ti, tw = c1
+    print(f"search C1 tile_log2={tile_log2}", flush=True)
+    assert_search_equal(ix, ref, ti[:64], tw[:64], 100, path="fused", tile_log2=tile_log2)
+
+
+@pytest.mark.parametrize("unroll,waves", [(1, 0), (2, 4), (8, 2)])
+def test_search_c1_launch_shapes(c1, unroll, waves):
+    ix, ref, ti, tw = c1
+    assert_search_equal(ix, ref, ti[:32], tw[:32], 50, path="fused", unroll=unroll, waves=waves)
+
+
+def test_search_dense_fallback_rows(c1):
+    """A candidate cap far below what the rows emit sends them to the dense path;
+    the answer must not change (the reference's overflow rule, fused_topk.py:96-102)."""
+    ix, ref, ti, tw = c1
+    timing = {}
+    s, i = gs.search(ix, (torch.from_numpy(ti[:40]), torch.from_numpy(tw[:40])), 200, path="fused",
+                     cand_cap=400, timing=timing)
+    assert timing["dense_rows"] > 0
+    vs, _, vi = O.c_search(ref, ti[:40], tw[:40], 200, threads=8)
+    assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+
+
+def test_search_small_sample_and_single_tile(c1):
+    ix, ref, ti, tw = c1
+    assert_search_equal(ix, ref, ti[:16], tw[:16], 30, path="fused", sample_tiles=1)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.uint8])
+def test_search_edge_cases(device, dtype):
+    """Empty queries, invalid term ids, duplicate list entries, k = N (zero-score
+    documents fill the list by ascending id) and k > N (clamped)."""
+    rng = np.random.default_rng(21)
+    csr = random_csr(rng, 700, 50, dtype=dtype, dup_rate=0.05, empty_rate=0.3, max_len=4)
+    ix = gs.build_index(csr, device)
+    ref = oracle_index(csr)
+    qdt = np.uint8 if dtype == np.uint8 else np.float32
+    ti, tw = random_queries(rng, 12, 50, dtype=qdt, invalid_rate=0.3, max_len=5)
+    ti[0, :] = -1
+    for k in (1, 17, 700):
+        for path in ("fused", "dense"):
+            print(f"edge dtype={dtype.__name__} k={k} path={path}", flush=True)
+            assert_search_equal(ix, ref, ti, tw, k, path=path, tile_log2=8)
+    s, i = gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), 10_000, tile_log2=8)
+    assert s.shape == (12, 700)
+
+
+def test_search_f16_config_reduced(device):
+    cfg = synth.scaled(synth.CONFIGS["C3"], n_docs=300_000, n_queries=64)
+    docs, queries = synth.generate(cfg)
+    ix = gs.build_index(docs, device)
+    assert ix.scores.dtype == torch.float16
+    ref = oracle_index(docs)
+    ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
+    for k in (10, 1000):
+        print(f"C3 reduced k={k}", flush=True)
+        assert_search_equal(ix, ref, ti, tw, k, path="fused")
+
+
+def test_search_u8_config_reduced(device):
+    cfg = synth.scaled(synth.CONFIGS["C5"], n_docs=300_000, n_queries=64)
+    docs, queries = synth.generate(cfg)
+    ix = gs.build_index(docs, device)
+    assert ix.scores.dtype == torch.uint8
+    ref = oracle_index(docs)
+    assert_index_equal(ix, ref)
+    ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
+    assert tw.dtype == np.uint8
+    assert_search_equal(ix, ref, ti, tw, 1000, path="fused")
+
+
+@pytest.mark.parametrize("tile_log2", [8, 10, 12])
+def test_search_head_heavy_reduced(device, tile_log2):
+    cfg = synth.scaled(synth.CONFIGS["C4"], n_docs=200_000, n_queries=32)
+    docs, queries = synth.generate(cfg)
+    ix = gs.build_index(docs, device)
+    ref = oracle_index(docs)
+    ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
+    print(f"C4 reduced tile_log2={tile_log2} T={ti.shape[1]}", flush=True)
+    assert_search_equal(ix, ref, ti, tw, 1000, path="fused", tile_log2=tile_log2)
+
+
+# ------------------------------------------------------------------ selection and scatter
+
+
+def test_compacted_topk_matches_oracle(device):
+    rng = np.random.default_rng(31)
+    s = rng.normal(size=(9, 5000)).astype(np.float32)
+    s[3, :] = 1.0                               # one row of ties
+    tau = np.array([0.5, 2.0, -np.inf, 1.0, 3.5, 0.0, 1.2, 9.0, -1.0], np.float32)
+    st = torch.from_numpy(s).to(device)
+    for k, max_cand in ((10, 8192), (300, 8192), (300, 300), (1000, 1000)):
+        v, i = gs.compacted_topk(st, torch.from_numpy(tau).to(device), k, max_cand=max_cand)
+        ov, oi = O.compacted_topk(s, tau, k)
+        assert np.array_equal(i.cpu().numpy(), oi) and np.array_equal(v.cpu().numpy(), ov)
+    v, i = gs.topk_rows(st[:, :4000], 77)
+    ov, oi = O.compacted_topk(s[:, :4000], None, 77)
+    assert np.array_equal(i.cpu().numpy(), oi) and np.array_equal(v.cpu().numpy(), ov)
+    # a strided [B, chunk] view, as the reference's final short chunk (triton_kernel_chunked.py:147-151)
+    v, i = gs.compacted_topk(st[:, :1234], torch.from_numpy(tau).to(device), 50)
+    ov, oi = O.compacted_topk(s[:, :1234], tau, 50)
+    assert np.array_equal(i.cpu().numpy(), oi) and np.array_equal(v.cpu().numpy(), ov)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.uint8])
+def test_scatter_add_matches_oracle(device, dtype):
+    rng = np.random.default_rng(32)
+    csr = random_csr(rng, 4000, 200, dtype=dtype)
+    ix = gs.build_index(csr, device)
+    ref = oracle_index(csr)
+    qdt = np.uint8 if dtype == np.uint8 else np.float32
+    ti, tw = random_queries(rng, 10, 200, dtype=qdt, invalid_rate=0.1)
+    odt = torch.int32 if dtype == np.uint8 else torch.float32
+    out = torch.zeros((10, 4000), dtype=odt, device=device)
+    gs.scatter_add(ix, torch.from_numpy(ti), torch.from_numpy(tw), out, block_pl=512)
+    if dtype == np.uint8:
+        assert np.array_equal(out.cpu().numpy().astype(np.uint32), O.scores_u32(ref, ti, tw))
+    else:
+        np.testing.assert_allclose(out.cpu().numpy(), O.scores_f64(ref, ti, tw), rtol=2e-6, atol=1e-6)
+    # one chunk through per-term bounds (the chunked kernel)
+    b = gs.build_chunk_boundaries(ix, 1500)
+    out2 = torch.zeros((10, 1500), dtype=odt, device=device)
+    gs.scatter_add(ix, torch.from_numpy(ti), torch.from_numpy(tw), out2, lo=b[1], hi=b[2], chunk_start=1500,
+                   chunk_len=1500)
+    assert np.array_equal(out2.cpu().numpy(), out.cpu().numpy()[:, 1500:3000]) or dtype != np.uint8
+    if dtype != np.uint8:
+        np.testing.assert_allclose(out2.cpu().numpy(), out.cpu().numpy()[:, 1500:3000], rtol=2e-6, atol=1e-6)
+
+
+def test_atomic_path_agrees(c1):
+    ix, ref, ti, tw = c1
+    s, i = gs.atomic_fused_score(ix, torch.from_numpy(ti[:32]), torch.from_numpy(tw[:32]), 10)
+    vs, s64, vi = O.c_search(ref, ti[:32], tw[:32], 10, threads=8)
+    assert np.max(np.abs(s.cpu().numpy() - s64)) <= 1e-5
+
+
+# ------------------------------------------------------------------ drop-in surface
+
+
+def test_reference_entry_points(c1):
+    ix, ref, ti, tw = c1
+    qt, qw = torch.from_numpy(ti[:50]).to(ix.device), torch.from_numpy(tw[:50]).to(ix.device)
+    vs, _, vi = O.c_search(ref, ti[:50], tw[:50], 100, threads=8)
+    for fn in (lambda: gs.triton_fused_score(ix, qt, qw, top_k=100),
+               lambda: gs.triton_fused_score(ix, qt, qw, top_k=100, block_pl=512),
+               lambda: gs.triton_chunked_score(ix, qt, qw, top_k=100, doc_chunk=30000),
+               lambda: gs.triton_chunked_score_fused(ix, qt, qw, top_k=100, doc_chunk=30000,
+                                                     chunk_bounds=gs.build_chunk_boundaries(ix, 30000))):
+        s, i = fn()
+        assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+    with pytest.raises(AssertionError, match="power of 2"):
+        gs.triton_fused_score(ix, qt, qw, block_pl=100)
+
+
+def test_retrieve_and_run_engine(device, tmp_path):
+    rng = np.random.default_rng(41)
+    csr = random_csr(rng, 3000, 400, max_len=20, sort_rows=True)
+    ti, tw = random_queries(rng, 30, 400, max_len=8)
+    docs = [(f"D{d}", csr.indices[csr.indptr[d]:csr.indptr[d + 1]].tolist(),
+             csr.data[csr.indptr[d]:csr.indptr[d + 1]].tolist()) for d in range(3000)]
+    qs = [(f"Q{q}", [int(t) for t in ti[q] if t >= 0], [float(w) for t, w in zip(ti[q], tw[q]) if t >= 0])
+          for q in range(30)]
+    res = gs.run_engine(docs, qs, str(tmp_path), 20, doc_chunk=1000, batch_size=7)
+    dim = gs.determine_dimension(docs, qs)
+    ref = oracle_index(CSR(csr.indptr, csr.indices, csr.data, (3000, dim)))
+    q_ids, qcsr = gs.to_csr(qs, dim)
+    oti, otw, _ = O.to_query_tensors(qcsr.indptr, qcsr.indices, qcsr.data)
+    vs, _, vi = O.c_search(ref, oti, otw, 20, threads=4)
+    want = O.rankings(q_ids, vs, vi, [d[0] for d in docs], 20)
+    assert res == want
+    assert (tmp_path / "run.txt.gz").exists()

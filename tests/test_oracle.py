@@ -1,0 +1,219 @@
+"""Pins the CPU oracle (oracle/oracle.py, oracle/oracle_score.c) against
+independent computations.  The reference holds no golden vectors for this path,
+so each oracle function is checked against a different algorithm: brute-force
+Python lists, dense matrix products, full sorts and closed forms."""
+import numpy as np
+import pytest
+
+from helpers import dense_docs, dense_queries, random_csr, random_queries
+from oracle import oracle as O
+
+
+def brute_index(csr, vocab):
+    """Dict-of-lists builder in the manner of src/gpu_inverted_index.py:59-99."""
+    lists = [[] for _ in range(vocab)]
+    for d in range(csr.shape[0]):
+        for p in range(csr.indptr[d], csr.indptr[d + 1]):
+            lists[int(csr.indices[p])].append((d, csr.data[p]))
+    docs, scores, offsets, lengths, padded, maxs = [], [], [], [], [], []
+    pos = 0
+    for t in range(vocab):
+        pl = sorted(lists[t], key=lambda x: x[0])  # Python's sort is stable
+        n = len(pl)
+        pn = (n + 31) // 32 * 32
+        offsets.append(pos)
+        lengths.append(n)
+        padded.append(pn)
+        maxs.append(max(float(s) for _, s in pl) if pl else 0.0)
+        docs.extend([d for d, _ in pl] + [-1] * (pn - n))
+        scores.extend([s for _, s in pl] + [0] * (pn - n))
+        pos += pn
+    return docs, scores, offsets, lengths, padded, maxs
+
+
+@pytest.mark.parametrize("seed,n_docs,vocab,dtype,dup", [
+    (0, 50, 40, np.float32, 0.0), (1, 200, 7, np.float32, 0.3), (2, 64, 1, np.float32, 0.0),
+    (3, 100, 300, np.float16, 0.1), (4, 80, 60, np.uint8, 0.0), (5, 0, 10, np.float32, 0.0)])
+def test_build_index_matches_brute_force(seed, n_docs, vocab, dtype, dup):
+    rng = np.random.default_rng(seed)
+    csr = random_csr(rng, n_docs, vocab, dtype=dtype, dup_rate=dup)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, n_docs, vocab)
+    docs, scores, offsets, lengths, padded, maxs = brute_index(csr, vocab)
+    assert ix["doc_ids"].tolist() == docs
+    assert ix["scores"].astype(np.float64).tolist() == [float(s) for s in scores]
+    assert ix["scores"].dtype == csr.data.dtype
+    assert ix["offsets"].tolist() == offsets
+    assert ix["lengths"].tolist() == lengths
+    assert ix["padded_lengths"].tolist() == padded
+    assert np.array_equal(ix["max_scores"], np.asarray(maxs, np.float32))
+
+
+def test_build_index_invariants():
+    rng = np.random.default_rng(7)
+    csr = random_csr(rng, 500, 90, dup_rate=0.05)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 500, 90)
+    assert int(ix["lengths"].sum()) == csr.nnz
+    assert np.all(ix["offsets"] % 32 == 0) and np.all(ix["padded_lengths"] % 32 == 0)
+    pairs = []
+    for t in range(90):
+        o, L, P = ix["offsets"][t], ix["lengths"][t], ix["padded_lengths"][t]
+        seg = ix["doc_ids"][o:o + L]
+        assert np.all(np.diff(seg) >= 0)
+        assert np.all(ix["doc_ids"][o + L:o + P] == -1) and np.all(ix["scores"][o + L:o + P] == 0)
+        pairs.extend((int(d), t) for d in seg)
+    rows = np.repeat(np.arange(500), np.diff(csr.indptr))
+    assert sorted(pairs) == sorted(zip(rows.tolist(), csr.indices.tolist()))
+
+
+def test_build_index_rejects_out_of_range_terms():
+    csr = random_csr(np.random.default_rng(0), 10, 5)
+    with pytest.raises(IndexError):
+        O.build_index(csr.indptr, csr.indices, csr.data, 10, int(csr.indices.max()))
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 17, 64, 1000])
+def test_chunk_bounds_match_linear_scan(chunk):
+    rng = np.random.default_rng(chunk)
+    csr = random_csr(rng, 150, 30, dup_rate=0.1)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 150, 30)
+    b = O.chunk_bounds(ix["doc_ids"], ix["offsets"], ix["lengths"], 30, 150, chunk)
+    n_chunks = (150 + chunk - 1) // chunk
+    assert b.shape == (n_chunks + 1, 30)
+    for t in range(30):
+        o, L = int(ix["offsets"][t]), int(ix["lengths"][t])
+        seg = ix["doc_ids"][o:o + L].tolist()
+        for c in range(n_chunks + 1):
+            edge = c * chunk if c < n_chunks else 150
+            first = next((i for i, d in enumerate(seg) if d >= edge), L)
+            assert b[c, t] == o + first
+        # the chunk sub-ranges partition the list
+        assert b[0, t] == o and b[-1, t] == o + L
+        assert np.all(np.diff(b[:, t]) >= 0)
+
+
+def test_chunk_bounds_reject_non_ascending():
+    csr = random_csr(np.random.default_rng(3), 100, 8, empty_rate=0.0)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 100, 8)
+    t = int(np.argmax(ix["lengths"]))
+    o = ix["offsets"][t]
+    ix["doc_ids"][o], ix["doc_ids"][o + 1] = ix["doc_ids"][o + 1], ix["doc_ids"][o]
+    with pytest.raises(ValueError, match="1 of .* posting lists are not ascending"):
+        O.chunk_bounds(ix["doc_ids"], ix["offsets"], ix["lengths"], 8, 100, 16)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_scores_f64_equal_dense_product(dtype):
+    rng = np.random.default_rng(11)
+    csr = random_csr(rng, 120, 50, dtype=dtype, dup_rate=0.1)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 120, 50)
+    ti, tw = random_queries(rng, 9, 50, invalid_rate=0.2)
+    got = O.scores_f64(ix, ti, tw)
+    want = dense_queries(ti, tw, 50) @ dense_docs(csr).T
+    np.testing.assert_allclose(got, want, rtol=1e-13, atol=1e-13)
+
+
+def test_scores_u32_equal_integer_product():
+    rng = np.random.default_rng(12)
+    csr = random_csr(rng, 120, 50, dtype=np.uint8, dup_rate=0.1)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 120, 50)
+    ti, tw = random_queries(rng, 9, 50, dtype=np.uint8, invalid_rate=0.2)
+    got = O.scores_u32(ix, ti, tw)
+    want = dense_queries(ti, tw, 50, dtype=np.int64) @ dense_docs(csr, dtype=np.int64).T
+    assert np.array_equal(got.astype(np.int64), want)
+
+
+def test_scores_f32_sequential_is_the_reference_cpu_accumulation():
+    """Scalar float32 loop of src/gpu_scoring.py:246-251 (product rounded to fp32,
+    added to the fp32 accumulator) on a tiny input."""
+    rng = np.random.default_rng(13)
+    csr = random_csr(rng, 40, 20)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 40, 20)
+    ti, tw = random_queries(rng, 5, 20)
+    got = O.scores_f32_sequential(ix, ti, tw)
+    for q in range(5):
+        acc = [np.float32(0)] * 40
+        for t, wq in zip(ti[q], tw[q]):
+            if t < 0:
+                continue
+            for d in range(40):
+                for p in range(csr.indptr[d], csr.indptr[d + 1]):
+                    if csr.indices[p] == t:
+                        acc[d] = np.float32(acc[d] + np.float32(float(wq) * float(csr.data[p])))
+        assert np.array_equal(got[q], np.asarray(acc, np.float32))
+
+
+def test_topk_tie_rule_matches_full_sort():
+    rng = np.random.default_rng(14)
+    s = rng.integers(0, 6, size=(7, 50)).astype(np.float64)  # many ties
+    v, i = O.topk(s, 13)
+    for q in range(7):
+        want = sorted(range(50), key=lambda d: (-s[q, d], d))[:13]
+        assert i[q].tolist() == want
+        assert v[q].tolist() == [s[q, d] for d in want]
+    vu, iu = O.topk(s.astype(np.uint32), 50)
+    assert np.array_equal(iu, np.stack([sorted(range(50), key=lambda d: (-s[q, d], d)) for q in range(7)]))
+
+
+def test_search_matches_brute_force_including_zero_fill():
+    rng = np.random.default_rng(15)
+    csr = random_csr(rng, 60, 30, empty_rate=0.3)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 60, 30)
+    ti, tw = random_queries(rng, 6, 30, max_len=3)
+    v, i = O.search(ix, ti, tw, 60)   # k = N: zero-score docs fill by ascending id
+    S = dense_queries(ti, tw, 30) @ dense_docs(csr).T
+    for q in range(6):
+        want = sorted(range(60), key=lambda d: (-S[q, d], d))
+        assert i[q].tolist() == want
+        np.testing.assert_allclose(v[q], S[q, want].astype(np.float32), rtol=1e-6)
+
+
+def test_compacted_topk_semantics():
+    rng = np.random.default_rng(16)
+    s = rng.normal(size=(5, 40)).astype(np.float32)
+    tau = np.array([0.0, 1.5, -np.inf, 3.0, 0.5], np.float32)
+    v, i = O.compacted_topk(s, tau, 12)
+    for b in range(5):
+        cand = [c for c in range(40) if s[b, c] >= tau[b]]
+        want = sorted(cand, key=lambda c: (-s[b, c], c))[:12]
+        assert i[b, :len(want)].tolist() == want
+        assert np.all(np.isneginf(v[b, len(want):])) and np.all(i[b, len(want):] == 0)
+    v2, i2 = O.compacted_topk(s, None, 40)
+    assert np.array_equal(i2, np.stack([sorted(range(40), key=lambda c: (-s[b, c], c)) for b in range(5)]))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.uint8])
+def test_c_oracle_equals_numpy_oracle(dtype):
+    rng = np.random.default_rng(17)
+    csr = random_csr(rng, 300, 80, dtype=dtype, dup_rate=0.05)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 300, 80)
+    qdt = np.uint8 if dtype == np.uint8 else np.float32
+    ti, tw = random_queries(rng, 11, 80, dtype=qdt, invalid_rate=0.1)
+    for k in (1, 7, 300):
+        v, s64, i = O.c_search(ix, ti, tw, k, threads=2)
+        vn, inn = O.search(ix, ti, tw, k)
+        assert np.array_equal(i, inn)
+        assert np.array_equal(v, vn)          # identical summation order -> identical bits
+
+
+def test_c_cpu_sequential_equals_reference_cpu_path():
+    rng = np.random.default_rng(18)
+    n_docs, vocab = 80, 25
+    doc_terms = [list(rng.choice(vocab, size=int(rng.integers(1, 8)), replace=False)) for _ in range(n_docs)]
+    doc_w = [list(np.float32(rng.lognormal(-0.5, 0.8, size=len(t)))) for t in doc_terms]
+    qt = [list(rng.choice(vocab, size=5, replace=False)) for _ in range(4)]
+    qw = [list(np.float32(rng.lognormal(-0.5, 0.8, size=5))) for _ in range(4)]
+    ref_s, ref_i = O.cpu_sequential_score(doc_terms, doc_w, qt, qw, n_docs, top_k=6)
+    indptr = np.cumsum([0] + [len(t) for t in doc_terms])
+    ix = O.build_index(indptr, np.concatenate(doc_terms), np.concatenate(doc_w).astype(np.float32), n_docs, vocab)
+    v, i = O.c_cpu_sequential(ix, np.asarray(qt, np.int32), np.asarray(qw, np.float32), 6)
+    for q in range(4):
+        assert np.array_equal(np.asarray(ref_s[q], np.float32), v[q])
+        assert set(ref_i[q]) == set(i[q].tolist()) or len(set(ref_s[q])) < 6
+
+
+def test_to_query_tensors_oracle():
+    indptr = np.array([0, 3, 3, 5]); indices = np.array([4, 1, 9, 2, 2]); data = np.array([.5, .25, 1., 2., 3.])
+    ti, ts, T = O.to_query_tensors(indptr, indices, data)
+    assert T == 3
+    assert ti.tolist() == [[4, 1, 9], [-1, -1, -1], [2, 2, -1]]
+    assert ts.tolist() == [[.5, .25, 1.], [0, 0, 0], [2., 3., 0]]
