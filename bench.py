@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--batch", type=int, default=512)
     ap.add_argument("--k", type=int, default=1000)
     ap.add_argument("--tile-log2", type=int, default=12)
-    ap.add_argument("--unroll", type=int, default=4)
+    ap.add_argument("--unroll", type=int, default=0, help="postings per lane per chunk (0: library default)")
     ap.add_argument("--waves", type=int, default=0)
     ap.add_argument("--cpu-queries-1", type=int, default=16, help="queries timed on one core")
     ap.add_argument("--cpu-queries-all", type=int, default=64, help="queries timed on all cores")
@@ -54,7 +54,38 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-queries", type=int, default=4)
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run a plain device-to-device copy of this many bytes (PMC counter calibration)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_k_score_union_C3.json")
+
+
+def measured_traffic(cfg_name, n_docs, tile_log2):
+    """HBM bytes per launch of the fused scorer from the committed rocprofv3 PMC
+    measurement (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size),
+    when it was taken on this workload; None otherwise."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("config") != cfg_name or t.get("n_docs") != n_docs or t.get("tile_log2") != tile_log2:
+        return None
+    return t.get("traffic_bytes_per_launch")
+
+
+def copy_only(nbytes):
+    """A plain copy kernel of known size: the calibration of FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    n = nbytes // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n * 4, "launches": 3}), flush=True)
 
 
 def cpu_rows(index_h, ti, tw, k, n1, n_all, cap):
@@ -93,6 +124,9 @@ def cpu_rows(index_h, ti, tw, k, n1, n_all, cap):
 
 def main():
     a = parse()
+    if a.copy_bytes:
+        copy_only(a.copy_bytes)
+        return
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
               "see DESIGN.md for how the index would shard.", file=sys.stderr)
@@ -177,8 +211,9 @@ def main():
         avg_ms = float(np.mean(kern_ms))
         achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                "kernel": "k_score_tiles<emit> (fused LDS-tile scoring + threshold emission)",
+                "frac": round(achieved / PEAK_HBM_GBS, 4),
+                "traffic": measured_traffic(cfg.name, int(index.num_docs), a.tile_log2),
+                "kernel": "k_score_union (fused group-tile LDS scoring + threshold emission)",
                 "kernel_ms_avg": round(avg_ms, 3), "kernel_ms_min": round(float(np.min(kern_ms)), 3),
                 "scored_postings_per_launch": post_launch, "bytes_per_posting": per_post,
                 "algorithmic_bytes_per_launch": bytes_launch,

@@ -55,8 +55,7 @@ def triton_chunked_score(index, query_term_ids, query_term_scores, top_k=10, doc
     """Drop-in for triton_chunked_score (src/triton_kernel_chunked.py:125-170)."""
     _check_pow2(block_pl)
     _check_bounds(index, chunk_bounds, doc_chunk)
-    unroll = max(1, min(8, block_pl // 64))
-    return search(index, (query_term_ids, query_term_scores), top_k, unroll=unroll, path="fused")
+    return search(index, (query_term_ids, query_term_scores), top_k, path="fused")
 
 
 def triton_chunked_score_fused(index, query_term_ids, query_term_scores, top_k=10, doc_chunk=131072, block_pl=128,
@@ -64,5 +63,4 @@ def triton_chunked_score_fused(index, query_term_ids, query_term_scores, top_k=1
     """Drop-in for triton_chunked_score_fused (src/fused_topk.py:106-160)."""
     _check_pow2(block_pl)
     _check_bounds(index, chunk_bounds, doc_chunk)
-    unroll = max(1, min(8, block_pl // 64))
-    return search(index, (query_term_ids, query_term_scores), top_k, unroll=unroll, path="fused")
+    return search(index, (query_term_ids, query_term_scores), top_k, path="fused")

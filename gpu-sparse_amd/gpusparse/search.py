@@ -81,7 +81,7 @@ def _dense_rows(index, gidx, qt, qw, k, rows, out_s, out_i, dense_budget):
 
 
 def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG2, path: str = "auto",
-           sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 4, waves: int = 0,
+           sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 0, waves: int = 0,
            dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None):
     """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
 
@@ -152,11 +152,10 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG
 def triton_fused_score(index, query_term_ids: torch.Tensor, query_term_scores: torch.Tensor, top_k: int = 10,
                        block_pl: int = 128):
     """Drop-in for triton_fused_score (src/triton_kernel.py:159-200): exact top-k,
-    (scores [B, k] desc, ids [B, k] int64).  block_pl sets the posting loads in
-    flight per lane (block_pl / 64, clamped to 1..8)."""
+    (scores [B, k] desc, ids [B, k] int64).  block_pl is validated as the
+    reference does; the LDS-tile scorer uses its own tuned posting chunk."""
     _check_pow2(block_pl)
-    unroll = max(1, min(8, block_pl // 64))
-    return search(index, (query_term_ids, query_term_scores), top_k, unroll=unroll)
+    return search(index, (query_term_ids, query_term_scores), top_k)
 
 
 def compacted_topk(scores: torch.Tensor, tau: torch.Tensor, k: int, max_cand: int = 8192, block: int = 1024):

@@ -66,8 +66,8 @@ typedef struct gs_index {
 typedef struct gs_search_opts {
     int32_t sample_tiles;  /* doc tiles scored densely to seed the k-th-score threshold (default 16) */
     int32_t cand_cap;      /* candidates kept per query before the dense fallback (default 65536) */
-    int32_t unroll;        /* posting loads in flight per lane: block_pl / 64, 1..8 (default 4) */
-    int32_t waves;         /* queries per tile workgroup: 4 or 8 (default: 8 if the tile fits) */
+    int32_t unroll;        /* postings per lane per chunk of the fused scorer: 1, 2, 4, 8 or 16 (default 8) */
+    int32_t waves;         /* waves per workgroup of the dense sample scorer: 1, 2 or 4 (default: fill 128 KiB) */
     void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
     void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
 } gs_search_opts;

@@ -139,7 +139,7 @@ def test_search_c1_tile_sizes(c1, tile_log2):
     assert_search_equal(ix, ref, ti[:64], tw[:64], 100, path="fused", tile_log2=tile_log2)
 
 
-@pytest.mark.parametrize("unroll,waves", [(1, 0), (2, 4), (8, 2)])
+@pytest.mark.parametrize("unroll,waves", [(1, 0), (2, 4), (16, 2)])
 def test_search_c1_launch_shapes(c1, unroll, waves):
     ix, ref, ti, tw = c1
     assert_search_equal(ix, ref, ti[:32], tw[:32], 50, path="fused", unroll=unroll, waves=waves)
