@@ -64,8 +64,8 @@ __global__ void k_fill(T *p, int64_t n, T v) {
 // Fixed-point scale and selection margin of each query.  A doc's score is a sum
 // of at most n = sum_j (1 + dup[t_j]) products, and sum |products| <= M =
 // sum_j |q_j| * max|w(t_j)| * (1 + dup[t_j]).  With scale S = 2^e,
-// c = rint(fl32(q * w) * S) is within 2^-24 |q w| S + 1/2 of q w S, so
-//   |sum c / S - exact| <= E = 2^-24 M + n / (2 S),   |sum c| <= M S (1 + 2^-24) + n / 2,
+// c = trunc(fl32(q * w) * S) is within 2^-24 |q w| S + 1 of q w S, so
+//   |sum c / S - exact| <= E = 2^-24 M + n / S,   |sum c| <= M S (1 + 2^-24),
 // and e is the largest exponent keeping the latter below 2^31.  The fp64
 // rescoring is within g64(2n) M of exact.  Any doc of the fp64 top k then has a
 // fixed-point score >= tau' - 2 (E + g64 M) S, which is the margin `mfix`.
@@ -102,7 +102,7 @@ __global__ void k_query_prep(const int32_t *__restrict__ qt, const void *__restr
     }
     const double S = ldexp(1.0, e);
     const double g64 = (2.0 * n + 2.0) * 0x1p-53 / (1.0 - (2.0 * n + 2.0) * 0x1p-53);
-    const double E = 0x1p-24 * M * (1.0 + 1e-9) + 0.5 * n / S + g64 * M;
+    const double E = 0x1p-24 * M * (1.0 + 1e-9) + n / S + g64 * M;
     double mf = ceil(2.0 * E * S) + 2.0;
     if (mf > 2147483647.0) mf = 2147483647.0;
     scale[q] = (float)S;
@@ -147,11 +147,12 @@ __device__ __forceinline__ void lds_add(A *p, A v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Fixed-point contribution of one posting: rint(fl32(qs * w)) with qs = q * 2^e.
+// Fixed-point contribution of one posting: trunc(fl32(qs * w)) with qs = q * 2^e
+// (one multiply and one v_cvt_i32_f32).
 template <int WT>
 __device__ __forceinline__ uint32_t fixed_contrib(uint32_t qbits, typename gs_weight<WT>::store_t w) {
     if (WT == GS_W_U8) return qbits * (uint32_t)w;
-    return (uint32_t)__float2int_rn(__uint_as_float(qbits) * (float)gs_weight<WT>::decode(w));
+    return (uint32_t)(int32_t)(__uint_as_float(qbits) * (float)gs_weight<WT>::decode(w));
 }
 
 // ---------------------------------------------------------------------- dense per-query tiles
@@ -378,14 +379,20 @@ struct UnionArgs {
 };
 
 constexpr int kUnionThreads = 1024;  // 16 waves
-constexpr int kUnionBatch = 1024;    // union terms staged in LDS at a time
+constexpr int kUnionBatch = 512;     // union terms staged in LDS at a time
+constexpr int kUnionEntries = 2048;  // (slot, weight) entries staged in LDS: G * T <= this
+
+// LDS bytes of k_score_union besides the G score slices
+constexpr size_t kUnionMetaLds = (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 1) * 8 +
+                                 (size_t)kUnionEntries * 5;
 
 // One workgroup = one doc tile x one query group; the G query slices of the
 // tile live in LDS as int32.  Per batch of union terms, every thread fetches one
 // term's posting sub-range for the tile and its chunk count (64 * UNROLL
-// postings per chunk); waves then take chunks round-robin, load each posting
-// once and add its fixed-point contribution to every query slot of the term
-// with ds_add_u32.  Afterwards the slices are scanned for candidates.
+// postings per chunk), and the batch's (slot, weight) entries are copied to LDS.
+// Waves then take chunks round-robin, load each posting once and add its
+// fixed-point contribution to every query slot of the term with ds_add_u32.
+// Afterwards the slices are scanned for candidates.
 template <int WT, int UNROLL>
 __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a) {
     using W = gs_weight<WT>;
@@ -405,17 +412,20 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     const int grp = (int)(lin % a.n_groups);
     const int nq = min(a.G, a.B - grp * a.G);
     const int TILE = 1 << a.tile_log2;
+    const int slice_shift = a.tile_log2 + 2;  // bytes per query slice = 1 << slice_shift
     const int64_t doc0 = (int64_t)tile << a.tile_log2;
 
     uint32_t *acc = reinterpret_cast<uint32_t *>(lds_raw);
-    int64_t *s_start = reinterpret_cast<int64_t *>(lds_raw + (size_t)a.G * TILE * sizeof(uint32_t));
+    int64_t *s_start = reinterpret_cast<int64_t *>(lds_raw + ((size_t)a.G << slice_shift));
     int32_t *s_len = reinterpret_cast<int32_t *>(s_start + kUnionBatch);
-    int32_t *s_cst = s_len + kUnionBatch;    // [kUnionBatch + 1]
-    int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch + 1]
+    int32_t *s_cst = s_len + kUnionBatch;    // [kUnionBatch + 1], s_cst[nb] = total chunks
+    int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch + 1], batch-local entry begin
+    uint32_t *s_ew = reinterpret_cast<uint32_t *>(s_e + kUnionBatch + 1);  // [kUnionEntries]
+    uint8_t *s_es = reinterpret_cast<uint8_t *>(s_ew + kUnionEntries);      // [kUnionEntries]
 
     {
         uint4 *z = reinterpret_cast<uint4 *>(acc);
-        const int n16 = (int)((size_t)nq * TILE * sizeof(uint32_t) / 16);
+        const int n16 = (nq << slice_shift) >> 4;
         for (int i = tid; i < n16; i += kUnionThreads) z[i] = make_uint4(0, 0, 0, 0);
     }
 
@@ -429,6 +439,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
 
     for (int b0 = 0; b0 < U; b0 += kUnionBatch) {
         const int nb = min(kUnionBatch, U - b0);
+        const int E0 = uebeg[b0], En = uebeg[b0 + nb];
         __syncthreads();  // LDS zeroed / previous batch consumed
         int nch = 0;
         if (tid < nb) {
@@ -437,10 +448,20 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
             const int lo = bt[0], hi = bt[1];
             s_start[tid] = a.offsets[t] + lo;
             s_len[tid] = hi - lo;
-            s_e[tid] = uebeg[b0 + tid];
-            if (tid == nb - 1) s_e[nb] = uebeg[b0 + nb];
+            s_e[tid] = uebeg[b0 + tid] - E0;
             nch = (hi - lo + CH - 1) / CH;
         }
+        if (tid == 0) s_e[nb] = En - E0;
+        // entries are staged when they fit (always for G > 1: the plan keeps
+        // G * T <= kUnionEntries); a single query wider than that reads them from HBM
+        const bool staged = En - E0 <= kUnionEntries;
+        if (staged)
+            for (int e = tid; e < En - E0; e += kUnionThreads) {
+                s_ew[e] = ew[E0 + e];
+                s_es[e] = (uint8_t)eslot[E0 + e];
+            }
+        auto entry_slot = [&](int e) { return staged ? (int)s_es[e] : eslot[E0 + e]; };
+        auto entry_w = [&](int e) { return staged ? s_ew[e] : ew[E0 + e]; };
         // exclusive scan of chunk counts
         int x = nch;
 #pragma unroll
@@ -462,60 +483,96 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         __syncthreads();
         if (tid < nb) s_cst[tid] = s_scan[wave] + x - nch;
         const int total = s_scan[16];
+        if (tid == 0) s_cst[nb] = total;
         __syncthreads();
 
-        for (int c = wave; c < total; c += NW) {
-            // last term whose first chunk is <= c (terms without chunks share the next start)
-            int lo_i = 0, hi_i = nb - 1;
-            while (lo_i < hi_i) {
-                const int mid = (lo_i + hi_i + 1) >> 1;
-                if (s_cst[mid] <= c)
-                    lo_i = mid;
-                else
-                    hi_i = mid - 1;
+        // Software-pipelined chunk loop: the next chunk of this wave is located and
+        // its posting / entry loads are issued before the current chunk's atomics,
+        // so every wave keeps one chunk of loads in flight behind its LDS work.
+        // Lanes past a chunk's end get weight 0 (adding 0 is harmless), so the adds
+        // need no lane masking; only the 64-posting groups that hold postings run.
+        struct Chunk {
+            int n, e0, m, base;  // base: LDS byte offset of the lane's entry slice
+            uint32_t my_w;
+            int col4[UNROLL];    // byte offset of the posting's doc inside a slice
+            store_t wv[UNROLL];
+        };
+        int cur_i = 0;  // term of the wave's current chunk (chunks are visited in order)
+        auto fetch = [&](int c, Chunk &k) {
+            // advance to the last term whose first chunk is <= c; s_cst is
+            // non-decreasing and s_cst[nb] = total > c, so the cursor stops in range
+            while (true) {
+                const int idx = cur_i + 1 + lane;
+                const int v = idx <= nb ? s_cst[idx] : 0x7FFFFFFF;
+                const int adv = __popcll(__ballot(v <= c));
+                cur_i += adv;
+                if (adv < 64) break;
             }
-            const int i = lo_i;
+            const int i = cur_i;
             const int ci = c - s_cst[i];
             const int64_t p0 = s_start[i] + (int64_t)ci * CH;
-            const int n = min(CH, s_len[i] - ci * CH);
-            // the term's (slot, weight) entries first (independent of the postings), then
-            // branch-free posting loads (lanes past the chunk re-read its last posting)
-            // so that all loads are in flight together; the adds below are masked
-            const int e0 = s_e[i], e1 = s_e[i + 1];
-            int my_slot = 0;
-            uint32_t my_w = 0;
-            if (lane < e1 - e0) {
-                my_slot = eslot[e0 + lane];
-                my_w = ew[e0 + lane];
-            }
-            int col[UNROLL];
-            store_t wv[UNROLL];
+            k.n = min(CH, s_len[i] - ci * CH);
+            k.e0 = s_e[i];
+            k.m = s_e[i + 1] - k.e0;
+            const int el = k.e0 + min(lane, max(k.m - 1, 0));
+            k.base = entry_slot(el) << slice_shift;
+            k.my_w = entry_w(el);
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) {
-                const int pp = min(u * 64 + lane, n - 1);
-                col[u] = (int)(a.doc[p0 + pp] - doc0);
-                wv[u] = wall[p0 + pp];
+                const int pp = u * 64 + lane;
+                const int pc = min(pp, k.n - 1);
+                k.col4[u] = (int)(a.doc[p0 + pc] - doc0) << 2;
+                const store_t w = wall[p0 + pc];
+                k.wv[u] = pp < k.n ? w : (store_t)0;
             }
-            for (int eb = e0; eb < e1; eb += 64) {
-                const int m = min(64, e1 - eb);
-                if (eb != e0) {  // more than 64 entries for one term (long duplicated queries)
-                    my_slot = lane < m ? eslot[eb + lane] : 0;
-                    my_w = lane < m ? ew[eb + lane] : 0u;
-                }
-                for (int j = 0; j < m; ++j) {
-                    const int slot = __builtin_amdgcn_readlane(my_slot, j);
-                    const uint32_t wb = __builtin_amdgcn_readlane(my_w, j);
-                    uint32_t *sl = acc + (size_t)slot * TILE;
+        };
+        auto add_entry = [&](const Chunk &k, int base, uint32_t wb) {
+            unsigned char *sl = lds_raw + base;
+            if (k.n == CH) {  // full chunk: straight-line adds
 #pragma unroll
-                    for (int u = 0; u < UNROLL; ++u)
-                        if (u * 64 + lane < n) lds_add<uint32_t>(sl + col[u], fixed_contrib<WT>(wb, wv[u]));
-                }
+                for (int u = 0; u < UNROLL; ++u)
+                    lds_add<uint32_t>(reinterpret_cast<uint32_t *>(sl + k.col4[u]), fixed_contrib<WT>(wb, k.wv[u]));
+            } else {          // last chunk of a term: only the 64-posting groups holding postings
+                const int ng = (k.n + 63) >> 6;
+#pragma unroll
+                for (int u = 0; u < UNROLL; ++u)
+                    if (u < ng)
+                        lds_add<uint32_t>(reinterpret_cast<uint32_t *>(sl + k.col4[u]),
+                                          fixed_contrib<WT>(wb, k.wv[u]));
+            }
+        };
+        auto apply = [&](const Chunk &k) {
+            if (k.m <= 64) {
+                for (int j = 0; j < k.m; ++j)
+                    add_entry(k, __builtin_amdgcn_readlane(k.base, j), __builtin_amdgcn_readlane(k.my_w, j));
+            } else {  // a term held by more than 64 query slots (queries repeating terms)
+                for (int e = k.e0; e < k.e0 + k.m; ++e) add_entry(k, entry_slot(e) << slice_shift, entry_w(e));
+            }
+        };
+        // two chunk buffers used alternately (no register copies between iterations)
+        Chunk ka, kb;
+        int c = wave;
+        if (c < total) {
+            fetch(c, ka);
+            while (true) {
+                int cn = c + NW;
+                fetch(cn < total ? cn : c, kb);  // unconditional: keeps the wait counts static
+                apply(ka);
+                if (cn >= total) break;
+                c = cn;
+                cn = c + NW;
+                fetch(cn < total ? cn : c, ka);
+                apply(kb);
+                if (cn >= total) break;
+                c = cn;
             }
         }
     }
     __syncthreads();
 
-    // ---- emission of candidates >= tau - margin, per query slot
+    // ---- emission of candidates >= tau - margin, per query slot; each lane
+    // checks 4 consecutive docs (one 16-byte LDS read), one slot reservation per
+    // 256 docs
     if (tid < nq) {
         const int q = grp * a.G + tid;
         s_thr[tid] = emit_threshold(gs_load_relaxed(a.tau + q), a.mfix[q]);
@@ -525,31 +582,41 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     __syncthreads();
     const int64_t left = a.n_docs - doc0;
     const int ncols = left < TILE ? (int)left : TILE;
-    const int cps = (ncols + 63) >> 6;  // 64-doc chunks per slot
+    const int cps = (ncols + 255) >> 8;  // 256-doc chunks per slot
     for (int ch = wave; ch < nq * cps; ch += NW) {
         const int g = ch / cps;
-        const int i = ((ch % cps) << 6) + lane;
+        const int d = ((ch % cps) << 8) + 4 * lane;
         const int q = grp * a.G + g;
-        bool keep = false;
-        uint32_t v = 0;
-        if (i < ncols) {
-            v = acc[(size_t)g * TILE + i];
-            keep = (int32_t)v > 0 && v >= s_thr[g];
+        const uint32_t thr = s_thr[g];
+        const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)g << a.tile_log2) + d);
+        const uint32_t vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        bool keep[4];
+        uint64_t mk[4];
+        uint32_t tot = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            keep[u] = d + u < ncols && (int32_t)vv[u] > 0 && vv[u] >= thr;
+            mk[u] = __ballot(keep[u]);
+            tot += (uint32_t)__popcll(mk[u]);
         }
-        const uint64_t m = __ballot(keep);
-        if (m == 0) continue;
+        if (tot == 0) continue;
         uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(a.cnt + q, (uint32_t)__popcll(m));
+        if (lane == 0) base = atomicAdd(a.cnt + q, tot);
         base = __shfl(base, 0, 64);
         uint32_t mb = 0;
-        if (keep) {
-            const uint32_t slot = base + (uint32_t)__popcll(m & gs_lanemask_lt());
-            if (slot < (uint32_t)a.cap) {
-                a.cand_doc[(int64_t)q * a.cap + slot] = (uint32_t)(doc0 + i);
-                a.cand_key[(int64_t)q * a.cap + slot] = v;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (keep[u]) {
+                const uint32_t slot = base + (uint32_t)__popcll(mk[u] & gs_lanemask_lt());
+                if (slot < (uint32_t)a.cap) {
+                    a.cand_doc[(int64_t)q * a.cap + slot] = (uint32_t)(doc0 + d + u);
+                    a.cand_key[(int64_t)q * a.cap + slot] = vv[u];
+                }
+                const uint32_t b = gs_bin_of((float)vv[u]);
+                atomicAdd(a.hist + (int64_t)q * GS_HIST_BINS + b, 1u);
+                mb = b > mb ? b : mb;
             }
-            mb = gs_bin_of((float)v);
-            atomicAdd(a.hist + (int64_t)q * GS_HIST_BINS + mb, 1u);
+            base += (uint32_t)__popcll(mk[u]);
         }
 #pragma unroll
         for (int dd = 32; dd >= 1; dd >>= 1) {
@@ -870,8 +937,7 @@ int launch_union(UnionArgs e, hipStream_t s) {
         GS_CHECK_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
         attr.store(true);
     }
-    const size_t lds = (size_t)e.G * ((size_t)1 << e.tile_log2) * 4 + (size_t)kUnionBatch * 12 +
-                       (size_t)(kUnionBatch + 1) * 8;
+    const size_t lds = ((size_t)e.G << (e.tile_log2 + 2)) + kUnionMetaLds;
     const int64_t total = (int64_t)e.tiles * e.n_groups;
     if (total == 0) return GS_OK;
     e.per_xcd = (int32_t)((total + 7) / 8);
@@ -917,7 +983,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
         while (np < g * T) np <<= 1;
         return np;
     };
-    while (G > 1 && np_of(G) > kGroupSortCap) G >>= 1;
+    while (G > 1 && (np_of(G) > kGroupSortCap || G * T > kUnionEntries)) G >>= 1;
     p.G = G;
     p.n_groups = (B + G - 1) / G;
     p.ecap = G * T;
