@@ -65,6 +65,11 @@ __device__ __forceinline__ uint64_t gs_lanemask_lt() {
 }
 
 __device__ __forceinline__ int gs_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t gs_uniform64(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 
 // Order-preserving maps of scores onto unsigned integers (larger score -> larger key).
 __device__ __forceinline__ uint32_t gs_key_f32(float f) {

@@ -367,7 +367,7 @@ struct UnionArgs {
     const void *w;
     const int64_t *offsets;
     const int32_t *tb;  // [V][n_tiles + 1]
-    int64_t n_docs;
+    int64_t n_docs, n_slots;
     int32_t V, tile_log2, n_tiles;
     int32_t B, G, n_groups, ecap;
     const int32_t *u_term, *u_ebeg, *u_count, *e_slot;
@@ -381,6 +381,7 @@ struct UnionArgs {
 constexpr int kUnionThreads = 1024;  // 16 waves
 constexpr int kUnionBatch = 512;     // union terms staged in LDS at a time
 constexpr int kUnionEntries = 2048;  // (slot, weight) entries staged in LDS: G * T <= this
+constexpr int kEmitChunks = (int)(kTileLds / 4 / 256);  // 256-doc emission chunks of one workgroup
 
 // LDS bytes of k_score_union besides the G score slices
 constexpr size_t kUnionMetaLds = (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 1) * 8 +
@@ -402,7 +403,8 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
 
     extern __shared__ __align__(16) unsigned char lds_raw[];
     __shared__ int32_t s_scan[17];
-    __shared__ uint32_t s_thr[64], s_emit[64], s_maxb[64];
+    __shared__ uint32_t s_thr[32], s_emit[32], s_maxb[32], s_base[32];
+    __shared__ uint32_t s_off[kEmitChunks];
 
     const int tid = threadIdx.x, lane = gs_lane();
     const int wave = gs_uniform(tid >> 6);
@@ -423,6 +425,13 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     uint32_t *s_ew = reinterpret_cast<uint32_t *>(s_e + kUnionBatch + 1);  // [kUnionEntries]
     uint8_t *s_es = reinterpret_cast<uint8_t *>(s_ew + kUnionEntries);      // [kUnionEntries]
 
+    // tau of the group's queries, read now so that its latency hides behind the
+    // scoring (tau only rises: an older value admits more candidates, never fewer)
+    uint32_t r_tau = 0, r_mfix = 0;
+    if (tid < nq) {
+        r_tau = gs_load_relaxed(a.tau + grp * a.G + tid);
+        r_mfix = a.mfix[grp * a.G + tid];
+    }
     {
         uint4 *z = reinterpret_cast<uint4 *>(acc);
         const int n16 = (nq << slice_shift) >> 4;
@@ -486,15 +495,16 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         if (tid == 0) s_cst[nb] = total;
         __syncthreads();
 
-        // Software-pipelined chunk loop: the next chunk of this wave is located and
-        // its posting / entry loads are issued before the current chunk's atomics,
-        // so every wave keeps one chunk of loads in flight behind its LDS work.
-        // Lanes past a chunk's end get weight 0 (adding 0 is harmless), so the adds
-        // need no lane masking; only the 64-posting groups that hold postings run.
+        // Chunk loop.  A chunk is 64 * UNROLL consecutive postings of one union
+        // term inside the tile.  Each lane loads postings lane, lane + 64, ... from
+        // a wave-uniform base, so the loads need no per-lane address arithmetic;
+        // past the chunk's end they read the neighbouring slots of the posting
+        // array (in bounds: chunks that could run past the array's end take clamped
+        // loads), and those lanes are neutralised before the adds.
         struct Chunk {
             int n, e0, m, base;  // base: LDS byte offset of the lane's entry slice
             uint32_t my_w;
-            int col4[UNROLL];    // byte offset of the posting's doc inside a slice
+            int32_t doc[UNROLL];
             store_t wv[UNROLL];
         };
         int cur_i = 0;  // term of the wave's current chunk (chunks are visited in order)
@@ -509,39 +519,60 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 if (adv < 64) break;
             }
             const int i = cur_i;
-            const int ci = c - s_cst[i];
-            const int64_t p0 = s_start[i] + (int64_t)ci * CH;
-            k.n = min(CH, s_len[i] - ci * CH);
-            k.e0 = s_e[i];
-            k.m = s_e[i + 1] - k.e0;
+            const int ci = gs_uniform(c - s_cst[i]);
+            const int64_t p0 = gs_uniform64(s_start[i]) + (int64_t)ci * CH;
+            k.n = gs_uniform(min(CH, s_len[i] - ci * CH));
+            k.e0 = gs_uniform(s_e[i]);
+            k.m = gs_uniform(s_e[i + 1]) - k.e0;
             const int el = k.e0 + min(lane, max(k.m - 1, 0));
             k.base = entry_slot(el) << slice_shift;
             k.my_w = entry_w(el);
+            if (p0 + CH <= a.n_slots) {
+                const int32_t *dp = a.doc + p0;
+                const store_t *wp = wall + p0;
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) {
-                const int pp = u * 64 + lane;
-                const int pc = min(pp, k.n - 1);
-                k.col4[u] = (int)(a.doc[p0 + pc] - doc0) << 2;
-                const store_t w = wall[p0 + pc];
-                k.wv[u] = pp < k.n ? w : (store_t)0;
+                for (int u = 0; u < UNROLL; ++u) {
+                    k.doc[u] = dp[u * 64 + lane];
+                    k.wv[u] = wp[u * 64 + lane];
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < UNROLL; ++u) {
+                    const int64_t pc = p0 + min(u * 64 + lane, k.n - 1);
+                    k.doc[u] = a.doc[pc];
+                    k.wv[u] = wall[pc];
+                }
             }
         };
+        // byte address of doc d in a slice at LDS offset `base`: (d << 2) + base -
+        // (doc0 << 2), in wrapping 32-bit arithmetic (one v_lshl_add per add)
+        const uint32_t doc0_4 = (uint32_t)doc0 << 2;
         auto add_entry = [&](const Chunk &k, int base, uint32_t wb) {
-            unsigned char *sl = lds_raw + base;
+            const uint32_t badj = (uint32_t)base - doc0_4;
             if (k.n == CH) {  // full chunk: straight-line adds
 #pragma unroll
                 for (int u = 0; u < UNROLL; ++u)
-                    lds_add<uint32_t>(reinterpret_cast<uint32_t *>(sl + k.col4[u]), fixed_contrib<WT>(wb, k.wv[u]));
+                    lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
+                                      fixed_contrib<WT>(wb, k.wv[u]));
             } else {          // last chunk of a term: only the 64-posting groups holding postings
                 const int ng = (k.n + 63) >> 6;
 #pragma unroll
                 for (int u = 0; u < UNROLL; ++u)
                     if (u < ng)
-                        lds_add<uint32_t>(reinterpret_cast<uint32_t *>(sl + k.col4[u]),
-                                          fixed_contrib<WT>(wb, k.wv[u]));
+                        lds_add<uint32_t>(
+                            reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
+                            fixed_contrib<WT>(wb, k.wv[u]));
             }
         };
-        auto apply = [&](const Chunk &k) {
+        auto apply = [&](Chunk &k) {
+            if (k.n < CH) {  // lanes past the chunk's end: doc0 with weight 0
+#pragma unroll
+                for (int u = 0; u < UNROLL; ++u) {
+                    const bool ok = u * 64 + lane < k.n;
+                    k.doc[u] = ok ? k.doc[u] : (int32_t)doc0;
+                    k.wv[u] = ok ? k.wv[u] : (store_t)0;
+                }
+            }
             if (k.m <= 64) {
                 for (int j = 0; j < k.m; ++j)
                     add_entry(k, __builtin_amdgcn_readlane(k.base, j), __builtin_amdgcn_readlane(k.my_w, j));
@@ -549,60 +580,107 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 for (int e = k.e0; e < k.e0 + k.m; ++e) add_entry(k, entry_slot(e) << slice_shift, entry_w(e));
             }
         };
-        // two chunk buffers used alternately (no register copies between iterations)
-        Chunk ka, kb;
+        // three chunk buffers in rotation: the loads of the wave's next two chunks
+        // are in flight while the current one is applied.  Fetches past the end
+        // re-read the last chunk (unconditional fetches keep the wait counts
+        // static, and the cursor only moves forward).
+        Chunk ka, kb, kc;
         int c = wave;
         if (c < total) {
+            const int last = total - 1;
             fetch(c, ka);
+            fetch(min(c + NW, last), kb);
             while (true) {
-                int cn = c + NW;
-                fetch(cn < total ? cn : c, kb);  // unconditional: keeps the wait counts static
+                fetch(min(c + 2 * NW, last), kc);
                 apply(ka);
-                if (cn >= total) break;
-                c = cn;
-                cn = c + NW;
-                fetch(cn < total ? cn : c, ka);
+                if (c + NW > last) break;
+                c += NW;
+                fetch(min(c + 2 * NW, last), ka);
                 apply(kb);
-                if (cn >= total) break;
-                c = cn;
+                if (c + NW > last) break;
+                c += NW;
+                fetch(min(c + 2 * NW, last), kb);
+                apply(kc);
+                if (c + NW > last) break;
+                c += NW;
             }
         }
     }
     __syncthreads();
 
-    // ---- emission of candidates >= tau - margin, per query slot; each lane
-    // checks 4 consecutive docs (one 16-byte LDS read), one slot reservation per
-    // 256 docs
-    if (tid < nq) {
-        const int q = grp * a.G + tid;
-        s_thr[tid] = emit_threshold(gs_load_relaxed(a.tau + q), a.mfix[q]);
-        s_emit[tid] = 0;
-        s_maxb[tid] = 0;
-    }
+    // ---- emission of candidates >= tau - margin.  The slices are scanned in
+    // 256-doc chunks, 4 docs per lane (one 16-byte LDS read).  Slices are zeroed
+    // whole and docs past n_docs get no adds, so no bound check is needed, and
+    // thr >= 1 makes the signed compare also reject zero and negative sums.
+    // Pass 1 counts each chunk's candidates; a per-slot scan gives every chunk
+    // its offset and one global atomic per slot reserves the slot's range; pass
+    // 2 revisits only the chunks holding candidates.
+    const int cps_log2 = a.tile_log2 - 8;  // 256-doc chunks per slice = 1 << cps_log2
+    const int cps = 1 << cps_log2;
+    const int nce = nq << cps_log2;        // <= kEmitChunks (G * TILE <= kTileLds / 4)
+    constexpr int kEmitIters = kEmitChunks / NW;
+    if (tid < nq) s_thr[tid] = emit_threshold(r_tau, r_mfix);
     __syncthreads();
-    const int64_t left = a.n_docs - doc0;
-    const int ncols = left < TILE ? (int)left : TILE;
-    const int cps = (ncols + 255) >> 8;  // 256-doc chunks per slot
-    for (int ch = wave; ch < nq * cps; ch += NW) {
-        const int g = ch / cps;
-        const int d = ((ch % cps) << 8) + 4 * lane;
-        const int q = grp * a.G + g;
-        const uint32_t thr = s_thr[g];
-        const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)g << a.tile_log2) + d);
-        const uint32_t vv[4] = {v4.x, v4.y, v4.z, v4.w};
-        bool keep[4];
-        uint64_t mk[4];
+    auto scan4 = [&](int ch, uint32_t vv[4], bool keep[4], uint64_t mk[4]) {
+        const int g = ch >> cps_log2;
+        const int thr = (int)s_thr[g];
+        const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
+        vv[0] = v4.x;
+        vv[1] = v4.y;
+        vv[2] = v4.z;
+        vv[3] = v4.w;
         uint32_t tot = 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            keep[u] = d + u < ncols && (int32_t)vv[u] > 0 && vv[u] >= thr;
+            keep[u] = (int32_t)vv[u] >= thr;
             mk[u] = __ballot(keep[u]);
             tot += (uint32_t)__popcll(mk[u]);
         }
-        if (tot == 0) continue;
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(a.cnt + q, tot);
-        base = __shfl(base, 0, 64);
+        return tot;
+    };
+    uint32_t it_cnt[kEmitIters];
+#pragma unroll
+    for (int it = 0; it < kEmitIters; ++it) {
+        const int ch = wave + it * NW;
+        it_cnt[it] = 0;
+        if (ch < nce) {
+            const int thr = (int)s_thr[ch >> cps_log2];
+            const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
+            const int mx = max(max((int32_t)v4.x, (int32_t)v4.y), max((int32_t)v4.z, (int32_t)v4.w));
+            if (__ballot(mx >= thr)) {
+                uint32_t vv[4];
+                bool keep[4];
+                uint64_t mk[4];
+                it_cnt[it] = scan4(ch, vv, keep, mk);
+            }
+            if (lane == 0) s_off[ch] = it_cnt[it];
+        }
+    }
+    __syncthreads();
+    if (tid < nq) {
+        uint32_t run = 0;
+        for (int i = 0; i < cps; ++i) {
+            const uint32_t t = s_off[(tid << cps_log2) + i];
+            s_off[(tid << cps_log2) + i] = run;
+            run += t;
+        }
+        s_base[tid] = run ? atomicAdd(a.cnt + grp * a.G + tid, run) : 0u;
+        s_emit[tid] = run;
+        s_maxb[tid] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kEmitIters; ++it) {
+        if (it_cnt[it] == 0) continue;
+        const int ch = wave + it * NW;
+        uint32_t vv[4];
+        bool keep[4];
+        uint64_t mk[4];
+        scan4(ch, vv, keep, mk);
+        const int g = ch >> cps_log2;
+        const int d = ((ch & (cps - 1)) << 8) + 4 * lane;
+        const int q = grp * a.G + g;
+        uint32_t base = s_base[g] + s_off[ch];
         uint32_t mb = 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -623,15 +701,23 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
             const uint32_t o = __shfl_xor(mb, dd, 64);
             mb = o > mb ? o : mb;
         }
-        if (lane == 0) {
-            s_emit[g] = 1;
-            atomicMax(&s_maxb[g], mb);
-        }
+        if (lane == 0) atomicMax(&s_maxb[g], mb);
     }
     __syncthreads();
+    // tau is recomputed from the histogram when a slot's candidate count crosses
+    // a multiple of max(k / 8, 64) at or above k; otherwise only the max bin is
+    // published
+    const uint32_t step = (uint32_t)max(a.k >> 3, 64);
     for (int g = wave; g < nq; g += NW) {
-        if (!s_emit[g]) continue;
+        const uint32_t e = s_emit[g];
+        if (!e) continue;
         const int q = grp * a.G + g;
+        const uint32_t c0 = s_base[g], c1 = c0 + e;
+        const bool raise = c1 >= (uint32_t)a.k && (c0 < (uint32_t)a.k || c0 / step != c1 / step);
+        if (!raise) {
+            if (lane == 0) atomicMax(a.maxbin + q, s_maxb[g]);
+            continue;
+        }
         uint32_t top = 0;
         if (lane == 0) top = atomicMax(a.maxbin + q, s_maxb[g]);
         top = __shfl(top, 0, 64);
@@ -1089,6 +1175,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         e.offsets = ix->offsets_d;
         e.tb = ix->tile_bounds_d;
         e.n_docs = ix->n_docs;
+        e.n_slots = ix->n_slots;
         e.V = ix->vocab;
         e.tile_log2 = ix->tile_log2;
         e.n_tiles = ix->n_tiles;
