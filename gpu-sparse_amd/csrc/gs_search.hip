@@ -379,13 +379,11 @@ struct UnionArgs {
 };
 
 constexpr int kUnionThreads = 1024;  // 16 waves
-constexpr int kUnionBatch = 512;     // union terms staged in LDS at a time
-constexpr int kUnionEntries = 2048;  // (slot, weight) entries staged in LDS: G * T <= this
+constexpr int kUnionBatch = 512;     // union terms described in LDS at a time
 constexpr int kEmitChunks = (int)(kTileLds / 4 / 256);  // 256-doc emission chunks of one workgroup
 
 // LDS bytes of k_score_union besides the G score slices
-constexpr size_t kUnionMetaLds = (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 1) * 8 +
-                                 (size_t)kUnionEntries * 5;
+constexpr size_t kUnionMetaLds = (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 1) * 8;
 
 // One workgroup = one doc tile x one query group; the G query slices of the
 // tile live in LDS as int32.  Per batch of union terms, every thread fetches one
@@ -413,7 +411,6 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     const int tile = a.tile_begin + (int)(lin / a.n_groups);
     const int grp = (int)(lin % a.n_groups);
     const int nq = min(a.G, a.B - grp * a.G);
-    const int TILE = 1 << a.tile_log2;
     const int slice_shift = a.tile_log2 + 2;  // bytes per query slice = 1 << slice_shift
     const int64_t doc0 = (int64_t)tile << a.tile_log2;
 
@@ -421,9 +418,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     int64_t *s_start = reinterpret_cast<int64_t *>(lds_raw + ((size_t)a.G << slice_shift));
     int32_t *s_len = reinterpret_cast<int32_t *>(s_start + kUnionBatch);
     int32_t *s_cst = s_len + kUnionBatch;    // [kUnionBatch + 1], s_cst[nb] = total chunks
-    int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch + 1], batch-local entry begin
-    uint32_t *s_ew = reinterpret_cast<uint32_t *>(s_e + kUnionBatch + 1);  // [kUnionEntries]
-    uint8_t *s_es = reinterpret_cast<uint8_t *>(s_ew + kUnionEntries);      // [kUnionEntries]
+    int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch + 1], first entry of each term
 
     // tau of the group's queries, read now so that its latency hides behind the
     // scoring (tau only rises: an older value admits more candidates, never fewer)
@@ -448,7 +443,6 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
 
     for (int b0 = 0; b0 < U; b0 += kUnionBatch) {
         const int nb = min(kUnionBatch, U - b0);
-        const int E0 = uebeg[b0], En = uebeg[b0 + nb];
         __syncthreads();  // LDS zeroed / previous batch consumed
         int nch = 0;
         if (tid < nb) {
@@ -457,20 +451,10 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
             const int lo = bt[0], hi = bt[1];
             s_start[tid] = a.offsets[t] + lo;
             s_len[tid] = hi - lo;
-            s_e[tid] = uebeg[b0 + tid] - E0;
+            s_e[tid] = uebeg[b0 + tid];
+            if (tid == nb - 1) s_e[nb] = uebeg[b0 + nb];
             nch = (hi - lo + CH - 1) / CH;
         }
-        if (tid == 0) s_e[nb] = En - E0;
-        // entries are staged when they fit (always for G > 1: the plan keeps
-        // G * T <= kUnionEntries); a single query wider than that reads them from HBM
-        const bool staged = En - E0 <= kUnionEntries;
-        if (staged)
-            for (int e = tid; e < En - E0; e += kUnionThreads) {
-                s_ew[e] = ew[E0 + e];
-                s_es[e] = (uint8_t)eslot[E0 + e];
-            }
-        auto entry_slot = [&](int e) { return staged ? (int)s_es[e] : eslot[E0 + e]; };
-        auto entry_w = [&](int e) { return staged ? s_ew[e] : ew[E0 + e]; };
         // exclusive scan of chunk counts
         int x = nch;
 #pragma unroll
@@ -496,113 +480,124 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         __syncthreads();
 
         // Chunk loop.  A chunk is 64 * UNROLL consecutive postings of one union
-        // term inside the tile.  Each lane loads postings lane, lane + 64, ... from
-        // a wave-uniform base, so the loads need no per-lane address arithmetic;
-        // past the chunk's end they read the neighbouring slots of the posting
-        // array (in bounds: chunks that could run past the array's end take clamped
-        // loads), and those lanes are neutralised before the adds.
+        // term inside the tile; wave w takes chunks w, w + NW, ...  Each wave first
+        // describes its next 64 chunks, one per lane (term found by binary search
+        // over the chunk scan), so the loop itself reads no LDS: chunk fields come
+        // from v_readlane, and the postings and the term's (slot, weight) entries
+        // come from global loads issued two chunks ahead.  Each lane loads
+        // postings lane, lane + 64, ... from a wave-uniform base, so the loads need
+        // no per-lane address arithmetic; past the chunk's end they read the
+        // neighbouring slots of the posting array (in bounds: chunks that could run
+        // past the array's end take clamped loads), and those lanes are
+        // neutralised before the adds.
         struct Chunk {
-            int n, e0, m, base;  // base: LDS byte offset of the lane's entry slice
-            uint32_t my_w;
+            int n, m;
+            int slot;      // lane j: slot of the term's j-th entry
+            uint32_t my_w; // lane j: its scaled query weight
             int32_t doc[UNROLL];
             store_t wv[UNROLL];
         };
-        int cur_i = 0;  // term of the wave's current chunk (chunks are visited in order)
-        auto fetch = [&](int c, Chunk &k) {
-            // advance to the last term whose first chunk is <= c; s_cst is
-            // non-decreasing and s_cst[nb] = total > c, so the cursor stops in range
+        for (int cb = wave; cb < total; cb += 64 * NW) {
+            const int nmine = min(64, (total - cb + NW - 1) / NW);  // chunks of this wave in the block
+            int64_t md_p0 = 0;
+            int md_n = 0, md_e0 = 0, md_m = 0;
+            {
+                const int c = cb + lane * NW;
+                if (c < total) {
+                    int lo = 0, hi = nb;  // s_cst[lo] <= c < s_cst[hi]
+                    while (hi - lo > 1) {
+                        const int mid = (lo + hi) >> 1;
+                        if (s_cst[mid] <= c) lo = mid;
+                        else hi = mid;
+                    }
+                    const int ci = c - s_cst[lo];
+                    md_p0 = s_start[lo] + (int64_t)ci * CH;
+                    md_n = min(CH, s_len[lo] - ci * CH);
+                    md_e0 = s_e[lo];
+                    md_m = s_e[lo + 1] - md_e0;
+                }
+            }
+            auto fetch = [&](int j, Chunk &k) {
+                const int64_t p0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(md_p0 >> 32), j) << 32) |
+                                             (uint32_t)__builtin_amdgcn_readlane((int)md_p0, j));
+                k.n = __builtin_amdgcn_readlane(md_n, j);
+                k.m = __builtin_amdgcn_readlane(md_m, j);
+                const int el = __builtin_amdgcn_readlane(md_e0, j) + min(lane, max(k.m - 1, 0));
+                k.slot = eslot[el];
+                k.my_w = ew[el];
+                if (p0 + CH <= a.n_slots) {
+                    const int32_t *dp = a.doc + p0;
+                    const store_t *wp = wall + p0;
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u) {
+                        k.doc[u] = dp[u * 64 + lane];
+                        k.wv[u] = wp[u * 64 + lane];
+                    }
+                } else {
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u) {
+                        const int64_t pc = p0 + min(u * 64 + lane, k.n - 1);
+                        k.doc[u] = a.doc[pc];
+                        k.wv[u] = wall[pc];
+                    }
+                }
+            };
+            // byte address of doc d in the slice at LDS offset `base`: (d << 2) +
+            // base - (doc0 << 2), in wrapping 32-bit arithmetic (one v_lshl_add)
+            const uint32_t doc0_4 = (uint32_t)doc0 << 2;
+            auto add_entry = [&](const Chunk &k, int slot, uint32_t wb) {
+                const uint32_t badj = ((uint32_t)slot << slice_shift) - doc0_4;
+                if (k.n == CH) {  // full chunk: straight-line adds
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u)
+                        lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
+                                          fixed_contrib<WT>(wb, k.wv[u]));
+                } else {          // last chunk of a term: only the 64-posting groups holding postings
+                    const int ng = (k.n + 63) >> 6;
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u)
+                        if (u < ng)
+                            lds_add<uint32_t>(
+                                reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
+                                fixed_contrib<WT>(wb, k.wv[u]));
+                }
+            };
+            auto apply = [&](Chunk &k, int j) {
+                if (k.n < CH) {  // lanes past the chunk's end: doc0 with weight 0
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u) {
+                        const bool ok = u * 64 + lane < k.n;
+                        k.doc[u] = ok ? k.doc[u] : (int32_t)doc0;
+                        k.wv[u] = ok ? k.wv[u] : (store_t)0;
+                    }
+                }
+                if (k.m <= 64) {
+                    for (int e = 0; e < k.m; ++e)
+                        add_entry(k, __builtin_amdgcn_readlane(k.slot, e), __builtin_amdgcn_readlane(k.my_w, e));
+                } else {  // a term held by more than 64 query slots (queries repeating terms)
+                    const int e0 = __builtin_amdgcn_readlane(md_e0, j);
+                    for (int e = e0; e < e0 + k.m; ++e) add_entry(k, eslot[e], ew[e]);
+                }
+            };
+            // three chunk buffers in rotation: the loads of the wave's next two
+            // chunks are in flight while the current one is applied.  Fetches past
+            // the end re-read the last chunk (unconditional fetches keep the wait
+            // counts static).
+            Chunk ka, kb, kc;
+            const int last = nmine - 1;
+            int j = 0;
+            fetch(0, ka);
+            fetch(min(1, last), kb);
             while (true) {
-                const int idx = cur_i + 1 + lane;
-                const int v = idx <= nb ? s_cst[idx] : 0x7FFFFFFF;
-                const int adv = __popcll(__ballot(v <= c));
-                cur_i += adv;
-                if (adv < 64) break;
-            }
-            const int i = cur_i;
-            const int ci = gs_uniform(c - s_cst[i]);
-            const int64_t p0 = gs_uniform64(s_start[i]) + (int64_t)ci * CH;
-            k.n = gs_uniform(min(CH, s_len[i] - ci * CH));
-            k.e0 = gs_uniform(s_e[i]);
-            k.m = gs_uniform(s_e[i + 1]) - k.e0;
-            const int el = k.e0 + min(lane, max(k.m - 1, 0));
-            k.base = entry_slot(el) << slice_shift;
-            k.my_w = entry_w(el);
-            if (p0 + CH <= a.n_slots) {
-                const int32_t *dp = a.doc + p0;
-                const store_t *wp = wall + p0;
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u) {
-                    k.doc[u] = dp[u * 64 + lane];
-                    k.wv[u] = wp[u * 64 + lane];
-                }
-            } else {
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u) {
-                    const int64_t pc = p0 + min(u * 64 + lane, k.n - 1);
-                    k.doc[u] = a.doc[pc];
-                    k.wv[u] = wall[pc];
-                }
-            }
-        };
-        // byte address of doc d in a slice at LDS offset `base`: (d << 2) + base -
-        // (doc0 << 2), in wrapping 32-bit arithmetic (one v_lshl_add per add)
-        const uint32_t doc0_4 = (uint32_t)doc0 << 2;
-        auto add_entry = [&](const Chunk &k, int base, uint32_t wb) {
-            const uint32_t badj = (uint32_t)base - doc0_4;
-            if (k.n == CH) {  // full chunk: straight-line adds
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u)
-                    lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
-                                      fixed_contrib<WT>(wb, k.wv[u]));
-            } else {          // last chunk of a term: only the 64-posting groups holding postings
-                const int ng = (k.n + 63) >> 6;
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u)
-                    if (u < ng)
-                        lds_add<uint32_t>(
-                            reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
-                            fixed_contrib<WT>(wb, k.wv[u]));
-            }
-        };
-        auto apply = [&](Chunk &k) {
-            if (k.n < CH) {  // lanes past the chunk's end: doc0 with weight 0
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u) {
-                    const bool ok = u * 64 + lane < k.n;
-                    k.doc[u] = ok ? k.doc[u] : (int32_t)doc0;
-                    k.wv[u] = ok ? k.wv[u] : (store_t)0;
-                }
-            }
-            if (k.m <= 64) {
-                for (int j = 0; j < k.m; ++j)
-                    add_entry(k, __builtin_amdgcn_readlane(k.base, j), __builtin_amdgcn_readlane(k.my_w, j));
-            } else {  // a term held by more than 64 query slots (queries repeating terms)
-                for (int e = k.e0; e < k.e0 + k.m; ++e) add_entry(k, entry_slot(e) << slice_shift, entry_w(e));
-            }
-        };
-        // three chunk buffers in rotation: the loads of the wave's next two chunks
-        // are in flight while the current one is applied.  Fetches past the end
-        // re-read the last chunk (unconditional fetches keep the wait counts
-        // static, and the cursor only moves forward).
-        Chunk ka, kb, kc;
-        int c = wave;
-        if (c < total) {
-            const int last = total - 1;
-            fetch(c, ka);
-            fetch(min(c + NW, last), kb);
-            while (true) {
-                fetch(min(c + 2 * NW, last), kc);
-                apply(ka);
-                if (c + NW > last) break;
-                c += NW;
-                fetch(min(c + 2 * NW, last), ka);
-                apply(kb);
-                if (c + NW > last) break;
-                c += NW;
-                fetch(min(c + 2 * NW, last), kb);
-                apply(kc);
-                if (c + NW > last) break;
-                c += NW;
+                fetch(min(j + 2, last), kc);
+                apply(ka, j);
+                if (++j > last) break;
+                fetch(min(j + 2, last), ka);
+                apply(kb, j);
+                if (++j > last) break;
+                fetch(min(j + 2, last), kb);
+                apply(kc, j);
+                if (++j > last) break;
             }
         }
     }
@@ -1069,7 +1064,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
         while (np < g * T) np <<= 1;
         return np;
     };
-    while (G > 1 && (np_of(G) > kGroupSortCap || G * T > kUnionEntries)) G >>= 1;
+    while (G > 1 && np_of(G) > kGroupSortCap) G >>= 1;
     p.G = G;
     p.n_groups = (B + G - 1) / G;
     p.ecap = G * T;
