@@ -97,6 +97,9 @@ struct gs_weight<GS_W_F32> {
     using acc_t = float;
     using qw_t = float;
     __device__ __forceinline__ static float decode(float w) { return w; }
+    __device__ __forceinline__ static float bload(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    }
 };
 template <>
 struct gs_weight<GS_W_F16> {
@@ -104,6 +107,9 @@ struct gs_weight<GS_W_F16> {
     using acc_t = float;
     using qw_t = float;
     __device__ __forceinline__ static float decode(_Float16 w) { return (float)w; }
+    __device__ __forceinline__ static _Float16 bload(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    }
 };
 template <>
 struct gs_weight<GS_W_U8> {
@@ -111,7 +117,19 @@ struct gs_weight<GS_W_U8> {
     using acc_t = uint32_t;
     using qw_t = uint8_t;
     __device__ __forceinline__ static uint32_t decode(uint8_t w) { return (uint32_t)w; }
+    __device__ __forceinline__ static uint8_t bload(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+    }
 };
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3:
+// 32-bit data format, no swizzle).  Loads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gs_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint32_t gs_bload32(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
 
 // Histogram bin of a positive score: bits of its fp32 value >> 20 (exponent and
 // three mantissa bits, ~9% wide bins), 2048 bins cover every positive float.

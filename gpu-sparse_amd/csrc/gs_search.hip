@@ -367,7 +367,7 @@ struct UnionArgs {
     const void *w;
     const int64_t *offsets;
     const int32_t *tb;  // [V][n_tiles + 1]
-    int64_t n_docs, n_slots;
+    int64_t n_docs;
     int32_t V, tile_log2, n_tiles;
     int32_t B, G, n_groups, ecap;
     const int32_t *u_term, *u_ebeg, *u_count, *e_slot;
@@ -484,12 +484,10 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         // describes its next 64 chunks, one per lane (term found by binary search
         // over the chunk scan), so the loop itself reads no LDS: chunk fields come
         // from v_readlane, and the postings and the term's (slot, weight) entries
-        // come from global loads issued two chunks ahead.  Each lane loads
-        // postings lane, lane + 64, ... from a wave-uniform base, so the loads need
-        // no per-lane address arithmetic; past the chunk's end they read the
-        // neighbouring slots of the posting array (in bounds: chunks that could run
-        // past the array's end take clamped loads), and those lanes are
-        // neutralised before the adds.
+        // come from buffer loads issued two chunks ahead.  The loads go through
+        // per-chunk buffer resources sized to the chunk, so every lane uses the
+        // same byte offset register (lane * size, plus an immediate per posting
+        // group) and lanes past the chunk's end read 0.
         struct Chunk {
             int n, m;
             int slot;      // lane j: slot of the term's j-th entry
@@ -522,24 +520,17 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                                              (uint32_t)__builtin_amdgcn_readlane((int)md_p0, j));
                 k.n = __builtin_amdgcn_readlane(md_n, j);
                 k.m = __builtin_amdgcn_readlane(md_m, j);
-                const int el = __builtin_amdgcn_readlane(md_e0, j) + min(lane, max(k.m - 1, 0));
-                k.slot = eslot[el];
-                k.my_w = ew[el];
-                if (p0 + CH <= a.n_slots) {
-                    const int32_t *dp = a.doc + p0;
-                    const store_t *wp = wall + p0;
+                const int e0 = __builtin_amdgcn_readlane(md_e0, j);
+                const auto re = gs_rsrc(eslot + e0, (uint32_t)k.m * 4u);
+                const auto rq = gs_rsrc(ew + e0, (uint32_t)k.m * 4u);
+                k.slot = (int)gs_bload32(re, lane * 4);
+                k.my_w = gs_bload32(rq, lane * 4);
+                const auto rd = gs_rsrc(a.doc + p0, (uint32_t)k.n * 4u);
+                const auto rw = gs_rsrc(wall + p0, (uint32_t)k.n * (uint32_t)sizeof(store_t));
 #pragma unroll
-                    for (int u = 0; u < UNROLL; ++u) {
-                        k.doc[u] = dp[u * 64 + lane];
-                        k.wv[u] = wp[u * 64 + lane];
-                    }
-                } else {
-#pragma unroll
-                    for (int u = 0; u < UNROLL; ++u) {
-                        const int64_t pc = p0 + min(u * 64 + lane, k.n - 1);
-                        k.doc[u] = a.doc[pc];
-                        k.wv[u] = wall[pc];
-                    }
+                for (int u = 0; u < UNROLL; ++u) {
+                    k.doc[u] = (int32_t)gs_bload32(rd, (u * 64 + lane) * 4);
+                    k.wv[u] = W::bload(rw, (u * 64 + lane) * (int)sizeof(store_t));
                 }
             };
             // byte address of doc d in the slice at LDS offset `base`: (d << 2) +
@@ -563,13 +554,9 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 }
             };
             auto apply = [&](Chunk &k, int j) {
-                if (k.n < CH) {  // lanes past the chunk's end: doc0 with weight 0
+                if (k.n < CH) {  // lanes past the chunk's end read doc 0, weight 0: move them into the tile
 #pragma unroll
-                    for (int u = 0; u < UNROLL; ++u) {
-                        const bool ok = u * 64 + lane < k.n;
-                        k.doc[u] = ok ? k.doc[u] : (int32_t)doc0;
-                        k.wv[u] = ok ? k.wv[u] : (store_t)0;
-                    }
+                    for (int u = 0; u < UNROLL; ++u) k.doc[u] = max(k.doc[u], (int32_t)doc0);
                 }
                 if (k.m <= 64) {
                     for (int e = 0; e < k.m; ++e)
@@ -1170,7 +1157,6 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         e.offsets = ix->offsets_d;
         e.tb = ix->tile_bounds_d;
         e.n_docs = ix->n_docs;
-        e.n_slots = ix->n_slots;
         e.V = ix->vocab;
         e.tile_log2 = ix->tile_log2;
         e.n_tiles = ix->n_tiles;
