@@ -372,7 +372,7 @@ struct UnionArgs {
     int32_t B, G, n_groups, ecap;
     const int32_t *u_term, *u_ebeg, *u_count, *e_slot;
     const uint32_t *e_w;
-    int32_t tile_begin, tiles, per_xcd;
+    int32_t tile_begin, tiles, tiles_per_wg, per_xcd;
     uint32_t *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key;
     const uint32_t *mfix;
     int32_t cap, k;
@@ -383,7 +383,8 @@ constexpr int kUnionBatch = 512;     // union terms described in LDS at a time
 constexpr int kEmitChunks = (int)(kTileLds / 4 / 256);  // 256-doc emission chunks of one workgroup
 
 // LDS bytes of k_score_union besides the G score slices
-constexpr size_t kUnionMetaLds = (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 1) * 8;
+constexpr size_t kUnionMetaLds =
+    (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 2) * 8 + (size_t)kUnionBatch * 12;
 
 // One workgroup = one doc tile x one query group; the G query slices of the
 // tile live in LDS as int32.  Per batch of union terms, every thread fetches one
@@ -401,37 +402,28 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
 
     extern __shared__ __align__(16) unsigned char lds_raw[];
     __shared__ int32_t s_scan[17];
-    __shared__ uint32_t s_thr[32], s_emit[32], s_maxb[32], s_base[32];
-    __shared__ uint32_t s_off[kEmitChunks];
+    __shared__ uint32_t s_thr[32], s_emit[32], s_maxb[32], s_base[32], s_mfix[32];
+    __shared__ uint32_t s_off[kEmitChunks], s_ccnt[kEmitChunks];
 
     const int tid = threadIdx.x, lane = gs_lane();
     const int wave = gs_uniform(tid >> 6);
     const int64_t lin = (int64_t)(blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
-    if (lin >= (int64_t)a.tiles * a.n_groups) return;
-    const int tile = a.tile_begin + (int)(lin / a.n_groups);
+    const int n_blk = (a.tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
+    if (lin >= (int64_t)n_blk * a.n_groups) return;
+    const int blk = (int)(lin / a.n_groups);
     const int grp = (int)(lin % a.n_groups);
+    const int tile_lo = a.tile_begin + blk * a.tiles_per_wg;
+    const int tile_hi = min(tile_lo + a.tiles_per_wg, a.tile_begin + a.tiles);
     const int nq = min(a.G, a.B - grp * a.G);
     const int slice_shift = a.tile_log2 + 2;  // bytes per query slice = 1 << slice_shift
-    const int64_t doc0 = (int64_t)tile << a.tile_log2;
 
     uint32_t *acc = reinterpret_cast<uint32_t *>(lds_raw);
     int64_t *s_start = reinterpret_cast<int64_t *>(lds_raw + ((size_t)a.G << slice_shift));
     int32_t *s_len = reinterpret_cast<int32_t *>(s_start + kUnionBatch);
     int32_t *s_cst = s_len + kUnionBatch;    // [kUnionBatch + 1], s_cst[nb] = total chunks
     int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch + 1], first entry of each term
-
-    // tau of the group's queries, read now so that its latency hides behind the
-    // scoring (tau only rises: an older value admits more candidates, never fewer)
-    uint32_t r_tau = 0, r_mfix = 0;
-    if (tid < nq) {
-        r_tau = gs_load_relaxed(a.tau + grp * a.G + tid);
-        r_mfix = a.mfix[grp * a.G + tid];
-    }
-    {
-        uint4 *z = reinterpret_cast<uint4 *>(acc);
-        const int n16 = (nq << slice_shift) >> 4;
-        for (int i = tid; i < n16; i += kUnionThreads) z[i] = make_uint4(0, 0, 0, 0);
-    }
+    int64_t *s_toff = reinterpret_cast<int64_t *>(s_e + kUnionBatch + 2);  // [kUnionBatch] list offsets
+    int32_t *s_tid = reinterpret_cast<int32_t *>(s_toff + kUnionBatch);    // [kUnionBatch] term ids
 
     const int64_t row = (int64_t)a.n_tiles + 1;
     const int U = a.u_count[grp];
@@ -441,18 +433,60 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     const uint32_t *ew = a.e_w + (int64_t)grp * a.ecap;
     const store_t *wall = reinterpret_cast<const store_t *>(a.w);
 
+    // A group whose union fits one batch describes its terms in LDS once (term
+    // id, list offset, entry range); thread `term` holds the term's bounds in the
+    // current tile and loads the next tile's while the current one is scored.
+    const bool single = U <= kUnionBatch;
+    int my_lo = 0, my_hi = 0;
+    if (single && tid < U) {
+        const int32_t t = uterm[tid];
+        s_tid[tid] = t;
+        s_toff[tid] = a.offsets[t];
+        s_e[tid] = uebeg[tid];
+        if (tid == U - 1) s_e[U] = uebeg[U];
+        my_lo = a.tb[(int64_t)t * row + tile_lo];
+        my_hi = a.tb[(int64_t)t * row + tile_lo + 1];
+    }
+    if (tid < nq) s_mfix[tid] = a.mfix[grp * a.G + tid];
+
+    for (int tile = tile_lo; tile < tile_hi; ++tile) {
+    const int64_t doc0 = (int64_t)tile << a.tile_log2;
+    // tau of the group's queries, read now so that its latency hides behind the
+    // scoring (tau only rises: an older value admits more candidates, never fewer)
+    uint32_t r_tau = 0;
+    if (tid < nq) r_tau = gs_load_relaxed(a.tau + grp * a.G + tid);
+    __syncthreads();  // the previous tile's emission is done with the slices
+    {
+        uint4 *z = reinterpret_cast<uint4 *>(acc);
+        const int n16 = (nq << slice_shift) >> 4;
+        for (int i = tid; i < n16; i += kUnionThreads) z[i] = make_uint4(0, 0, 0, 0);
+    }
+
     for (int b0 = 0; b0 < U; b0 += kUnionBatch) {
         const int nb = min(kUnionBatch, U - b0);
         __syncthreads();  // LDS zeroed / previous batch consumed
         int nch = 0;
         if (tid < nb) {
-            const int32_t t = uterm[b0 + tid];
-            const int32_t *bt = a.tb + (int64_t)t * row + tile;
-            const int lo = bt[0], hi = bt[1];
-            s_start[tid] = a.offsets[t] + lo;
+            int lo, hi;
+            if (single) {
+                lo = my_lo;
+                hi = my_hi;
+                s_start[tid] = s_toff[tid] + lo;
+                if (tile + 1 < tile_hi) {  // prefetch the next tile's bounds
+                    const int32_t *bt = a.tb + (int64_t)s_tid[tid] * row + tile + 1;
+                    my_lo = bt[0];
+                    my_hi = bt[1];
+                }
+            } else {
+                const int32_t t = uterm[b0 + tid];
+                const int32_t *bt = a.tb + (int64_t)t * row + tile;
+                lo = bt[0];
+                hi = bt[1];
+                s_start[tid] = a.offsets[t] + lo;
+                s_e[tid] = uebeg[b0 + tid];
+                if (tid == nb - 1) s_e[nb] = uebeg[b0 + nb];
+            }
             s_len[tid] = hi - lo;
-            s_e[tid] = uebeg[b0 + tid];
-            if (tid == nb - 1) s_e[nb] = uebeg[b0 + nb];
             nch = (hi - lo + CH - 1) / CH;
         }
         // exclusive scan of chunk counts
@@ -570,20 +604,16 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
             // chunks are in flight while the current one is applied.  Fetches past
             // the end re-read the last chunk (unconditional fetches keep the wait
             // counts static).
-            Chunk ka, kb, kc;
+            Chunk ka, kb;
             const int last = nmine - 1;
             int j = 0;
             fetch(0, ka);
-            fetch(min(1, last), kb);
             while (true) {
-                fetch(min(j + 2, last), kc);
+                fetch(min(j + 1, last), kb);
                 apply(ka, j);
                 if (++j > last) break;
-                fetch(min(j + 2, last), ka);
+                fetch(min(j + 1, last), ka);
                 apply(kb, j);
-                if (++j > last) break;
-                fetch(min(j + 2, last), kb);
-                apply(kc, j);
                 if (++j > last) break;
             }
         }
@@ -600,8 +630,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     const int cps_log2 = a.tile_log2 - 8;  // 256-doc chunks per slice = 1 << cps_log2
     const int cps = 1 << cps_log2;
     const int nce = nq << cps_log2;        // <= kEmitChunks (G * TILE <= kTileLds / 4)
-    constexpr int kEmitIters = kEmitChunks / NW;
-    if (tid < nq) s_thr[tid] = emit_threshold(r_tau, r_mfix);
+    if (tid < nq) s_thr[tid] = emit_threshold(r_tau, s_mfix[tid]);
     __syncthreads();
     auto scan4 = [&](int ch, uint32_t vv[4], bool keep[4], uint64_t mk[4]) {
         const int g = ch >> cps_log2;
@@ -620,22 +649,19 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         }
         return tot;
     };
-    uint32_t it_cnt[kEmitIters];
-#pragma unroll
-    for (int it = 0; it < kEmitIters; ++it) {
-        const int ch = wave + it * NW;
-        it_cnt[it] = 0;
-        if (ch < nce) {
-            const int thr = (int)s_thr[ch >> cps_log2];
-            const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
-            const int mx = max(max((int32_t)v4.x, (int32_t)v4.y), max((int32_t)v4.z, (int32_t)v4.w));
-            if (__ballot(mx >= thr)) {
-                uint32_t vv[4];
-                bool keep[4];
-                uint64_t mk[4];
-                it_cnt[it] = scan4(ch, vv, keep, mk);
-            }
-            if (lane == 0) s_off[ch] = it_cnt[it];
+    for (int ch = wave; ch < nce; ch += NW) {
+        const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
+        const int mx = max(max((int32_t)v4.x, (int32_t)v4.y), max((int32_t)v4.z, (int32_t)v4.w));
+        uint32_t cnt = 0;
+        if (__ballot(mx >= (int)s_thr[ch >> cps_log2])) {
+            uint32_t vv[4];
+            bool keep[4];
+            uint64_t mk[4];
+            cnt = scan4(ch, vv, keep, mk);
+        }
+        if (lane == 0) {
+            s_off[ch] = cnt;
+            s_ccnt[ch] = cnt;
         }
     }
     __syncthreads();
@@ -651,10 +677,8 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         s_maxb[tid] = 0;
     }
     __syncthreads();
-#pragma unroll
-    for (int it = 0; it < kEmitIters; ++it) {
-        if (it_cnt[it] == 0) continue;
-        const int ch = wave + it * NW;
+    for (int ch = wave; ch < nce; ch += NW) {
+        if (s_ccnt[ch] == 0) continue;
         uint32_t vv[4];
         bool keep[4];
         uint64_t mk[4];
@@ -678,12 +702,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
             }
             base += (uint32_t)__popcll(mk[u]);
         }
-#pragma unroll
-        for (int dd = 32; dd >= 1; dd >>= 1) {
-            const uint32_t o = __shfl_xor(mb, dd, 64);
-            mb = o > mb ? o : mb;
-        }
-        if (lane == 0) atomicMax(&s_maxb[g], mb);
+        if (mb) atomicMax(&s_maxb[g], mb);  // lanes holding candidates
     }
     __syncthreads();
     // tau is recomputed from the histogram when a slot's candidate count crosses
@@ -706,6 +725,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         top = top > s_maxb[g] ? top : s_maxb[g];
         raise_tau(a.tau + q, a.hist + (int64_t)q * GS_HIST_BINS, top, a.k);
     }
+    }  // tile
 }
 
 // ---------------------------------------------------------------------- seeding
@@ -1006,7 +1026,7 @@ int launch_union(UnionArgs e, hipStream_t s) {
         attr.store(true);
     }
     const size_t lds = ((size_t)e.G << (e.tile_log2 + 2)) + kUnionMetaLds;
-    const int64_t total = (int64_t)e.tiles * e.n_groups;
+    const int64_t total = (int64_t)((e.tiles + e.tiles_per_wg - 1) / e.tiles_per_wg) * e.n_groups;
     if (total == 0) return GS_OK;
     e.per_xcd = (int32_t)((total + 7) / 8);
     const int64_t grid = (int64_t)e.per_xcd * 8;
@@ -1017,7 +1037,7 @@ int launch_union(UnionArgs e, hipStream_t s) {
 }
 
 struct SearchPlan {
-    int S, cap, rcap, waves, unroll, G, n_groups, ecap, gt_np;
+    int S, cap, rcap, waves, unroll, G, n_groups, ecap, gt_np, tiles_per_wg;
     int32_t *u_term, *u_ebeg, *u_count, *e_slot;
     uint32_t *e_w;
     float *scale;
@@ -1062,6 +1082,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     if (p.cap < 2 * k) p.cap = 2 * k;
     p.rcap = kRescoreCap;
     p.unroll = (o && o->unroll > 0) ? o->unroll : 8;
+    p.tiles_per_wg = (o && o->tiles_per_wg > 0) ? o->tiles_per_wg : 0;
     int w = dense_waves(ix->tile_log2, 4);
     if (o && (o->waves == 4 || o->waves == 2 || o->waves == 1) && o->waves < w) w = o->waves;
     p.waves = w;
@@ -1171,6 +1192,12 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         e.e_w = p.e_w;
         e.tile_begin = p.S;
         e.tiles = ix->n_tiles - p.S;
+        e.tiles_per_wg = p.tiles_per_wg;
+        if (e.tiles_per_wg == 0) {  // default: up to 8 tiles while >= 4096 workgroups remain
+            e.tiles_per_wg = 1;
+            while (e.tiles_per_wg < 8 && (int64_t)(e.tiles / (2 * e.tiles_per_wg)) * p.n_groups >= 4096)
+                e.tiles_per_wg *= 2;
+        }
         e.tau = p.tau;
         e.cnt = p.cnt;
         e.maxbin = p.maxbin;
@@ -1268,6 +1295,8 @@ extern "C" int gs_search(const gs_index *index, const int32_t *q_terms_d, const 
     GS_REQUIRE(k >= 1 && k <= kMaxK && (int64_t)k <= index->n_docs, "k=%d outside [1, min(n_docs, %d)]", k, kMaxK);
     GS_REQUIRE(T <= kGroupSortCap, "query width T=%d exceeds %d terms", T, kGroupSortCap);
     GS_REQUIRE(q_terms_d && q_weights_d && out_scores_d && out_ids_d && status_d && workspace_d, "null pointer");
+    GS_REQUIRE(!opts || (opts->tiles_per_wg >= 0 && opts->tiles_per_wg <= 64), "tiles_per_wg=%d outside [0, 64]",
+               opts->tiles_per_wg);
     hipStream_t s = gs_stream(stream);
     switch (index->wtype) {
         case GS_W_F32:

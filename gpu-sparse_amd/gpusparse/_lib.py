@@ -55,6 +55,7 @@ class GsSearchOpts(C.Structure):
         ("waves", C.c_int32),
         ("ev_score_begin", C.c_void_p),
         ("ev_score_end", C.c_void_p),
+        ("tiles_per_wg", C.c_int32),
     ]
 
 

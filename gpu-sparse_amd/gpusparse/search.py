@@ -82,7 +82,7 @@ def _dense_rows(index, gidx, qt, qw, k, rows, out_s, out_i, dense_budget):
 
 def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG2, path: str = "auto",
            sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 0, waves: int = 0,
-           dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None):
+           tiles_per_wg: int = 0, dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None):
     """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
 
     path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense".
@@ -117,7 +117,7 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG
     if use_dense:
         _dense_rows(index, gidx, qt, qw, kk, None, out_s, out_i, max(dense_budget, 1))
         return out_s, out_i
-    opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, waves, None, None)
+    opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, waves, None, None, tiles_per_wg)
     need = _lib.C.c_size_t()
     _lib.check(L.gs_search_workspace(_lib.C.byref(gidx), B, T, kk, _lib.C.byref(opts), _lib.C.byref(need)),
                "gs_search_workspace")

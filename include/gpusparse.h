@@ -70,6 +70,8 @@ typedef struct gs_search_opts {
     int32_t waves;         /* waves per workgroup of the dense sample scorer: 1, 2 or 4 (default: fill 128 KiB) */
     void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
     void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
+    int32_t tiles_per_wg;  /* consecutive doc tiles walked by one scoring workgroup, 1..64
+                              (default: up to 8 while at least 4096 workgroups remain) */
 } gs_search_opts;
 
 int gs_query_version(void);
