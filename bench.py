@@ -39,8 +39,8 @@ def log(msg):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=15)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C3")
     ap.add_argument("--n-docs", type=int, default=None, help="override the config's collection size")
     ap.add_argument("--batch", type=int, default=512)
@@ -48,18 +48,22 @@ def parse():
     ap.add_argument("--tile-log2", type=int, default=12)
     ap.add_argument("--unroll", type=int, default=0, help="postings per lane per chunk (0: library default)")
     ap.add_argument("--waves", type=int, default=0)
-    ap.add_argument("--cpu-queries-1", type=int, default=16, help="queries timed on one core")
-    ap.add_argument("--cpu-queries-all", type=int, default=64, help="queries timed on all cores")
+    ap.add_argument("--tiles-per-wg", type=int, default=0, help="tiles walked by one scoring workgroup (0: default)")
+    ap.add_argument("--cpu-queries-1", type=int, default=96, help="queries timed on one core")
+    ap.add_argument("--cpu-queries-all", type=int, default=512, help="queries timed on all cores")
     ap.add_argument("--cpu-cores", type=int, default=16, help="cap on the cores of the all-core row")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-queries", type=int, default=4)
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
+    ap.add_argument("--summarize-traffic", default=None, metavar="DIR",
+                    help="write profiles/traffic_k_score_union_<config>.json from rocprofv3 --pmc runs under DIR")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run a plain device-to-device copy of this many bytes (PMC counter calibration)")
     return ap.parse_args()
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_k_score_union_C3.json")
+def traffic_file(cfg_name):
+    return os.path.join(ROOT, "profiles", f"traffic_k_score_union_{cfg_name}.json")
 
 
 def measured_traffic(cfg_name, n_docs, tile_log2):
@@ -67,13 +71,54 @@ def measured_traffic(cfg_name, n_docs, tile_log2):
     measurement (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size),
     when it was taken on this workload; None otherwise."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(traffic_file(cfg_name)) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
     if t.get("config") != cfg_name or t.get("n_docs") != n_docs or t.get("tile_log2") != tile_log2:
         return None
     return t.get("traffic_bytes_per_launch")
+
+
+def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
+    """Writes the traffic file from four rocprofv3 --pmc runs under `d`: f/ and w/
+    (FETCH_SIZE, WRITE_SIZE of this benchmark), cf/ and cw/ (the same counters over
+    ``--copy-bytes`` copies).  Each counter is scaled by bytes copied / counter
+    value of the last copy dispatch; values are KiB per dispatch, summed over
+    the counter's instances, last dispatch of the kernel."""
+    import csv
+    import glob
+
+    def last(sub, name):
+        rows = {}
+        for path in glob.glob(os.path.join(d, sub, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                if name in r["Kernel_Name"]:
+                    did = int(r["Dispatch_Id"])
+                    rows[did] = rows.get(did, 0.0) + float(r["Counter_Value"])
+        if not rows:
+            raise SystemExit(f"no {name} dispatch under {os.path.join(d, sub)}")
+        return rows[max(rows)]
+
+    f, w = last("f", "k_score_union"), last("w", "k_score_union")
+    cf, cw = last("cf", "copyBuffer"), last("cw", "copyBuffer")
+    fs, ws = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+    out = {"config": cfg_name, "n_docs": n_docs, "tile_log2": tile_log2, "kernel": "k_score_union",
+           "fetch_kib_per_launch": f, "write_kib_per_launch": w, "copy_bytes": copy_bytes,
+           "copy_fetch_kib": cf, "copy_write_kib": cw, "fetch_scale": fs, "write_scale": ws,
+           "fetch_bytes_per_launch": f * 1024 * fs, "write_bytes_per_launch": w * 1024 * ws,
+           "traffic_bytes_per_launch": f * 1024 * fs + w * 1024 * ws,
+           "commands": [
+               f"rocprofv3 --pmc FETCH_SIZE -d <out>/f -o f --output-format csv -- python3 bench.py --config {cfg_name} "
+               "--no-cpu --parity-queries 0 --steps 1 --warmup 1",
+               f"rocprofv3 --pmc WRITE_SIZE -d <out>/w -o w --output-format csv -- python3 bench.py --config {cfg_name} "
+               "--no-cpu --parity-queries 0 --steps 1 --warmup 1",
+               f"rocprofv3 --pmc FETCH_SIZE -d <out>/cf -o cf --output-format csv -- python3 bench.py --copy-bytes {copy_bytes}",
+               f"rocprofv3 --pmc WRITE_SIZE -d <out>/cw -o cw --output-format csv -- python3 bench.py --copy-bytes {copy_bytes}",
+               f"python3 bench.py --config {cfg_name} --summarize-traffic <out>"]}
+    with open(traffic_file(cfg_name), "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out), flush=True)
 
 
 def copy_only(nbytes):
@@ -124,6 +169,12 @@ def cpu_rows(index_h, ti, tw, k, n1, n_all, cap):
 
 def main():
     a = parse()
+    if a.summarize_traffic:
+        from gpusparse import synth
+        cfg = synth.CONFIGS[a.config]
+        n_docs = a.n_docs or cfg.docs.n_rows
+        summarize_traffic(a.summarize_traffic, cfg.name, n_docs, a.tile_log2, a.copy_bytes or (1 << 30))
+        return
     if a.copy_bytes:
         copy_only(a.copy_bytes)
         return
@@ -172,7 +223,7 @@ def main():
         if a.path == "atomic":
             return gs.atomic_fused_score(index, qt, qw, k)
         return gs.search(index, (qt, qw), k, tile_log2=a.tile_log2, path=a.path, unroll=a.unroll,
-                         waves=a.waves, timing=timing)
+                         waves=a.waves, tiles_per_wg=a.tiles_per_wg, timing=timing)
 
     for _ in range(a.warmup):
         step()
@@ -214,7 +265,8 @@ def main():
                 "frac": round(achieved / PEAK_HBM_GBS, 4),
                 "traffic": measured_traffic(cfg.name, int(index.num_docs), a.tile_log2),
                 "kernel": "k_score_union (fused group-tile LDS scoring + threshold emission)",
-                "kernel_ms_avg": round(avg_ms, 3), "kernel_ms_min": round(float(np.min(kern_ms)), 3),
+                "kernel_ms_avg": round(avg_ms, 3), "kernel_ms_median": round(float(np.median(kern_ms)), 3),
+                "kernel_ms_min": round(float(np.min(kern_ms)), 3),
                 "scored_postings_per_launch": post_launch, "bytes_per_posting": per_post,
                 "algorithmic_bytes_per_launch": bytes_launch,
                 "search_call_ms_avg": round(float(np.mean(call_ms)), 3),
@@ -223,6 +275,16 @@ def main():
         log(f"scoring kernel {avg_ms:.2f} ms avg: {achieved:.0f} GB/s algorithmic "
             f"({100 * achieved / PEAK_HBM_GBS:.1f}% of {PEAK_HBM_GBS:.0f} GB/s); "
             f"batch scored postings {post_all:.3e}")
+
+    # ---- per-phase times of gs_search (HIP events recorded by the library on
+    # its launch stream), medians over the timed steps
+    components = None
+    if a.path == "fused" and timing.get("phases"):
+        from gpusparse import _lib
+        per = np.array([[ev[i].elapsed_time(ev[i + 1]) for i in range(len(ev) - 1)] for ev in timing["phases"]])
+        components = {name: round(float(np.median(per[:, i])), 3) for i, name in enumerate(_lib.PHASE_NAMES)}
+        components["total_gs_search"] = round(float(np.median(per.sum(axis=1))), 3)
+        log(f"phases (median ms): {components}")
 
     # ---- parity sample at full size, and the CPU baseline
     parity = None
@@ -259,7 +321,7 @@ def main():
                    "postings": int(index.lengths.sum().item()), "global_batch": B, "k": k, "max_query_terms": T,
                    "weights": str(index.scores.dtype).replace("torch.", ""), "tile_docs": 1 << a.tile_log2,
                    "path": a.path},
-        "roofline": roof, "cpu_baseline": cpu, "parity": parity,
+        "roofline": roof, "cpu_baseline": cpu, "parity": parity, "components_ms": components,
         "index_build_s": round(t_build, 3), "tile_bounds_s": round(t_bounds, 3), "generate_s": round(t_gen, 1),
         "dense_rows": timing.get("dense_rows", 0),
     }

@@ -1135,11 +1135,32 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         return GS_ENOSPC;
     }
     const int64_t TILE = 1ll << ix->tile_log2;
+    // optional per-phase events: start, query prep, threshold seed, scoring,
+    // candidate selection, fp64 rescoring, final sort
+    auto phase = [&](int i) -> int {
+        if (o && o->ev_phases && o->ev_phases[i])
+            GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_phases[i]), s));
+        return GS_OK;
+    };
+    int rc = phase(0);
+    if (rc) return rc;
     k_query_prep<WT><<<gs_blocks(B, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d, ix->dup_d, p.scale,
                                                       p.mfix, p.tau, p.cnt, p.maxbin);
     k_fill<uint32_t><<<gs_blocks((int64_t)B * GS_HIST_BINS, 256, 4096), 256, 0, s>>>(
         p.hist, (int64_t)B * GS_HIST_BINS, 0u);
     GS_CHECK_LAUNCH();
+    if (ix->n_tiles > p.S) {  // per group of G queries: the union of their terms
+        static std::atomic<bool> attr{false};
+        if (!attr.load()) {
+            GS_CHECK_HIP(hipFuncSetAttribute((const void *)k_group_terms<WT>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+            attr.store(true);
+        }
+        k_group_terms<WT><<<p.n_groups, 256, (size_t)p.gt_np * 12, s>>>(
+            qt, qw, p.scale, B, T, ix->vocab, p.G, p.ecap, p.u_term, p.u_ebeg, p.u_count, p.e_slot, p.e_w);
+        GS_CHECK_LAUNCH();
+    }
+    if ((rc = phase(1))) return rc;
 
     // 1. dense fixed-point sample of tiles [0, S), then the seed threshold
     DenseArgs a = dense_args(ix, qt, qw, T);
@@ -1150,28 +1171,18 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     a.dense = p.sample;
     a.dense_ld = (int64_t)p.S * TILE;
     a.dense_col0 = 0;
-    int rc = launch_dense<WT, kDenseFixed>(a, p.waves, s);
+    rc = launch_dense<WT, kDenseFixed>(a, p.waves, s);
     if (rc) return rc;
     int64_t sample_cols = (int64_t)p.S * TILE;
     if (sample_cols > ix->n_docs) sample_cols = ix->n_docs;
     k_seed<<<B, 1024, 0, s>>>(p.sample, (int64_t)p.S * TILE, sample_cols, k, p.mfix, p.tau, p.cnt, p.maxbin, p.hist,
                               p.cand_doc, p.cand_key, p.cap);
     GS_CHECK_LAUNCH();
+    if ((rc = phase(2))) return rc;
 
-    // 2. fused scoring + emission over the remaining tiles, one workgroup per
-    //    (tile, query group) over the group's union of terms
+    // 2. fused scoring + emission over the remaining tiles: one workgroup per
+    //    (run of consecutive tiles, query group) over the group's union of terms
     if (ix->n_tiles > p.S) {
-        {
-            static std::atomic<bool> attr{false};
-            if (!attr.load()) {
-                GS_CHECK_HIP(hipFuncSetAttribute((const void *)k_group_terms<WT>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
-                attr.store(true);
-            }
-            k_group_terms<WT><<<p.n_groups, 256, (size_t)p.gt_np * 12, s>>>(
-                qt, qw, p.scale, B, T, ix->vocab, p.G, p.ecap, p.u_term, p.u_ebeg, p.u_count, p.e_slot, p.e_w);
-            GS_CHECK_LAUNCH();
-        }
         UnionArgs e{};
         e.doc = ix->doc_ids_d;
         e.w = ix->weights_d;
@@ -1192,12 +1203,11 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         e.e_w = p.e_w;
         e.tile_begin = p.S;
         e.tiles = ix->n_tiles - p.S;
-        e.tiles_per_wg = p.tiles_per_wg;
-        if (e.tiles_per_wg == 0) {  // default: up to 8 tiles while >= 4096 workgroups remain
-            e.tiles_per_wg = 1;
-            while (e.tiles_per_wg < 8 && (int64_t)(e.tiles / (2 * e.tiles_per_wg)) * p.n_groups >= 4096)
-                e.tiles_per_wg *= 2;
-        }
+        // default one tile per workgroup: the workgroups of one tile then run at
+        // the same time on one XCD and share its postings in that XCD's L2 (walking
+        // several tiles per workgroup saves per-tile set-up but the groups drift
+        // apart, and the scorer's HBM fetch grows from ~1.3x to ~8x the index at C3)
+        e.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : 1;
         e.tau = p.tau;
         e.cnt = p.cnt;
         e.maxbin = p.maxbin;
@@ -1218,21 +1228,27 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         if (rc) return rc;
         if (o && o->ev_score_end) GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_score_end), s));
     }
+    if ((rc = phase(3))) return rc;
 
     // 3. selection (+ fp64 rescoring for float weights)
     k_select_cands<WT><<<B, kSelThreads, 0, s>>>(p.cand_doc, p.cand_key, p.cnt, p.cap, k, p.mfix, p.resc_doc,
                                                  p.resc_cnt, p.rcap, out_scores, out_ids, status);
     GS_CHECK_LAUNCH();
+    if ((rc = phase(4))) return rc;
     if (FP) {
         dim3 g(64u, (unsigned)B);
         k_rescore<WT><<<g, 256, 0, s>>>(ix->doc_ids_d, ix->weights_d, ix->offsets_d, ix->tile_bounds_d, ix->vocab,
                                         ix->n_tiles, ix->tile_log2, qt, reinterpret_cast<const float *>(qw), T,
                                         p.resc_doc, p.resc_cnt, p.rcap, p.resc_key);
+        GS_CHECK_LAUNCH();
+    }
+    if ((rc = phase(5))) return rc;
+    if (FP) {
         k_select_final<WT><<<B, kSelThreads, 0, s>>>(p.resc_doc, p.resc_key, p.resc_cnt, p.rcap, k, status,
                                                      reinterpret_cast<float *>(out_scores), out_ids);
         GS_CHECK_LAUNCH();
     }
-    return GS_OK;
+    return phase(6);
 }
 
 template <int WT>

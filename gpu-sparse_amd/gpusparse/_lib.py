@@ -20,7 +20,9 @@ SYNTH_PATH = os.path.join(_HERE, "libgs_synth.so")
 GS_OK, GS_EINVAL, GS_EHIP, GS_ENOSPC = 0, 1, 2, 3
 GS_W_F32, GS_W_F16, GS_W_U8 = 0, 1, 2
 GS_ROW_DONE, GS_ROW_DENSE = 0, 1
-ABI_VERSION = 1
+GS_SEARCH_PHASES = 7
+PHASE_NAMES = ("query_prep", "threshold_seed", "scoring", "candidate_select", "fp64_rescore", "final_sort")
+ABI_VERSION = 2
 
 WTYPE_OF_DTYPE = {torch.float32: GS_W_F32, torch.float16: GS_W_F16, torch.uint8: GS_W_U8}
 
@@ -56,6 +58,7 @@ class GsSearchOpts(C.Structure):
         ("ev_score_begin", C.c_void_p),
         ("ev_score_end", C.c_void_p),
         ("tiles_per_wg", C.c_int32),
+        ("ev_phases", C.POINTER(C.c_void_p)),
     ]
 
 

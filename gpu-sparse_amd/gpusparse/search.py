@@ -88,7 +88,9 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG
     path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense".
     timing: optional dict; receives event pairs on the launch stream bracketing the
     fused scoring kernel ("score_kernel") and the whole gs_search call ("search"),
-    and the number of rows finished by the dense path ("dense_rows")."""
+    the GS_SEARCH_PHASES events of each call ("phases": start, query prep,
+    threshold seed, scoring, candidate selection, fp64 rescoring, final sort) and
+    the number of rows finished by the dense path ("dense_rows")."""
     dev = _lib.require_gpu(_device_of(index))
     N = int(index.num_docs)
     kk = min(int(k), N)
@@ -125,12 +127,15 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG
     status = torch.empty(B, dtype=torch.int32, device=dev)
     s = _lib.stream_ptr(dev)
     if timing is not None:
-        # events recorded by gs_search itself around the fused scoring kernel, and
-        # around the whole gs_search call, on the launch stream
+        # events recorded by gs_search itself around the fused scoring kernel and at
+        # its phase boundaries, and around the whole gs_search call, on the launch stream
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-        for e in evs:
+        ph = [torch.cuda.Event(enable_timing=True) for _ in range(_lib.GS_SEARCH_PHASES)]
+        for e in evs + ph:
             e.record()
         opts.ev_score_begin, opts.ev_score_end = evs[0].cuda_event, evs[1].cuda_event
+        ph_arr = (_lib.C.c_void_p * len(ph))(*[e.cuda_event for e in ph])
+        opts.ev_phases = _lib.C.cast(ph_arr, _lib.C.POINTER(_lib.C.c_void_p))
         evs[2].record()
     _lib.check(L.gs_search(_lib.C.byref(gidx), _lib.ptr(qt), _lib.ptr(qw), B, T, kk, _lib.C.byref(opts),
                            _lib.ptr(out_s), _lib.ptr(out_i), _lib.ptr(status), _lib.ptr(ws), ws.numel(), s),
@@ -139,6 +144,7 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG
         evs[3].record()
         timing.setdefault("score_kernel", []).append((evs[0], evs[1]))
         timing.setdefault("search", []).append((evs[2], evs[3]))
+        timing.setdefault("phases", []).append(ph)
     st = status.cpu().numpy()
     bad = np.nonzero(st != _lib.GS_ROW_DONE)[0]
     if timing is not None:

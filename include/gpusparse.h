@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 1
+#define GS_ABI_VERSION 2
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -70,9 +70,14 @@ typedef struct gs_search_opts {
     int32_t waves;         /* waves per workgroup of the dense sample scorer: 1, 2 or 4 (default: fill 128 KiB) */
     void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
     void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
-    int32_t tiles_per_wg;  /* consecutive doc tiles walked by one scoring workgroup, 1..64
-                              (default: up to 8 while at least 4096 workgroups remain) */
+    int32_t tiles_per_wg;  /* consecutive doc tiles walked by one scoring workgroup, 1..64 (default 1) */
+    void **ev_phases;      /* optional array of GS_SEARCH_PHASES hipEvent_t (entries may be NULL)
+                              recorded on `stream` at the phase boundaries of gs_search: start,
+                              query prep, threshold seed, scoring, candidate selection, fp64
+                              rescoring, final sort; may be NULL */
 } gs_search_opts;
+
+#define GS_SEARCH_PHASES 7
 
 int gs_query_version(void);
 const char *gs_last_error(void);

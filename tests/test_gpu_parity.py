@@ -139,10 +139,12 @@ def test_search_c1_tile_sizes(c1, tile_log2):
     assert_search_equal(ix, ref, ti[:64], tw[:64], 100, path="fused", tile_log2=tile_log2)
 
 
-@pytest.mark.parametrize("unroll,waves", [(1, 0), (2, 4), (16, 2)])
-def test_search_c1_launch_shapes(c1, unroll, waves):
+@pytest.mark.parametrize("unroll,waves,tiles_per_wg", [(1, 0, 1), (2, 4, 3), (16, 2, 64), (8, 0, 5)])
+def test_search_c1_launch_shapes(c1, unroll, waves, tiles_per_wg):
     ix, ref, ti, tw = c1
-    assert_search_equal(ix, ref, ti[:32], tw[:32], 50, path="fused", unroll=unroll, waves=waves)
+    print(f"C1 unroll={unroll} waves={waves} tiles_per_wg={tiles_per_wg}", flush=True)
+    assert_search_equal(ix, ref, ti[:32], tw[:32], 50, path="fused", unroll=unroll, waves=waves,
+                        tiles_per_wg=tiles_per_wg)
 
 
 def test_search_dense_fallback_rows(c1):
@@ -205,15 +207,16 @@ def test_search_u8_config_reduced(device):
     assert_search_equal(ix, ref, ti, tw, 1000, path="fused")
 
 
-@pytest.mark.parametrize("tile_log2", [8, 10, 12])
-def test_search_head_heavy_reduced(device, tile_log2):
+@pytest.mark.parametrize("tile_log2,tiles_per_wg", [(8, 0), (10, 0), (12, 0), (10, 4)])
+def test_search_head_heavy_reduced(device, tile_log2, tiles_per_wg):
+    """Wide head-heavy queries: group unions above one LDS batch of terms."""
     cfg = synth.scaled(synth.CONFIGS["C4"], n_docs=200_000, n_queries=32)
     docs, queries = synth.generate(cfg)
     ix = gs.build_index(docs, device)
     ref = oracle_index(docs)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
-    print(f"C4 reduced tile_log2={tile_log2} T={ti.shape[1]}", flush=True)
-    assert_search_equal(ix, ref, ti, tw, 1000, path="fused", tile_log2=tile_log2)
+    print(f"C4 reduced tile_log2={tile_log2} tiles_per_wg={tiles_per_wg} T={ti.shape[1]}", flush=True)
+    assert_search_equal(ix, ref, ti, tw, 1000, path="fused", tile_log2=tile_log2, tiles_per_wg=tiles_per_wg)
 
 
 # ------------------------------------------------------------------ selection and scatter
