@@ -279,6 +279,65 @@ __global__ void __launch_bounds__(kRsThreads)
     (void)lane;
 }
 
+// ------------------------------------------------------------------ forward (doc-major) copy
+
+// Exclusive scan of the list lengths (int64), single block; excl[V] = total.
+__global__ void __launch_bounds__(1024) k_len_scan(const int32_t *lengths, int32_t V, int64_t *excl) {
+    __shared__ int64_t sh[17];
+    int64_t carry = 0;
+    for (int base = 0; base < V; base += blockDim.x) {
+        const int i = base + threadIdx.x;
+        const int64_t len = i < V ? lengths[i] : 0;
+        int64_t tot;
+        const int64_t ex = block_excl_scan<int64_t>(len, sh, &tot);
+        if (i < V) excl[i] = carry + ex;
+        carry += tot;
+    }
+    if (threadIdx.x == 0) excl[V] = carry;
+}
+
+// The postings of the term-major index without padding, in list order: key =
+// doc id (n_docs for ids outside [0, n_docs), which then sort after every row),
+// payload = term id and weight bits.  One wave per list.
+__global__ void k_flatten(const int32_t *__restrict__ doc_ids, const void *__restrict__ w, int w_bytes,
+                          const int64_t *__restrict__ offsets, const int32_t *__restrict__ lengths, int32_t V,
+                          int64_t n_docs, const int64_t *__restrict__ excl, uint32_t *__restrict__ key,
+                          uint32_t *__restrict__ term, uint32_t *__restrict__ code) {
+    const int lane = gs_lane();
+    const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    for (int64_t t = wave; t < V; t += nwaves) {
+        const int64_t off = offsets[t], dst = excl[t];
+        const int len = lengths[t];
+        for (int i = lane; i < len; i += 64) {
+            const int32_t d = doc_ids[off + i];
+            key[dst + i] = (d >= 0 && d < n_docs) ? (uint32_t)d : (uint32_t)n_docs;
+            term[dst + i] = (uint32_t)t;
+            code[dst + i] = load_code(w, off + i, w_bytes);
+        }
+    }
+}
+
+// Sorted (doc, term, weight) entries -> row pointers, term ids and typed weights.
+template <int WT>
+__global__ void k_unpack_rows(const uint32_t *__restrict__ doc, const uint32_t *__restrict__ term,
+                              const uint32_t *__restrict__ code, int64_t n, int64_t n_docs,
+                              int64_t *__restrict__ row_ptr, int32_t *__restrict__ fwd_term, void *__restrict__ fwd_w) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i <= n; i += (int64_t)gridDim.x * blockDim.x) {
+        // rows (prev, cur] start at i: the first entry of a doc, or the end for the
+        // trailing docs (keys are <= n_docs, the key n_docs marks ids out of range)
+        const int64_t prev = i > 0 ? (int64_t)doc[i - 1] : -1;
+        const int64_t cur = i < n ? (int64_t)doc[i] : n_docs;
+        for (int64_t d = prev + 1; d <= cur; ++d) row_ptr[d] = i;
+        if (i < n) {
+            fwd_term[i] = (int32_t)term[i];
+            if (WT == GS_W_F32) reinterpret_cast<uint32_t *>(fwd_w)[i] = code[i];
+            else if (WT == GS_W_F16) reinterpret_cast<uint16_t *>(fwd_w)[i] = (uint16_t)code[i];
+            else reinterpret_cast<uint8_t *>(fwd_w)[i] = (uint8_t)code[i];
+        }
+    }
+}
+
 // Padding slots [offsets + lengths, offsets + padded) <- (-1, 0).
 template <int WT>
 __global__ void k_fill_pads(const int64_t *__restrict__ offsets, const int32_t *__restrict__ lengths,
@@ -676,6 +735,96 @@ extern "C" int gs_tile_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d
     const int64_t total = (n_tiles + 1) * (int64_t)vocab;
     k_tile_bounds<<<gs_blocks(total, 256, 1 << 16), 256, 0, gs_stream(stream)>>>(
         doc_ids_d, offsets_d, lengths_d, vocab, tile_log2, n_tiles, bounds_d);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+// ------------------------------------------------------------------ forward copy ABI
+
+namespace {
+struct FwdLayout {
+    int64_t *excl;
+    uint32_t *kb[2], *tb[2], *cb[2], *hist, *parts;
+};
+size_t fwd_layout(int64_t nnz, int32_t vocab, gs_arena &a, FwdLayout &l) {
+    const FillPlan p = fill_plan(nnz, vocab);
+    l.excl = a.take<int64_t>((size_t)vocab + 1);
+    for (int b = 0; b < 2; ++b) {
+        l.kb[b] = a.take<uint32_t>(nnz);
+        l.tb[b] = a.take<uint32_t>(nnz);
+        l.cb[b] = a.take<uint32_t>(nnz);
+    }
+    l.hist = a.take<uint32_t>(p.hist_n);
+    l.parts = a.take<uint32_t>(p.nparts);
+    return a.used;
+}
+}  // namespace
+
+extern "C" size_t gs_forward_fill_workspace(int64_t nnz, int32_t vocab) {
+    gs_arena a{nullptr, 0, 0};
+    FwdLayout l;
+    return fwd_layout(nnz, vocab, a, l) + 256;
+}
+
+extern "C" int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype,
+                               const int64_t *offsets_d, const int32_t *lengths_d, int32_t vocab, int64_t n_docs,
+                               int64_t nnz, int64_t *row_ptr_d, int32_t *fwd_terms_d, void *fwd_weights_d,
+                               void *workspace_d, size_t workspace_bytes, void *stream) {
+    GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
+    GS_REQUIRE(n_docs > 0 && n_docs < 0x7FFFFFFFll, "n_docs %lld outside [1, 2^31-1)", (long long)n_docs);
+    GS_REQUIRE(nnz >= 0 && nnz < 0xFFFFFFFFll, "nnz %lld outside [0, 2^32-1)", (long long)nnz);
+    GS_REQUIRE(wtype >= GS_W_F32 && wtype <= GS_W_U8, "unknown weight type %d", wtype);
+    GS_REQUIRE(doc_ids_d && weights_d && offsets_d && lengths_d && row_ptr_d && workspace_d, "null pointer");
+    GS_REQUIRE(nnz == 0 || (fwd_terms_d && fwd_weights_d), "null output arrays");
+    hipStream_t s = gs_stream(stream);
+    gs_arena a{reinterpret_cast<char *>(workspace_d), 0, workspace_bytes};
+    FwdLayout l;
+    fwd_layout(nnz, vocab, a, l);
+    if (!a.ok()) {
+        gs_set_error("forward_fill workspace too small: need %zu bytes, got %zu", a.used, workspace_bytes);
+        return GS_ENOSPC;
+    }
+    const int w_bytes = wtype == GS_W_F32 ? 4 : (wtype == GS_W_F16 ? 2 : 1);
+    k_len_scan<<<1, 1024, 0, s>>>(lengths_d, vocab, l.excl);
+    GS_CHECK_LAUNCH();
+    int cur = 0;
+    if (nnz > 0) {
+        k_flatten<<<gs_blocks((int64_t)vocab * 64, 256, 65536), 256, 0, s>>>(
+            doc_ids_d, weights_d, w_bytes, offsets_d, lengths_d, vocab, n_docs, l.excl, l.kb[0], l.tb[0], l.cb[0]);
+        GS_CHECK_LAUNCH();
+        // stable LSD radix sort by doc id: rows come out with ascending terms, and
+        // the entries of a repeated (doc, term) pair keep their list order
+        const FillPlan p = fill_plan(nnz, vocab);
+        int total_bits = 1;  // keys are <= n_docs
+        while (total_bits < 31 && (1ll << total_bits) <= n_docs) ++total_bits;
+        for (int shift = 0; shift < total_bits; shift += 8) {
+            const int bits = total_bits - shift < 8 ? total_bits - shift : 8;
+            k_rs_hist<<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(l.kb[cur], nnz, shift, l.hist, p.nblocks);
+            k_scan_reduce<<<(unsigned)p.nparts, 1024, 0, s>>>(l.hist, p.hist_n, l.parts);
+            k_scan_parts<<<1, 1024, 0, s>>>(l.parts, p.nparts);
+            k_scan_down<<<(unsigned)p.nparts, 1024, 0, s>>>(l.hist, p.hist_n, l.parts);
+            k_rs_scatter<false, GS_W_F32><<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(
+                l.kb[cur], l.tb[cur], l.cb[cur], 4, nnz, shift, bits, l.hist, p.nblocks, l.kb[cur ^ 1],
+                l.tb[cur ^ 1], l.cb[cur ^ 1], nullptr, nullptr, nullptr);
+            GS_CHECK_LAUNCH();
+            cur ^= 1;
+        }
+    }
+    const unsigned g = gs_blocks(nnz + 1, 256, 1 << 16);
+    switch (wtype) {
+        case GS_W_F32:
+            k_unpack_rows<GS_W_F32><<<g, 256, 0, s>>>(l.kb[cur], l.tb[cur], l.cb[cur], nnz, n_docs, row_ptr_d,
+                                                      fwd_terms_d, fwd_weights_d);
+            break;
+        case GS_W_F16:
+            k_unpack_rows<GS_W_F16><<<g, 256, 0, s>>>(l.kb[cur], l.tb[cur], l.cb[cur], nnz, n_docs, row_ptr_d,
+                                                      fwd_terms_d, fwd_weights_d);
+            break;
+        default:
+            k_unpack_rows<GS_W_U8><<<g, 256, 0, s>>>(l.kb[cur], l.tb[cur], l.cb[cur], nnz, n_docs, row_ptr_d,
+                                                     fwd_terms_d, fwd_weights_d);
+            break;
+    }
     GS_CHECK_LAUNCH();
     return GS_OK;
 }

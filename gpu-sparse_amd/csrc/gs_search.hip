@@ -43,7 +43,7 @@ namespace {
 using namespace gs;
 
 constexpr int kRescoreCap = 16384;   // candidates rescored per query before the dense fallback
-constexpr int kDefaultSample = 16;
+constexpr int kDefaultSample = 16;        // most tiles of the default threshold sample
 constexpr int kDefaultCandCap = 65536;
 constexpr size_t kTileLds = 128 * 1024;  // LDS of the score slices of one scoring workgroup
 constexpr int kGroupSortCap = 8192;      // term entries of one query group sorted in LDS
@@ -921,16 +921,82 @@ __global__ void __launch_bounds__(256)
                 }
             }
             const double p = cnt_p ? wq * (double)gs_weight<WT>::decode(wall[pos]) : 0.0;
-            // add the products in term order, and duplicates in list order, exactly as
-            // the scatter-add does; terms without a posting of d add nothing
-            const int nj = min(64, T - j0);
-            for (int l = 0; l < nj; ++l) {
-                const int cl = __shfl(cnt_p, l, 64);
-                if (cl == 0) continue;
-                s += __shfl(p, l, 64);
-                if (cl > 1) {
-                    const double wl = __shfl(wq, l, 64);
-                    const int64_t pl = __shfl(pos, l, 64);
+            // add the products in term order (ascending lanes), and duplicates in
+            // list order, exactly as the scatter-add does; terms without a posting of
+            // d add nothing.  Lane values are read with v_readlane (no LDS traffic).
+            uint64_t hit = __ballot(cnt_p > 0);
+            const uint64_t dup = __ballot(cnt_p > 1);
+            while (hit) {
+                const int l = __ffsll((unsigned long long)hit) - 1;
+                hit &= hit - 1;
+                s += gs_readlane_f64(p, l);
+                if ((dup >> l) & 1ull) {
+                    const int cl = __builtin_amdgcn_readlane(cnt_p, l);
+                    const double wl = gs_readlane_f64(wq, l);
+                    const int64_t pl = gs_readlane_i64(pos, l);
+                    for (int r = 1; r < cl; ++r) s += wl * (double)gs_weight<WT>::decode(wall[pl + r]);
+                }
+            }
+        }
+        if (lane == 0) resc_key[(int64_t)q * resc_cap + i] = gs_key_f64(s);
+    }
+}
+
+// The same exact fp64 score from the doc-major copy: lane j binary-searches
+// query term j in the candidate's row (a few hundred bytes that stay in L1
+// across the lanes) instead of in term j's posting list.  Rows hold a doc's
+// postings with ascending terms and repeated (doc, term) entries in list order,
+// so products and duplicates are added in the same order as above.
+template <int WT>
+__global__ void __launch_bounds__(256)
+    k_rescore_fwd(const int64_t *__restrict__ row_ptr, const int32_t *__restrict__ fterm,
+                  const void *__restrict__ fw, int32_t V, const int32_t *__restrict__ qt,
+                  const float *__restrict__ qw, int32_t T, const uint32_t *__restrict__ resc_doc,
+                  const uint32_t *__restrict__ resc_cnt, int32_t resc_cap, uint64_t *__restrict__ resc_key) {
+    using store_t = typename gs_weight<WT>::store_t;
+    const int q = blockIdx.y;
+    const uint32_t m = resc_cnt[q];
+    const int lane = gs_lane();
+    const int wpb = blockDim.x >> 6;
+    const store_t *wall = reinterpret_cast<const store_t *>(fw);
+    for (uint32_t i = blockIdx.x * wpb + (threadIdx.x >> 6); i < m; i += gridDim.x * wpb) {
+        const int32_t d = (int32_t)resc_doc[(int64_t)q * resc_cap + i];
+        const int64_t r0 = row_ptr[d], r1 = row_ptr[d + 1];
+        double s = 0.0;
+        for (int j0 = 0; j0 < T; j0 += 64) {
+            const int j = j0 + lane;
+            int cnt_p = 0;    // entries of term j in the row (> 1 only for duplicates)
+            int64_t pos = 0;  // the first of them
+            double wq = 0.0;
+            if (j < T) {
+                const int32_t t = qt[(int64_t)q * T + j];
+                if ((uint32_t)t < (uint32_t)V) {
+                    int64_t lo = r0, len = r1 - r0;
+                    while (len > 0) {
+                        const int64_t half = len >> 1;
+                        if (fterm[lo + half] < t) {
+                            lo += half + 1;
+                            len -= half + 1;
+                        } else {
+                            len = half;
+                        }
+                    }
+                    while (lo + cnt_p < r1 && fterm[lo + cnt_p] == t) ++cnt_p;
+                    pos = lo;
+                    wq = (double)qw[(int64_t)q * T + j];
+                }
+            }
+            const double p = cnt_p ? wq * (double)gs_weight<WT>::decode(wall[pos]) : 0.0;
+            uint64_t hit = __ballot(cnt_p > 0);
+            const uint64_t dup = __ballot(cnt_p > 1);
+            while (hit) {
+                const int l = __ffsll((unsigned long long)hit) - 1;
+                hit &= hit - 1;
+                s += gs_readlane_f64(p, l);
+                if ((dup >> l) & 1ull) {
+                    const int cl = __builtin_amdgcn_readlane(cnt_p, l);
+                    const double wl = gs_readlane_f64(wq, l);
+                    const int64_t pl = gs_readlane_i64(pos, l);
                     for (int r = 1; r < cl; ++r) s += wl * (double)gs_weight<WT>::decode(wall[pl + r]);
                 }
             }
@@ -1054,6 +1120,8 @@ int check_index(const gs_index *ix) {
                "n_tiles %d inconsistent with n_docs and tile_log2", ix->n_tiles);
     GS_REQUIRE(ix->doc_ids_d && ix->weights_d && ix->offsets_d && ix->max_abs_d && ix->dup_d && ix->tile_bounds_d,
                "index has a null device array");
+    GS_REQUIRE(!ix->fwd_ptr_d || (ix->fwd_terms_d && ix->fwd_weights_d) || ix->n_slots == 0,
+               "doc-major copy without term or weight array");
     return GS_OK;
 }
 
@@ -1076,7 +1144,10 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.n_groups = (B + G - 1) / G;
     p.ecap = G * T;
     p.gt_np = np_of(G);
-    p.S = (o && o->sample_tiles > 0) ? o->sample_tiles : kDefaultSample;
+    // default sample: 4 tiles, more for large k (about 16 k sampled docs), at most 16
+    int64_t s_def = (16ll * k + (1ll << ix->tile_log2) - 1) >> ix->tile_log2;
+    s_def = s_def < 4 ? 4 : (s_def > kDefaultSample ? kDefaultSample : s_def);
+    p.S = (o && o->sample_tiles > 0) ? o->sample_tiles : (int)s_def;
     if (p.S > ix->n_tiles) p.S = ix->n_tiles;
     p.cap = (o && o->cand_cap > 0) ? o->cand_cap : kDefaultCandCap;
     if (p.cap < 2 * k) p.cap = 2 * k;
@@ -1237,9 +1308,15 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     if ((rc = phase(4))) return rc;
     if (FP) {
         dim3 g(64u, (unsigned)B);
-        k_rescore<WT><<<g, 256, 0, s>>>(ix->doc_ids_d, ix->weights_d, ix->offsets_d, ix->tile_bounds_d, ix->vocab,
-                                        ix->n_tiles, ix->tile_log2, qt, reinterpret_cast<const float *>(qw), T,
-                                        p.resc_doc, p.resc_cnt, p.rcap, p.resc_key);
+        if (ix->fwd_ptr_d)
+            k_rescore_fwd<WT><<<g, 256, 0, s>>>(ix->fwd_ptr_d, ix->fwd_terms_d, ix->fwd_weights_d, ix->vocab, qt,
+                                                reinterpret_cast<const float *>(qw), T, p.resc_doc, p.resc_cnt,
+                                                p.rcap, p.resc_key);
+        else
+            k_rescore<WT><<<g, 256, 0, s>>>(ix->doc_ids_d, ix->weights_d, ix->offsets_d, ix->tile_bounds_d,
+                                            ix->vocab, ix->n_tiles, ix->tile_log2, qt,
+                                            reinterpret_cast<const float *>(qw), T, p.resc_doc, p.resc_cnt, p.rcap,
+                                            p.resc_key);
         GS_CHECK_LAUNCH();
     }
     if ((rc = phase(5))) return rc;

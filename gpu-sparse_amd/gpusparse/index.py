@@ -275,8 +275,31 @@ def require_ascending(index) -> None:
             f"np.argsort(..., kind='stable')); otherwise results are silently wrong.")
 
 
-def ensure_search_state(index, tile_log2: int = DEFAULT_TILE_LOG2) -> dict:
-    """Derived arrays gs_search needs: max |w|, duplicate counts, tile bounds."""
+def build_forward(index):
+    """Doc-major copy of the index (row pointers, term ids, weights) built on the
+    GPU by gs_forward_fill; the exact rescoring of float indexes reads it."""
+    dev = _device_of(index)
+    L = _lib.lib()
+    V = int(index.vocab_size)
+    N = int(index.num_docs)
+    nnz = int(index.lengths.sum().item())
+    row_ptr = torch.empty(N + 1, dtype=torch.int64, device=dev)
+    terms = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)
+    w = torch.empty(max(nnz, 1), dtype=index.scores.dtype, device=dev)
+    ws = torch.empty(int(L.gs_forward_fill_workspace(nnz, V)), dtype=torch.uint8, device=dev)
+    _lib.check(L.gs_forward_fill(_lib.ptr(index.doc_ids), _lib.ptr(index.scores), index.wtype,
+                                 _lib.ptr(index.offsets), _lib.ptr(index.lengths), V, N, nnz, _lib.ptr(row_ptr),
+                                 _lib.ptr(terms), _lib.ptr(w), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev)),
+               "gs_forward_fill")
+    del ws
+    return row_ptr, terms, w
+
+
+def ensure_search_state(index, tile_log2: int = DEFAULT_TILE_LOG2, forward: bool = True) -> dict:
+    """Derived arrays gs_search needs: max |w|, duplicate counts, tile bounds, and
+    for float weights the doc-major copy used by the exact rescoring (skipped when
+    `forward` is false or the GPU has no room for it: the rescoring then searches
+    the term lists, with the same results)."""
     a = index.aux()
     dev = _device_of(index)
     L = _lib.lib()
@@ -299,6 +322,11 @@ def ensure_search_state(index, tile_log2: int = DEFAULT_TILE_LOG2) -> dict:
         _lib.check(L.gs_tile_bounds(_lib.ptr(index.doc_ids), _lib.ptr(index.offsets), _lib.ptr(index.lengths), V,
                                     N, tile_log2, _lib.ptr(tb), _lib.stream_ptr(dev)), "gs_tile_bounds")
         a[key] = tb
+    if forward and "fwd" not in a and index.wtype != _lib.GS_W_U8 and int(index.num_docs) > 0:
+        try:
+            a["fwd"] = build_forward(index)
+        except torch.cuda.OutOfMemoryError:
+            a["fwd"] = None
     return a
 
 
@@ -319,6 +347,9 @@ def gs_index_struct(index, tile_log2: int = DEFAULT_TILE_LOG2) -> _lib.GsIndex:
     s.wtype = index.wtype
     s.tile_log2 = tile_log2
     s.n_tiles = (N + (1 << tile_log2) - 1) >> tile_log2
+    fwd = a.get("fwd")
+    if fwd is not None:
+        s.fwd_ptr_d, s.fwd_terms_d, s.fwd_weights_d = (t.data_ptr() for t in fwd)
     return s
 
 

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 2
+#define GS_ABI_VERSION 3
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -60,11 +60,16 @@ typedef struct gs_index {
     int32_t wtype;                /* GS_W_* */
     int32_t tile_log2;            /* docs per tile = 1 << tile_log2 */
     int32_t n_tiles;              /* ceil(n_docs / tile) */
+    const int64_t *fwd_ptr_d;     /* optional doc-major copy (gs_forward_fill), used by the exact */
+    const int32_t *fwd_terms_d;   /* rescoring of float indexes: [n_docs + 1] row offsets, [nnz] */
+    const void *fwd_weights_d;    /* term ids ascending within a row, [nnz] weights; NULL: the
+                                     rescoring searches the term lists instead */
 } gs_index;
 
 /* Tuning knobs of gs_search; zero selects the default. */
 typedef struct gs_search_opts {
-    int32_t sample_tiles;  /* doc tiles scored densely to seed the k-th-score threshold (default 16) */
+    int32_t sample_tiles;  /* doc tiles scored densely to seed the k-th-score threshold
+                              (default: ceil(16 k / tile docs) clamped to [4, 16]) */
     int32_t cand_cap;      /* candidates kept per query before the dense fallback (default 65536) */
     int32_t unroll;        /* postings per lane per chunk of the fused scorer: 1, 2, 4, 8 or 16 (default 8) */
     int32_t waves;         /* waves per workgroup of the dense sample scorer: 1, 2 or 4 (default: fill 128 KiB) */
@@ -133,6 +138,19 @@ int gs_chunk_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d, const in
  * The reference's per-(term, chunk) sub-ranges at LDS-tile granularity. */
 int gs_tile_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d, const int32_t *lengths_d,
                    int32_t vocab, int64_t n_docs, int32_t tile_log2, int32_t *bounds_d, void *stream);
+
+/* Doc-major copy of a term-major index, for exact candidate rescoring (the
+ * forward-index layout of src/triton_kernel_v4.py:92-158, built on the GPU from
+ * the inverted index instead of from a dense matrix).  Row d holds the postings
+ * of doc d: row_ptr_d [n_docs + 1] int64 offsets, fwd_terms_d [nnz] int32 term ids
+ * ascending within the row (entries of a repeated (doc, term) pair keep their
+ * list order), fwd_weights_d [nnz] weights in `wtype`.  nnz = sum of lengths.
+ * Doc ids outside [0, n_docs) are left out of every row. */
+size_t gs_forward_fill_workspace(int64_t nnz, int32_t vocab);
+int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, const int64_t *offsets_d,
+                    const int32_t *lengths_d, int32_t vocab, int64_t n_docs, int64_t nnz, int64_t *row_ptr_d,
+                    int32_t *fwd_terms_d, void *fwd_weights_d, void *workspace_d, size_t workspace_bytes,
+                    void *stream);
 
 /* ------------------------------------------------------------ search
  * Replaces triton_fused_score (src/triton_kernel.py:159-200) and

@@ -12,6 +12,7 @@ products, exhaustive sorting, closed forms):
 
   build_index            pinned: dict-of-lists builder + layout invariants
   chunk_bounds           pinned: linear scan per list + partition invariant
+  forward_index          pinned: the CSR rows sorted stably by column
   scores_f64 / _u32      pinned: dense Q @ D^T (float64 / int64) on small inputs
   scores_f32_sequential  pinned: scalar float32 loop of gpu_scoring.py:246-251
   topk                   pinned: Python sorted() with the same key
@@ -69,6 +70,27 @@ def build_index(indptr, indices, data, n_docs: int, vocab: int) -> dict:
     return {"doc_ids": all_docs, "scores": all_scores, "offsets": offsets, "lengths": lengths,
             "padded_lengths": padded.astype(np.int32), "max_scores": max_scores,
             "num_docs": int(n_docs), "vocab_size": int(vocab)}
+
+
+def forward_index(index: dict):
+    """Doc-major copy of a term-major index: (row_ptr [N+1] int64, terms int32,
+    weights) with each doc's postings in ascending term order and the entries of a
+    repeated (doc, term) pair in list order.  The layout of the forward index of
+    src/triton_kernel_v4.py:92-158 (doc-major term ids + weights per doc), taken
+    from the inverted index instead of a dense matrix."""
+    V, N = index["vocab_size"], index["num_docs"]
+    lengths = index["lengths"].astype(np.int64)
+    docs = np.concatenate([index["doc_ids"][index["offsets"][t]:index["offsets"][t] + lengths[t]]
+                           for t in range(V)] or [np.zeros(0, np.int32)]).astype(np.int64)
+    terms = np.repeat(np.arange(V, dtype=np.int64), lengths)
+    w = np.concatenate([index["scores"][index["offsets"][t]:index["offsets"][t] + lengths[t]]
+                        for t in range(V)] or [np.zeros(0, index["scores"].dtype)])
+    keep = (docs >= 0) & (docs < N)
+    docs, terms, w = docs[keep], terms[keep], w[keep]
+    order = np.argsort(docs, kind="stable")
+    row_ptr = np.zeros(N + 1, dtype=np.int64)
+    np.cumsum(np.bincount(docs, minlength=N), out=row_ptr[1:])
+    return row_ptr, terms[order].astype(np.int32), w[order]
 
 
 def chunk_bounds(doc_ids, offsets, lengths, vocab: int, n_docs: int, doc_chunk: int) -> np.ndarray:

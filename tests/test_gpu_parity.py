@@ -56,6 +56,35 @@ def test_build_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
     assert_index_equal(ix, oracle_index(csr))
 
 
+@pytest.mark.parametrize("seed,n_docs,vocab,dtype,dup", [
+    (0, 500, 300, np.float32, 0.0), (1, 2000, 9, np.float32, 0.2), (3, 1000, 700, np.float16, 0.05),
+    (4, 700, 250, np.uint8, 0.0), (5, 1, 3, np.float32, 0.0), (6, 400, 70000, np.float16, 0.1)])
+def test_forward_index_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
+    from gpusparse.index import build_forward
+    print(f"forward case seed={seed} n_docs={n_docs} vocab={vocab} dtype={dtype.__name__}", flush=True)
+    csr = random_csr(np.random.default_rng(seed), n_docs, vocab, dtype=dtype, dup_rate=dup)
+    ix = gs.build_index(csr, device)
+    row_ptr, terms, w = build_forward(ix)
+    want = O.forward_index(oracle_index(csr))
+    nnz = int(want[0][-1])
+    assert np.array_equal(row_ptr.cpu().numpy(), want[0])
+    assert np.array_equal(terms.cpu().numpy()[:nnz], want[1])
+    assert w.cpu().numpy()[:nnz].tobytes() == want[2].tobytes()
+
+
+def test_rescoring_without_forward_copy(c1):
+    """The rescoring that searches the term lists (used when the doc-major copy is
+    absent) gives the same answer."""
+    ix, ref, ti, tw = c1
+    a = ix.aux()
+    saved = a.get("fwd")
+    a["fwd"] = None
+    try:
+        assert_search_equal(ix, ref, ti[:32], tw[:32], 100, path="fused")
+    finally:
+        a["fwd"] = saved
+
+
 def test_build_generated_c1(device):
     docs, _ = synth.generate("C1")
     ix = gs.build_index(docs, device)

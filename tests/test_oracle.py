@@ -71,6 +71,23 @@ def test_build_index_rejects_out_of_range_terms():
         O.build_index(csr.indptr, csr.indices, csr.data, 10, int(csr.indices.max()))
 
 
+@pytest.mark.parametrize("seed,dtype,dup", [(0, np.float32, 0.0), (1, np.float16, 0.3), (2, np.uint8, 0.1)])
+def test_forward_index_is_the_csr_sorted_by_column(seed, dtype, dup):
+    """Transposing the term-major index back gives each CSR row with its columns
+    sorted stably: a (doc, term) pair repeated in a row keeps its row order, which
+    is also its list order in the inverted index."""
+    rng = np.random.default_rng(seed)
+    csr = random_csr(rng, 300, 40, dtype=dtype, dup_rate=dup)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 300, 40)
+    row_ptr, terms, w = O.forward_index(ix)
+    assert np.array_equal(row_ptr, csr.indptr)
+    for d in range(300):
+        b, e = csr.indptr[d], csr.indptr[d + 1]
+        order = sorted(range(b, e), key=lambda i: (csr.indices[i], i))
+        assert terms[b:e].tolist() == [int(csr.indices[i]) for i in order]
+        assert w[b:e].tobytes() == csr.data[order].tobytes()
+
+
 @pytest.mark.parametrize("chunk", [1, 3, 17, 64, 1000])
 def test_chunk_bounds_match_linear_scan(chunk):
     rng = np.random.default_rng(chunk)
