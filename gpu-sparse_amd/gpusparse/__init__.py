@@ -12,6 +12,7 @@ from .search import (MAX_K, atomic_fused_score, compacted_topk, scatter_add, sea
                      triton_fused_score)
 from .chunked import build_chunk_boundaries, triton_chunked_score, triton_chunked_score_fused
 from .engine import determine_dimension, retrieve, run_engine, to_csr, to_query_tensors, write_run
+from .storage import load_index, save_index
 
 __all__ = [
     "BLOCK_SIZE", "CSR", "VOCAB_SIZE", "GPUInvertedIndex", "build_from_csr", "build_gpu_index_from_csr",
@@ -19,5 +20,5 @@ __all__ = [
     "index_memory_stats", "require_ascending", "MAX_K", "atomic_fused_score", "compacted_topk", "scatter_add",
     "search", "topk_rows", "triton_fused_score", "build_chunk_boundaries", "triton_chunked_score",
     "triton_chunked_score_fused", "determine_dimension", "retrieve", "run_engine", "to_csr", "to_query_tensors",
-    "write_run",
+    "write_run", "load_index", "save_index",
 ]
