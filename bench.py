@@ -43,8 +43,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C3")
     ap.add_argument("--n-docs", type=int, default=None, help="override the config's collection size")
-    ap.add_argument("--batch", type=int, default=512)
-    ap.add_argument("--k", type=int, default=1000)
+    ap.add_argument("--batch", type=int, default=0, help="queries per batch (0: the config's)")
+    ap.add_argument("--k", type=int, default=0, help="top-k (0: the config's)")
     ap.add_argument("--tile-log2", type=int, default=12)
     ap.add_argument("--unroll", type=int, default=0, help="postings per lane per chunk (0: library default)")
     ap.add_argument("--waves", type=int, default=0)
@@ -196,7 +196,8 @@ def main():
     cfg = synth.CONFIGS[a.config]
     if a.n_docs:
         cfg = synth.scaled(cfg, n_docs=a.n_docs)
-    cfg = synth.scaled(cfg, n_queries=a.batch)
+    if a.batch:
+        cfg = synth.scaled(cfg, n_queries=a.batch)
 
     t0 = time.perf_counter()
     docs, queries = synth.generate(cfg)
@@ -217,7 +218,7 @@ def main():
         f"{t_bounds:.3f}s")
     qt, qw, T = gs.to_query_tensors(queries, dev)
     B = qt.shape[0]
-    k = min(a.k, docs.shape[0])
+    k = min(a.k or cfg.k, docs.shape[0])
     del docs
 
     def step(timing=None):
@@ -315,7 +316,8 @@ def main():
 
     n_docs = int(index.num_docs)
     res = {
-        "metric": METRIC, "value": round(qps, 2), "unit": "queries/s", "n_gpus": 1, "steps": a.steps,
+        "metric": METRIC if (cfg.name == "C3" and k == 1000 and B == 512)
+        else f"queries/s @{n_docs} docs k={k} batch {B} ({cfg.name})", "value": round(qps, 2), "unit": "queries/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32" if wbytes != 1 else "u32", "data": "synthetic",
         "config": {"workload": f"{cfg.name}: {cfg.description}", "n_docs": n_docs,
