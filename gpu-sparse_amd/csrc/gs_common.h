@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 #include <stdio.h>
 
@@ -75,6 +76,18 @@ __device__ __forceinline__ int64_t gs_readlane_i64(int64_t v, int l) {
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), l);
     return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+// f(std::integral_constant<int, n>{}) for a runtime n in [1, N] (one compare
+// chain, then straight-line code specialised for n)
+template <int N, class F>
+__device__ __forceinline__ void gs_dispatch_upto(int n, F &&f) {
+    if constexpr (N >= 1) {
+        if (n >= N) {
+            f(std::integral_constant<int, N>{});
+            return;
+        }
+        gs_dispatch_upto<N - 1>(n, f);
+    }
 }
 __device__ __forceinline__ int64_t gs_uniform64(int64_t v) {
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);

@@ -561,49 +561,59 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 k.my_w = gs_bload32(rq, lane * 4);
                 const auto rd = gs_rsrc(a.doc + p0, (uint32_t)k.n * 4u);
                 const auto rw = gs_rsrc(wall + p0, (uint32_t)k.n * (uint32_t)sizeof(store_t));
+                // lane offsets re-defined here (empty asm) so that the per-group
+                // constants fold into the loads' immediate offsets instead of
+                // being hoisted into one register each
+                int o_doc = lane * 4, o_w = lane * (int)sizeof(store_t);
+                asm volatile("" : "+v"(o_doc), "+v"(o_w));
 #pragma unroll
                 for (int u = 0; u < UNROLL; ++u) {
-                    k.doc[u] = (int32_t)gs_bload32(rd, (u * 64 + lane) * 4);
-                    k.wv[u] = W::bload(rw, (u * 64 + lane) * (int)sizeof(store_t));
+                    k.doc[u] = (int32_t)gs_bload32(rd, o_doc + u * 256);
+                    k.wv[u] = W::bload(rw, o_w + u * 64 * (int)sizeof(store_t));
                 }
             };
             // byte address of doc d in the slice at LDS offset `base`: (d << 2) +
             // base - (doc0 << 2), in wrapping 32-bit arithmetic (one v_lshl_add)
             const uint32_t doc0_4 = (uint32_t)doc0 << 2;
-            auto add_entry = [&](const Chunk &k, int slot, uint32_t wb) {
+            // the first NG 64-posting groups of a chunk, added to one query slot
+            auto add_groups = [&](const Chunk &k, auto ngc, int slot, uint32_t wb) {
+                constexpr int NG = decltype(ngc)::value;
                 const uint32_t badj = ((uint32_t)slot << slice_shift) - doc0_4;
-                if (k.n == CH) {  // full chunk: straight-line adds
 #pragma unroll
-                    for (int u = 0; u < UNROLL; ++u)
-                        lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
-                                          fixed_contrib<WT>(wb, k.wv[u]));
-                } else {          // last chunk of a term: only the 64-posting groups holding postings
-                    const int ng = (k.n + 63) >> 6;
-#pragma unroll
-                    for (int u = 0; u < UNROLL; ++u)
-                        if (u < ng)
-                            lds_add<uint32_t>(
-                                reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
-                                fixed_contrib<WT>(wb, k.wv[u]));
-                }
+                for (int u = 0; u < NG; ++u)
+                    lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
+                                      fixed_contrib<WT>(wb, k.wv[u]));
+            };
+            // every entry (query slot) of the chunk's term; the group count is
+            // resolved once per chunk, so the entry loop is straight-line adds
+            auto add_entries = [&](const Chunk &k, auto ngc) {
+                for (int e = 0; e < k.m; ++e)
+                    add_groups(k, ngc, __builtin_amdgcn_readlane(k.slot, e), __builtin_amdgcn_readlane(k.my_w, e));
             };
             auto apply = [&](Chunk &k, int j) {
-                if (k.n < CH) {  // lanes past the chunk's end read doc 0, weight 0: move them into the tile
+                if (k.m > 64) {  // a term held by more than 64 query slots (queries repeating terms)
+                    if (k.n < CH)
 #pragma unroll
-                    for (int u = 0; u < UNROLL; ++u) k.doc[u] = max(k.doc[u], (int32_t)doc0);
-                }
-                if (k.m <= 64) {
-                    for (int e = 0; e < k.m; ++e)
-                        add_entry(k, __builtin_amdgcn_readlane(k.slot, e), __builtin_amdgcn_readlane(k.my_w, e));
-                } else {  // a term held by more than 64 query slots (queries repeating terms)
+                        for (int u = 0; u < UNROLL; ++u) k.doc[u] = max(k.doc[u], (int32_t)doc0);
                     const int e0 = __builtin_amdgcn_readlane(md_e0, j);
-                    for (int e = e0; e < e0 + k.m; ++e) add_entry(k, eslot[e], ew[e]);
+                    for (int e = e0; e < e0 + k.m; ++e)
+                        add_groups(k, std::integral_constant<int, UNROLL>{}, eslot[e], ew[e]);
+                    return;
                 }
+                if (k.n == CH) {
+                    add_entries(k, std::integral_constant<int, UNROLL>{});
+                    return;
+                }
+                // last chunk of a term: lanes past its end read doc 0 and weight 0,
+                // moved into the tile; only the 64-posting groups holding postings run
+#pragma unroll
+                for (int u = 0; u < UNROLL; ++u) k.doc[u] = max(k.doc[u], (int32_t)doc0);
+                gs_dispatch_upto<UNROLL>((k.n + 63) >> 6, [&](auto ngc) { add_entries(k, ngc); });
             };
-            // three chunk buffers in rotation: the loads of the wave's next two
-            // chunks are in flight while the current one is applied.  Fetches past
-            // the end re-read the last chunk (unconditional fetches keep the wait
-            // counts static).
+            // two chunk buffers in rotation: the loads of the wave's next chunk are
+            // in flight while the current one is applied.  Fetches past the end
+            // re-read the last chunk (unconditional fetches keep the wait counts
+            // static).
             Chunk ka, kb;
             const int last = nmine - 1;
             int j = 0;
