@@ -559,13 +559,15 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 const auto rq = gs_rsrc(ew + e0, (uint32_t)k.m * 4u);
                 k.slot = (int)gs_bload32(re, lane * 4);
                 k.my_w = gs_bload32(rq, lane * 4);
-                const auto rd = gs_rsrc(a.doc + p0, (uint32_t)k.n * 4u);
-                const auto rw = gs_rsrc(wall + p0, (uint32_t)k.n * (uint32_t)sizeof(store_t));
-                // lane offsets re-defined here (empty asm) so that the per-group
-                // constants fold into the loads' immediate offsets instead of
-                // being hoisted into one register each
-                int o_doc = lane * 4, o_w = lane * (int)sizeof(store_t);
-                asm volatile("" : "+v"(o_doc), "+v"(o_w));
+                // The resources start at p0 rounded down to 64 postings; the lane
+                // offset carries the remainder.  It changes per chunk, so it is
+                // computed here and the per-group constants fold into the loads'
+                // immediate offsets.
+                const int64_t pb = p0 & ~int64_t(63);
+                const int sh = (int)(p0 - pb);
+                const auto rd = gs_rsrc(a.doc + pb, (uint32_t)(sh + k.n) * 4u);
+                const auto rw = gs_rsrc(wall + pb, (uint32_t)(sh + k.n) * (uint32_t)sizeof(store_t));
+                const int o_doc = (lane + sh) * 4, o_w = (lane + sh) * (int)sizeof(store_t);
 #pragma unroll
                 for (int u = 0; u < UNROLL; ++u) {
                     k.doc[u] = (int32_t)gs_bload32(rd, o_doc + u * 256);
