@@ -954,47 +954,62 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// The same exact fp64 score from the doc-major copy: lane j binary-searches
-// query term j in the candidate's row (a few hundred bytes that stay in L1
-// across the lanes) instead of in term j's posting list.  Rows hold a doc's
-// postings with ascending terms and repeated (doc, term) entries in list order,
-// so products and duplicates are added in the same order as above.
+// The same exact fp64 score from the doc-major copy.  The wave copies the
+// candidate's row of term ids (a few hundred bytes, one coalesced load) into
+// LDS, and lane j binary-searches query term j there instead of in term j's
+// posting list; rows longer than the LDS stage are searched in place.  Rows
+// hold a doc's postings with ascending terms and repeated (doc, term) entries in
+// list order, so products and duplicates are added in the same order as above.
+constexpr int kRescoreWaves = 4;
+constexpr int kRowStage = 512;  // row entries staged in LDS per wave
+
 template <int WT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * kRescoreWaves)
     k_rescore_fwd(const int64_t *__restrict__ row_ptr, const int32_t *__restrict__ fterm,
                   const void *__restrict__ fw, int32_t V, const int32_t *__restrict__ qt,
                   const float *__restrict__ qw, int32_t T, const uint32_t *__restrict__ resc_doc,
                   const uint32_t *__restrict__ resc_cnt, int32_t resc_cap, uint64_t *__restrict__ resc_key) {
     using store_t = typename gs_weight<WT>::store_t;
+    __shared__ int32_t s_row[kRescoreWaves][kRowStage];
     const int q = blockIdx.y;
     const uint32_t m = resc_cnt[q];
     const int lane = gs_lane();
-    const int wpb = blockDim.x >> 6;
+    const int w = threadIdx.x >> 6;
+    int32_t *row = s_row[w];
     const store_t *wall = reinterpret_cast<const store_t *>(fw);
-    for (uint32_t i = blockIdx.x * wpb + (threadIdx.x >> 6); i < m; i += gridDim.x * wpb) {
+    for (uint32_t i = blockIdx.x * kRescoreWaves + w; i < m; i += gridDim.x * kRescoreWaves) {
         const int32_t d = (int32_t)resc_doc[(int64_t)q * resc_cap + i];
         const int64_t r0 = row_ptr[d], r1 = row_ptr[d + 1];
+        const int n = (int)(r1 - r0);
+        const bool staged = n <= kRowStage;
+        if (staged) {
+            for (int e = lane; e < n; e += 64) row[e] = fterm[r0 + e];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        auto term_at = [&](int64_t e) { return staged ? row[e] : fterm[r0 + e]; };
         double s = 0.0;
         for (int j0 = 0; j0 < T; j0 += 64) {
             const int j = j0 + lane;
             int cnt_p = 0;    // entries of term j in the row (> 1 only for duplicates)
-            int64_t pos = 0;  // the first of them
+            int64_t pos = 0;  // the first of them, in the doc-major arrays
             double wq = 0.0;
             if (j < T) {
                 const int32_t t = qt[(int64_t)q * T + j];
                 if ((uint32_t)t < (uint32_t)V) {
-                    int64_t lo = r0, len = r1 - r0;
+                    int lo = 0, len = n;
                     while (len > 0) {
-                        const int64_t half = len >> 1;
-                        if (fterm[lo + half] < t) {
+                        const int half = len >> 1;
+                        if (term_at(lo + half) < t) {
                             lo += half + 1;
                             len -= half + 1;
                         } else {
                             len = half;
                         }
                     }
-                    while (lo + cnt_p < r1 && fterm[lo + cnt_p] == t) ++cnt_p;
-                    pos = lo;
+                    while (lo + cnt_p < n && term_at(lo + cnt_p) == t) ++cnt_p;
+                    pos = r0 + lo;
                     wq = (double)qw[(int64_t)q * T + j];
                 }
             }
@@ -1014,6 +1029,7 @@ __global__ void __launch_bounds__(256)
             }
         }
         if (lane == 0) resc_key[(int64_t)q * resc_cap + i] = gs_key_f64(s);
+        __builtin_amdgcn_wave_barrier();  // the row stage is reused by the next candidate
     }
 }
 
@@ -1321,9 +1337,9 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     if (FP) {
         dim3 g(64u, (unsigned)B);
         if (ix->fwd_ptr_d)
-            k_rescore_fwd<WT><<<g, 256, 0, s>>>(ix->fwd_ptr_d, ix->fwd_terms_d, ix->fwd_weights_d, ix->vocab, qt,
-                                                reinterpret_cast<const float *>(qw), T, p.resc_doc, p.resc_cnt,
-                                                p.rcap, p.resc_key);
+            k_rescore_fwd<WT><<<g, 64 * kRescoreWaves, 0, s>>>(
+                ix->fwd_ptr_d, ix->fwd_terms_d, ix->fwd_weights_d, ix->vocab, qt,
+                reinterpret_cast<const float *>(qw), T, p.resc_doc, p.resc_cnt, p.rcap, p.resc_key);
         else
             k_rescore<WT><<<g, 256, 0, s>>>(ix->doc_ids_d, ix->weights_d, ix->offsets_d, ix->tile_bounds_d,
                                             ix->vocab, ix->n_tiles, ix->tile_log2, qt,
