@@ -43,14 +43,13 @@ namespace {
 using namespace gs;
 
 constexpr int kRescoreCap = 16384;   // candidates rescored per query before the dense fallback
-constexpr int kDefaultSample = 16;        // most tiles of the default threshold sample
+constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
 constexpr size_t kTileLds = 128 * 1024;  // LDS of the score slices of one scoring workgroup
 constexpr int kGroupSortCap = 8192;      // term entries of one query group sorted in LDS
 // dynamic-LDS cap requested per kernel: 160 KiB per workgroup minus room for static LDS
 constexpr int kMaxDynLds = 152 * 1024;
 
-enum ScoreMode { kDenseFixed = 0, kDenseExact = 1 };
 
 template <class T>
 __global__ void k_fill(T *p, int64_t n, T v) {
@@ -164,7 +163,6 @@ struct DenseArgs {
     const int32_t *tb;  // [V][n_tiles + 1]
     const int32_t *qt;
     const void *qw;
-    const float *scale;   // kDenseFixed: per-query fixed-point scale
     const int32_t *rows;  // optional row -> query map
     int64_t n_docs;
     int32_t V, T, R, tile_log2, n_tiles;
@@ -175,14 +173,13 @@ struct DenseArgs {
 
 // One wave owns one (query, tile): it walks the query's terms in order, adds
 // every posting of the tile into its LDS slice and writes the slice to a dense
-// row.  kDenseFixed: fixed-point int32 (the seeding sample).  kDenseExact:
-// fp64 for float weights (terms added in query order, i.e. the fp64 scatter-add
-// itself) or uint32 for uint8 impacts -- the exact dense path.
-template <int WT, int MODE, int UNROLL>
+// row: fp64 for float weights (terms added in query order, i.e. the fp64
+// scatter-add itself) or uint32 for uint8 impacts -- the exact dense path.
+template <int WT, int UNROLL>
 __global__ void __launch_bounds__(512) k_score_dense(const DenseArgs a) {
     using W = gs_weight<WT>;
     using store_t = typename W::store_t;
-    constexpr bool kF64 = MODE == kDenseExact && WT != GS_W_U8;
+    constexpr bool kF64 = WT != GS_W_U8;
     using acc_t = typename std::conditional<kF64, double, uint32_t>::type;
 
     extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -207,7 +204,6 @@ __global__ void __launch_bounds__(512) k_score_dense(const DenseArgs a) {
     const int32_t *qt = a.qt + (int64_t)q * a.T;
     const int64_t row = (int64_t)a.n_tiles + 1;
     const store_t *wall = reinterpret_cast<const store_t *>(a.w);
-    const float sc = (MODE == kDenseFixed && WT != GS_W_U8) ? a.scale[q] : 1.0f;
     for (int j = 0; j < a.T; ++j) {
         const int32_t t = qt[j];
         if ((uint32_t)t >= (uint32_t)a.V) continue;
@@ -217,15 +213,12 @@ __global__ void __launch_bounds__(512) k_score_dense(const DenseArgs a) {
         const int64_t base = a.offsets[t];
         const int32_t *dp = a.doc + base;
         const store_t *wp = wall + base;
-        uint32_t qbits;
+        uint32_t qbits = 0;
         double wq64 = 0.0;
-        if (WT == GS_W_U8) {
+        if (WT == GS_W_U8)
             qbits = reinterpret_cast<const uint8_t *>(a.qw)[(int64_t)q * a.T + j];
-        } else {
-            const float wq = reinterpret_cast<const float *>(a.qw)[(int64_t)q * a.T + j];
-            qbits = __float_as_uint(wq * sc);
-            wq64 = (double)wq;
-        }
+        else
+            wq64 = (double)reinterpret_cast<const float *>(a.qw)[(int64_t)q * a.T + j];
         auto contrib = [&](store_t wv) -> acc_t {
             if (kF64) return (acc_t)(wq64 * (double)W::decode(wv));
             return (acc_t)fixed_contrib<WT>(qbits, wv);
@@ -742,79 +735,15 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
 
 // ---------------------------------------------------------------------- seeding
 
-// Per query: tau from the histogram of the dense fixed-point sample, then
-// emission of the sample's candidates exactly as the scoring kernel emits them.
-__global__ void __launch_bounds__(1024)
-    k_seed(const uint32_t *__restrict__ sample, int64_t ld, int64_t ncols, int32_t k,
-           const uint32_t *__restrict__ mfix, uint32_t *__restrict__ tau_arr, uint32_t *__restrict__ cnt,
-           uint32_t *__restrict__ maxbin, uint32_t *__restrict__ hist_all, uint32_t *__restrict__ cand_doc,
-           uint32_t *__restrict__ cand_key, int32_t cap) {
-    __shared__ uint32_t h[GS_HIST_BINS];
-    __shared__ uint32_t s_tau, s_maxbin;
-    const int q = blockIdx.x;
-    const uint32_t *row = sample + (int64_t)q * ld;
-    for (int b = threadIdx.x; b < GS_HIST_BINS; b += blockDim.x) h[b] = 0;
-    if (threadIdx.x == 0) {
-        s_tau = 0;
-        s_maxbin = 0;
-    }
-    __syncthreads();
-    for (int64_t i = threadIdx.x; i < ncols; i += blockDim.x) {
-        const uint32_t v = row[i];
-        if ((int32_t)v > 0) atomicAdd(&h[gs_bin_of((float)v)], 1u);
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        uint32_t cum = 0;
-        for (int b = GS_HIST_BINS - 1; b >= 0; b -= 64) {
-            const int bb = b - gs_lane();
-            const uint32_t c = bb >= 0 ? h[bb] : 0u;
-            const uint32_t inc = gs_wave_incl_scan(c);
-            const uint64_t hit = __ballot(cum + inc >= (uint32_t)k);
-            if (hit) {
-                const uint32_t bin = (uint32_t)(b - (__ffsll((unsigned long long)hit) - 1));
-                if (gs_lane() == 0) s_tau = int_threshold_of_bin(bin);
-                break;
-            }
-            cum += __shfl(inc, 63, 64);
-        }
-    }
-    __syncthreads();
-    const uint32_t tau = s_tau;
-    const uint32_t thr = emit_threshold(tau, mfix[q]);
-    uint32_t *hist = hist_all + (int64_t)q * GS_HIST_BINS;
-    uint32_t max_bin = 0;
-    const int lane = gs_lane();
-    const int64_t span = (ncols + 63) & ~int64_t(63);
-    for (int64_t i = threadIdx.x; i < span; i += blockDim.x) {
-        bool keep = false;
-        uint32_t v = 0;
-        if (i < ncols) {
-            v = row[i];
-            keep = (int32_t)v > 0 && v >= thr;
-        }
-        const uint64_t m = __ballot(keep);
-        if (m == 0) continue;
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(cnt + q, (uint32_t)__popcll(m));
-        base = __shfl(base, 0, 64);
-        if (keep) {
-            const uint32_t slot = base + (uint32_t)__popcll(m & gs_lanemask_lt());
-            if (slot < (uint32_t)cap) {
-                cand_doc[(int64_t)q * cap + slot] = (uint32_t)i;
-                cand_key[(int64_t)q * cap + slot] = v;
-            }
-            const uint32_t b = gs_bin_of((float)v);
-            atomicAdd(hist + b, 1u);
-            max_bin = b > max_bin ? b : max_bin;
-        }
-    }
-    atomicMax(&s_maxbin, max_bin);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        tau_arr[q] = tau;
-        maxbin[q] = s_maxbin;
-    }
+// Per query (one wave): tau from the histogram of the candidates emitted so
+// far (every positive doc of the first tiles): the lower edge of the highest bin
+// with at least k candidates at or above it.
+__global__ void __launch_bounds__(256)
+    k_tau_seed(uint32_t *__restrict__ tau, const uint32_t *__restrict__ maxbin, const uint32_t *__restrict__ hist,
+               int32_t B, int32_t k) {
+    const int q = (int)((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6);
+    if (q >= B) return;
+    raise_tau(tau + q, hist + (int64_t)q * GS_HIST_BINS, gs_load_relaxed(maxbin + q), k);
 }
 
 // ---------------------------------------------------------------------- selection
@@ -1085,10 +1014,10 @@ int dense_waves(int tile_log2, size_t acc_bytes) {
     return w;
 }
 
-template <int WT, int MODE, int UNROLL>
+template <int WT, int UNROLL>
 int launch_dense_u(DenseArgs a, int waves, size_t acc_bytes, hipStream_t s) {
     static std::atomic<bool> attr_set{false};
-    auto fn = k_score_dense<WT, MODE, UNROLL>;
+    auto fn = k_score_dense<WT, UNROLL>;
     const size_t lds = (size_t)waves * (size_t(1) << a.tile_log2) * acc_bytes;
     if (!attr_set.load()) {
         GS_CHECK_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
@@ -1105,10 +1034,10 @@ int launch_dense_u(DenseArgs a, int waves, size_t acc_bytes, hipStream_t s) {
     return GS_OK;
 }
 
-template <int WT, int MODE>
+template <int WT>
 int launch_dense(DenseArgs a, int waves, hipStream_t s) {
-    constexpr size_t acc_bytes = (MODE == kDenseExact && WT != GS_W_U8) ? 8 : 4;
-    return launch_dense_u<WT, MODE, 4>(a, waves, acc_bytes, s);
+    constexpr size_t acc_bytes = WT != GS_W_U8 ? 8 : 4;
+    return launch_dense_u<WT, 4>(a, waves, acc_bytes, s);
 }
 
 template <int WT, int UNROLL>
@@ -1131,11 +1060,11 @@ int launch_union(UnionArgs e, hipStream_t s) {
 }
 
 struct SearchPlan {
-    int S, cap, rcap, waves, unroll, G, n_groups, ecap, gt_np, tiles_per_wg;
+    int S, cap, rcap, unroll, G, n_groups, ecap, gt_np, tiles_per_wg;
     int32_t *u_term, *u_ebeg, *u_count, *e_slot;
     uint32_t *e_w;
     float *scale;
-    uint32_t *mfix, *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key, *resc_doc, *resc_cnt, *sample;
+    uint32_t *mfix, *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key, *resc_doc, *resc_cnt;
     uint64_t *resc_key;
 };
 
@@ -1172,9 +1101,12 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.n_groups = (B + G - 1) / G;
     p.ecap = G * T;
     p.gt_np = np_of(G);
-    // default sample: 4 tiles, more for large k (about 16 k sampled docs), at most 16
-    int64_t s_def = (16ll * k + (1ll << ix->tile_log2) - 1) >> ix->tile_log2;
-    s_def = s_def < 4 ? 4 : (s_def > kDefaultSample ? kDefaultSample : s_def);
+    // default first tiles scored with tau = 0: about 4 k docs, at least 2 tiles
+    // and at most 32 Ki docs (all of their positive docs become candidates)
+    const int64_t TILE = 1ll << ix->tile_log2;
+    int64_t s_def = (4ll * k + TILE - 1) >> ix->tile_log2;
+    const int64_t s_max = std::max<int64_t>(2, kSeedDocs >> ix->tile_log2);
+    s_def = std::min<int64_t>(std::max<int64_t>(s_def, 2), s_max);
     p.S = (o && o->sample_tiles > 0) ? o->sample_tiles : (int)s_def;
     if (p.S > ix->n_tiles) p.S = ix->n_tiles;
     p.cap = (o && o->cand_cap > 0) ? o->cand_cap : kDefaultCandCap;
@@ -1182,10 +1114,6 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.rcap = kRescoreCap;
     p.unroll = (o && o->unroll > 0) ? o->unroll : 8;
     p.tiles_per_wg = (o && o->tiles_per_wg > 0) ? o->tiles_per_wg : 0;
-    int w = dense_waves(ix->tile_log2, 4);
-    if (o && (o->waves == 4 || o->waves == 2 || o->waves == 1) && o->waves < w) w = o->waves;
-    p.waves = w;
-    const int64_t TILE = 1ll << ix->tile_log2;
     p.scale = ar.take<float>(B);
     p.mfix = ar.take<uint32_t>(B);
     p.tau = ar.take<uint32_t>(B);
@@ -1193,7 +1121,6 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.maxbin = ar.take<uint32_t>(B);
     p.resc_cnt = ar.take<uint32_t>(B);
     p.hist = ar.take<uint32_t>((size_t)B * GS_HIST_BINS);
-    p.sample = ar.take<uint32_t>((size_t)B * p.S * TILE);
     p.cand_doc = ar.take<uint32_t>((size_t)B * p.cap);
     p.cand_key = ar.take<uint32_t>((size_t)B * p.cap);
     p.resc_doc = ar.take<uint32_t>((size_t)B * p.rcap);
@@ -1233,7 +1160,6 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         gs_set_error("search workspace too small: need %zu bytes, got %zu", ar.used, ws_bytes);
         return GS_ENOSPC;
     }
-    const int64_t TILE = 1ll << ix->tile_log2;
     // optional per-phase events: start, query prep, threshold seed, scoring,
     // candidate selection, fp64 rescoring, final sort
     auto phase = [&](int i) -> int {
@@ -1261,70 +1187,60 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     }
     if ((rc = phase(1))) return rc;
 
-    // 1. dense fixed-point sample of tiles [0, S), then the seed threshold
-    DenseArgs a = dense_args(ix, qt, qw, T);
-    a.scale = p.scale;
-    a.R = B;
-    a.tile_begin = 0;
-    a.tiles = p.S;
-    a.dense = p.sample;
-    a.dense_ld = (int64_t)p.S * TILE;
-    a.dense_col0 = 0;
-    rc = launch_dense<WT, kDenseFixed>(a, p.waves, s);
-    if (rc) return rc;
-    int64_t sample_cols = (int64_t)p.S * TILE;
-    if (sample_cols > ix->n_docs) sample_cols = ix->n_docs;
-    k_seed<<<B, 1024, 0, s>>>(p.sample, (int64_t)p.S * TILE, sample_cols, k, p.mfix, p.tau, p.cnt, p.maxbin, p.hist,
-                              p.cand_doc, p.cand_key, p.cap);
+    // 1. the first S tiles with tau = 0 (every positive doc is a candidate), then
+    //    tau from the histogram of those candidates; 2. the remaining tiles.
+    //    Both are the fused scorer: one workgroup per (run of consecutive tiles,
+    //    query group) over the group's union of terms.
+    UnionArgs e{};
+    e.doc = ix->doc_ids_d;
+    e.w = ix->weights_d;
+    e.offsets = ix->offsets_d;
+    e.tb = ix->tile_bounds_d;
+    e.n_docs = ix->n_docs;
+    e.V = ix->vocab;
+    e.tile_log2 = ix->tile_log2;
+    e.n_tiles = ix->n_tiles;
+    e.B = B;
+    e.G = p.G;
+    e.n_groups = p.n_groups;
+    e.ecap = p.ecap;
+    e.u_term = p.u_term;
+    e.u_ebeg = p.u_ebeg;
+    e.u_count = p.u_count;
+    e.e_slot = p.e_slot;
+    e.e_w = p.e_w;
+    // default one tile per workgroup: the workgroups of one tile then run at the
+    // same time on one XCD and share its postings in that XCD's L2 (walking
+    // several tiles per workgroup saves per-tile set-up but the groups drift
+    // apart, and the scorer's HBM fetch grows from ~1.3x to ~8x the index at C3)
+    e.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : 1;
+    e.tau = p.tau;
+    e.cnt = p.cnt;
+    e.maxbin = p.maxbin;
+    e.hist = p.hist;
+    e.cand_doc = p.cand_doc;
+    e.cand_key = p.cand_key;
+    e.mfix = p.mfix;
+    e.cap = p.cap;
+    e.k = k;
+    auto run_union = [&](int tile_begin, int tiles) -> int {
+        e.tile_begin = tile_begin;
+        e.tiles = tiles;
+        switch (p.unroll) {
+            case 1: return launch_union<WT, 1>(e, s);
+            case 2: return launch_union<WT, 2>(e, s);
+            case 4: return launch_union<WT, 4>(e, s);
+            case 16: return launch_union<WT, 16>(e, s);
+            default: return launch_union<WT, 8>(e, s);
+        }
+    };
+    if ((rc = run_union(0, p.S))) return rc;
+    k_tau_seed<<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(p.tau, p.maxbin, p.hist, B, k);
     GS_CHECK_LAUNCH();
     if ((rc = phase(2))) return rc;
-
-    // 2. fused scoring + emission over the remaining tiles: one workgroup per
-    //    (run of consecutive tiles, query group) over the group's union of terms
     if (ix->n_tiles > p.S) {
-        UnionArgs e{};
-        e.doc = ix->doc_ids_d;
-        e.w = ix->weights_d;
-        e.offsets = ix->offsets_d;
-        e.tb = ix->tile_bounds_d;
-        e.n_docs = ix->n_docs;
-        e.V = ix->vocab;
-        e.tile_log2 = ix->tile_log2;
-        e.n_tiles = ix->n_tiles;
-        e.B = B;
-        e.G = p.G;
-        e.n_groups = p.n_groups;
-        e.ecap = p.ecap;
-        e.u_term = p.u_term;
-        e.u_ebeg = p.u_ebeg;
-        e.u_count = p.u_count;
-        e.e_slot = p.e_slot;
-        e.e_w = p.e_w;
-        e.tile_begin = p.S;
-        e.tiles = ix->n_tiles - p.S;
-        // default one tile per workgroup: the workgroups of one tile then run at
-        // the same time on one XCD and share its postings in that XCD's L2 (walking
-        // several tiles per workgroup saves per-tile set-up but the groups drift
-        // apart, and the scorer's HBM fetch grows from ~1.3x to ~8x the index at C3)
-        e.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : 1;
-        e.tau = p.tau;
-        e.cnt = p.cnt;
-        e.maxbin = p.maxbin;
-        e.hist = p.hist;
-        e.cand_doc = p.cand_doc;
-        e.cand_key = p.cand_key;
-        e.mfix = p.mfix;
-        e.cap = p.cap;
-        e.k = k;
         if (o && o->ev_score_begin) GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_score_begin), s));
-        switch (p.unroll) {
-            case 1: rc = launch_union<WT, 1>(e, s); break;
-            case 2: rc = launch_union<WT, 2>(e, s); break;
-            case 4: rc = launch_union<WT, 4>(e, s); break;
-            case 16: rc = launch_union<WT, 16>(e, s); break;
-            default: rc = launch_union<WT, 8>(e, s); break;
-        }
-        if (rc) return rc;
+        if ((rc = run_union(p.S, ix->n_tiles - p.S))) return rc;
         if (o && o->ev_score_end) GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_score_end), s));
     }
     if ((rc = phase(3))) return rc;
@@ -1385,7 +1301,7 @@ int search_dense_impl(const gs_index *ix, const int32_t *qt, const void *qw, int
             a.qt = qt + (int64_t)r0 * T;
             a.qw = reinterpret_cast<const char *>(qw) + (int64_t)r0 * T * (WT == GS_W_U8 ? 1 : 4);
         }
-        int rc = launch_dense<WT, kDenseExact>(a, waves, s);
+        int rc = launch_dense<WT>(a, waves, s);
         if (rc) return rc;
         k_select_dense<WT><<<n, kSelThreads, 0, s>>>(ws, ld, ix->n_docs, k, rows, r0, out_scores, out_ids);
         GS_CHECK_LAUNCH();

@@ -68,11 +68,12 @@ typedef struct gs_index {
 
 /* Tuning knobs of gs_search; zero selects the default. */
 typedef struct gs_search_opts {
-    int32_t sample_tiles;  /* doc tiles scored densely to seed the k-th-score threshold
-                              (default: ceil(16 k / tile docs) clamped to [4, 16]) */
+    int32_t sample_tiles;  /* doc tiles scored first with tau = 0 (all their positive docs become
+                              candidates) to seed the k-th-score threshold (default: about 4 k
+                              docs, at least 2 tiles, at most 32 Ki docs) */
     int32_t cand_cap;      /* candidates kept per query before the dense fallback (default 65536) */
     int32_t unroll;        /* postings per lane per chunk of the fused scorer: 1, 2, 4, 8 or 16 (default 8) */
-    int32_t waves;         /* waves per workgroup of the dense sample scorer: 1, 2 or 4 (default: fill 128 KiB) */
+    int32_t waves;         /* reserved, ignored */
     void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
     void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
     int32_t tiles_per_wg;  /* consecutive doc tiles walked by one scoring workgroup, 1..64 (default 1) */
