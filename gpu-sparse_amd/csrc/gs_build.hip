@@ -298,22 +298,37 @@ __global__ void __launch_bounds__(1024) k_len_scan(const int32_t *lengths, int32
 
 // The postings of the term-major index without padding, in list order: key =
 // doc id (n_docs for ids outside [0, n_docs), which then sort after every row),
-// payload = term id and weight bits.  One wave per list.
+// payload = term id and weight bits.  Each wave takes a segment of 64 * kFlatRounds
+// consecutive flattened postings, whatever the list lengths: lane 0 finds the
+// segment's first term by binary search over the exclusive scan `excl`, then
+// every lane walks forward to the term of its posting.
+constexpr int kFlatRounds = 16;
 __global__ void k_flatten(const int32_t *__restrict__ doc_ids, const void *__restrict__ w, int w_bytes,
-                          const int64_t *__restrict__ offsets, const int32_t *__restrict__ lengths, int32_t V,
-                          int64_t n_docs, const int64_t *__restrict__ excl, uint32_t *__restrict__ key,
+                          const int64_t *__restrict__ offsets, int32_t V, int64_t n_docs,
+                          const int64_t *__restrict__ excl, int64_t nnz, uint32_t *__restrict__ key,
                           uint32_t *__restrict__ term, uint32_t *__restrict__ code) {
     const int lane = gs_lane();
     const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
     const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
-    for (int64_t t = wave; t < V; t += nwaves) {
-        const int64_t off = offsets[t], dst = excl[t];
-        const int len = lengths[t];
-        for (int i = lane; i < len; i += 64) {
-            const int32_t d = doc_ids[off + i];
-            key[dst + i] = (d >= 0 && d < n_docs) ? (uint32_t)d : (uint32_t)n_docs;
-            term[dst + i] = (uint32_t)t;
-            code[dst + i] = load_code(w, off + i, w_bytes);
+    constexpr int64_t SEG = 64 * kFlatRounds;
+    for (int64_t s0 = wave * SEG; s0 < nnz; s0 += nwaves * SEG) {
+        // last t with excl[t] <= s0 (excl is non-decreasing, excl[0] = 0, excl[V] = nnz > s0)
+        int lo = 0, hi = V;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (excl[mid] <= s0) lo = mid;
+            else hi = mid;
+        }
+        int t = lo;
+        for (int r = 0; r < kFlatRounds; ++r) {
+            const int64_t i = s0 + r * 64 + lane;
+            if (i >= nnz) break;
+            while (excl[t + 1] <= i) ++t;  // t < V: excl[V] = nnz > i
+            const int64_t src = offsets[t] + (i - excl[t]);
+            const int32_t d = doc_ids[src];
+            key[i] = (d >= 0 && d < n_docs) ? (uint32_t)d : (uint32_t)n_docs;
+            term[i] = (uint32_t)t;
+            code[i] = load_code(w, src, w_bytes);
         }
     }
 }
@@ -789,8 +804,8 @@ extern "C" int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, 
     GS_CHECK_LAUNCH();
     int cur = 0;
     if (nnz > 0) {
-        k_flatten<<<gs_blocks((int64_t)vocab * 64, 256, 65536), 256, 0, s>>>(
-            doc_ids_d, weights_d, w_bytes, offsets_d, lengths_d, vocab, n_docs, l.excl, l.kb[0], l.tb[0], l.cb[0]);
+        k_flatten<<<gs_blocks((nnz + 63) / 64 * 64 / kFlatRounds + 64, 256, 65536), 256, 0, s>>>(
+            doc_ids_d, weights_d, w_bytes, offsets_d, vocab, n_docs, l.excl, nnz, l.kb[0], l.tb[0], l.cb[0]);
         GS_CHECK_LAUNCH();
         // stable LSD radix sort by doc id: rows come out with ascending terms, and
         // the entries of a repeated (doc, term) pair keep their list order
