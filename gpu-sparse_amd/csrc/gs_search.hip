@@ -1174,7 +1174,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     k_fill<uint32_t><<<gs_blocks((int64_t)B * GS_HIST_BINS, 256, 4096), 256, 0, s>>>(
         p.hist, (int64_t)B * GS_HIST_BINS, 0u);
     GS_CHECK_LAUNCH();
-    if (ix->n_tiles > p.S) {  // per group of G queries: the union of their terms
+    {  // per group of G queries: the union of their terms (every search runs the fused scorer)
         static std::atomic<bool> attr{false};
         if (!attr.load()) {
             GS_CHECK_HIP(hipFuncSetAttribute((const void *)k_group_terms<WT>,

@@ -193,6 +193,22 @@ def test_search_small_sample_and_single_tile(c1):
     assert_search_equal(ix, ref, ti[:16], tw[:16], 30, path="fused", sample_tiles=1)
 
 
+@pytest.mark.parametrize("n_docs,tile_log2", [(3000, 12), (700, 8), (9000, 12)])
+def test_search_few_tiles_with_dirty_workspace(device, n_docs, tile_log2):
+    """Collections of 1-3 tiles (all of them in the tau = 0 seed launch) give the
+    oracle's answer whatever the workspace held before the call."""
+    rng = np.random.default_rng(n_docs)
+    csr = random_csr(rng, n_docs, 90, dup_rate=0.05)
+    ix = gs.build_index(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = random_queries(rng, 20, 90, max_len=8)
+    assert_search_equal(ix, ref, ti, tw, 7, path="fused", tile_log2=tile_log2)
+    ix.aux()["workspace"].fill_(0xAB)
+    print(f"few tiles n_docs={n_docs} tile_log2={tile_log2}, dirty workspace", flush=True)
+    for k in (7, min(300, n_docs)):
+        assert_search_equal(ix, ref, ti, tw, k, path="fused", tile_log2=tile_log2)
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, np.uint8])
 def test_search_edge_cases(device, dtype):
     """Empty queries, invalid term ids, duplicate list entries, k = N (zero-score
