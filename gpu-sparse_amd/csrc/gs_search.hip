@@ -43,6 +43,7 @@ namespace {
 using namespace gs;
 
 constexpr int kRescoreCap = 16384;   // candidates rescored per query before the dense fallback
+constexpr int64_t kSeedMinDocs = 8192;    // fewest docs of the default first tiles scored with tau = 0
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
 constexpr size_t kTileLds = 128 * 1024;  // LDS of the score slices of one scoring workgroup
@@ -1101,12 +1102,13 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.n_groups = (B + G - 1) / G;
     p.ecap = G * T;
     p.gt_np = np_of(G);
-    // default first tiles scored with tau = 0: about 4 k docs, at least 2 tiles
+    // default first tiles scored with tau = 0: about 4 k docs, at least 8 Ki docs
     // and at most 32 Ki docs (all of their positive docs become candidates)
     const int64_t TILE = 1ll << ix->tile_log2;
+    const int64_t s_min = std::max<int64_t>(1, kSeedMinDocs >> ix->tile_log2);
+    const int64_t s_max = std::max<int64_t>(s_min, kSeedDocs >> ix->tile_log2);
     int64_t s_def = (4ll * k + TILE - 1) >> ix->tile_log2;
-    const int64_t s_max = std::max<int64_t>(2, kSeedDocs >> ix->tile_log2);
-    s_def = std::min<int64_t>(std::max<int64_t>(s_def, 2), s_max);
+    s_def = std::min<int64_t>(std::max<int64_t>(s_def, s_min), s_max);
     p.S = (o && o->sample_tiles > 0) ? o->sample_tiles : (int)s_def;
     if (p.S > ix->n_tiles) p.S = ix->n_tiles;
     p.cap = (o && o->cand_cap > 0) ? o->cand_cap : kDefaultCandCap;

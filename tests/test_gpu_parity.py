@@ -193,7 +193,7 @@ def test_search_small_sample_and_single_tile(c1):
     assert_search_equal(ix, ref, ti[:16], tw[:16], 30, path="fused", sample_tiles=1)
 
 
-@pytest.mark.parametrize("n_docs,tile_log2", [(3000, 12), (700, 8), (9000, 12)])
+@pytest.mark.parametrize("n_docs,tile_log2", [(3000, 12), (700, 8), (9000, 12), (9000, 13), (20000, 13)])
 def test_search_few_tiles_with_dirty_workspace(device, n_docs, tile_log2):
     """Collections of 1-3 tiles (all of them in the tau = 0 seed launch) give the
     oracle's answer whatever the workspace held before the call."""
@@ -252,7 +252,7 @@ def test_search_u8_config_reduced(device):
     assert_search_equal(ix, ref, ti, tw, 1000, path="fused")
 
 
-@pytest.mark.parametrize("tile_log2,tiles_per_wg", [(8, 0), (10, 0), (12, 0), (10, 4)])
+@pytest.mark.parametrize("tile_log2,tiles_per_wg", [(8, 0), (10, 0), (12, 0), (13, 0), (10, 4), (13, 2)])
 def test_search_head_heavy_reduced(device, tile_log2, tiles_per_wg):
     """Wide head-heavy queries: group unions above one LDS batch of terms."""
     cfg = synth.scaled(synth.CONFIGS["C4"], n_docs=200_000, n_queries=32)
