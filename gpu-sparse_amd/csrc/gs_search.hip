@@ -48,6 +48,7 @@ constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tile
 constexpr int kDefaultCandCap = 65536;
 constexpr size_t kTileLds = 128 * 1024;  // LDS of the score slices of one scoring workgroup
 constexpr int kGroupSortCap = 8192;      // term entries of one query group sorted in LDS
+static_assert(kGroupSortCap < (1 << 15), "union terms pack (entry count << 16 | first entry) into int32");
 // dynamic-LDS cap requested per kernel: 160 KiB per workgroup minus room for static LDS
 constexpr int kMaxDynLds = 152 * 1024;
 
@@ -250,9 +251,10 @@ __global__ void __launch_bounds__(512) k_score_dense(const DenseArgs a) {
 
 // Queries are processed in groups of G.  Per group, the (term, query slot,
 // weight) entries of its valid query terms are sorted by (term, slot, position)
-// so that each distinct term u owns the contiguous entry range
-// [u_ebeg[u], u_ebeg[u + 1]).  Entry weights are stored pre-scaled (q * 2^e_q
-// as fp32 bits for float weights, the uint8 weight for impacts).
+// so that each distinct term owns a contiguous entry range; u_term / u_ebeg list
+// the distinct terms (see the reordering at the end) with u_ebeg = entry count
+// << 16 | first entry.  Entry weights are stored pre-scaled (q * 2^e_q as fp32
+// bits for float weights, the uint8 weight for impacts).
 template <int WT>
 __global__ void __launch_bounds__(256)
     k_group_terms(const int32_t *__restrict__ qt, const void *__restrict__ qw, const float *__restrict__ scale,
@@ -352,6 +354,41 @@ __global__ void __launch_bounds__(256)
         u_count[grp] = carry;
         u_ebeg[(int64_t)grp * (ecap + 1) + carry] = s_tot;
     }
+    __syncthreads();
+    // Reorder the union terms by entry count, descending (ties by term id), and
+    // store each as (count << 16 | first entry).  The scorer hands chunks to its
+    // waves round-robin in this order, so the last chunks of a tile are the
+    // cheapest ones and the waves reach the closing barrier close together.
+    int32_t *ut = u_term + (int64_t)grp * ecap;
+    int32_t *ue = u_ebeg + (int64_t)grp * (ecap + 1);
+    const int U = carry;
+    for (int i = threadIdx.x; i < np; i += blockDim.x)
+        key[i] = i < U ? ((uint64_t)(uint32_t)(kGroupSortCap - (ue[i + 1] - ue[i])) << 32) | (uint32_t)i : ~0ull;
+    __syncthreads();
+    for (int size = 2; size <= np; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < np / 2; i += blockDim.x) {
+                const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const uint64_t ka = key[lo], kb = key[hi];
+                if ((ka > kb) == up) {
+                    key[lo] = kb;
+                    key[hi] = ka;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = threadIdx.x; i < U; i += blockDim.x) {
+        const int u = (int)(uint32_t)key[i];
+        const int m = kGroupSortCap - (int)(key[i] >> 32);
+        key[i] = ((uint64_t)(uint32_t)ut[u] << 32) | (uint32_t)((m << 16) | ue[u]);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < U; i += blockDim.x) {
+        ut[i] = (int32_t)(key[i] >> 32);
+        ue[i] = (int32_t)(uint32_t)key[i];
+    }
 }
 
 // ---------------------------------------------------------------------- group-tile scoring
@@ -415,7 +452,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     int64_t *s_start = reinterpret_cast<int64_t *>(lds_raw + ((size_t)a.G << slice_shift));
     int32_t *s_len = reinterpret_cast<int32_t *>(s_start + kUnionBatch);
     int32_t *s_cst = s_len + kUnionBatch;    // [kUnionBatch + 1], s_cst[nb] = total chunks
-    int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch + 1], first entry of each term
+    int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch + 1], (entry count << 16 | first entry) per term
     int64_t *s_toff = reinterpret_cast<int64_t *>(s_e + kUnionBatch + 2);  // [kUnionBatch] list offsets
     int32_t *s_tid = reinterpret_cast<int32_t *>(s_toff + kUnionBatch);    // [kUnionBatch] term ids
 
@@ -437,7 +474,6 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         s_tid[tid] = t;
         s_toff[tid] = a.offsets[t];
         s_e[tid] = uebeg[tid];
-        if (tid == U - 1) s_e[U] = uebeg[U];
         my_lo = a.tb[(int64_t)t * row + tile_lo];
         my_hi = a.tb[(int64_t)t * row + tile_lo + 1];
     }
@@ -478,7 +514,6 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 hi = bt[1];
                 s_start[tid] = a.offsets[t] + lo;
                 s_e[tid] = uebeg[b0 + tid];
-                if (tid == nb - 1) s_e[nb] = uebeg[b0 + nb];
             }
             s_len[tid] = hi - lo;
             nch = (hi - lo + CH - 1) / CH;
@@ -523,6 +558,21 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
             int32_t doc[UNROLL];
             store_t wv[UNROLL];
         };
+        // Waves of a SIMD are served oldest first, so with equal shares the
+        // youngest wave of each SIMD would finish last.  A wave instead lowers
+        // its issue priority as its share of the chunks completes (3 for the
+        // first quarter, then 2, 1, 0): waves that are behind are served first.
+        const int my_total = (total - wave + NW - 1) / NW;  // chunks of this wave in the batch
+        int level = 0;
+        __builtin_amdgcn_s_setprio(3);
+        auto progress = [&](int done) {
+            const int lv = (4 * done) / max(my_total, 1);
+            if (lv == level) return;
+            level = lv;
+            if (lv == 1) __builtin_amdgcn_s_setprio(2);
+            else if (lv == 2) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+        };
         for (int cb = wave; cb < total; cb += 64 * NW) {
             const int nmine = min(64, (total - cb + NW - 1) / NW);  // chunks of this wave in the block
             int64_t md_p0 = 0;
@@ -539,8 +589,8 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                     const int ci = c - s_cst[lo];
                     md_p0 = s_start[lo] + (int64_t)ci * CH;
                     md_n = min(CH, s_len[lo] - ci * CH);
-                    md_e0 = s_e[lo];
-                    md_m = s_e[lo + 1] - md_e0;
+                    md_e0 = s_e[lo] & 0xFFFF;
+                    md_m = s_e[lo] >> 16;
                 }
             }
             auto fetch = [&](int j, Chunk &k) {
@@ -612,18 +662,22 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
             // static).
             Chunk ka, kb;
             const int last = nmine - 1;
+            const int done0 = (cb - wave) / NW;  // chunks this wave applied in earlier blocks
             int j = 0;
             fetch(0, ka);
             while (true) {
                 fetch(min(j + 1, last), kb);
+                progress(done0 + j);
                 apply(ka, j);
                 if (++j > last) break;
                 fetch(min(j + 1, last), ka);
+                progress(done0 + j);
                 apply(kb, j);
                 if (++j > last) break;
             }
         }
     }
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
 
     // ---- emission of candidates >= tau - margin.  The slices are scanned in
