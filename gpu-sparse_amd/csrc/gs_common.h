@@ -154,12 +154,26 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gs_rsrc(const void *base, uint
 __device__ __forceinline__ uint32_t gs_bload32(__amdgpu_buffer_rsrc_t r, int off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
+__device__ __forceinline__ uint2 gs_bload64(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint2(v[0], v[1]);
+}
 
 // Histogram bin of a positive score: bits of its fp32 value >> 20 (exponent and
 // three mantissa bits, ~9% wide bins), 2048 bins cover every positive float.
 constexpr int GS_HIST_BINS = 2048;
 __device__ __forceinline__ uint32_t gs_bin_of(float v) { return __float_as_uint(v) >> 20; }
 __device__ __forceinline__ float gs_bin_edge(uint32_t b) { return __uint_as_float(b << 20); }
+
+// Orders LDS accesses among the lanes of one wave.  The LDS executes a wave's
+// instructions in order, but without a fence the compiler may move or forward
+// an access across the exchange point (it assumes no other lane writes what
+// this lane reads), so lanes that pass data through LDS call this in between.
+__device__ __forceinline__ void gs_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // Wave-wide inclusive prefix sum of 32-bit values (lane order).
 __device__ __forceinline__ uint32_t gs_wave_incl_scan(uint32_t v) {

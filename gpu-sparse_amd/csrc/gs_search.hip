@@ -46,6 +46,7 @@ constexpr int kRescoreCap = 16384;   // candidates rescored per query before the
 constexpr int64_t kSeedMinDocs = 8192;    // fewest docs of the default first tiles scored with tau = 0
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
+constexpr int64_t kPairMinWgs = 32768;    // scoring workgroups (~128 per CU) above which a workgroup scores two tiles
 constexpr size_t kTileLds = 128 * 1024;  // LDS of the score slices of one scoring workgroup
 constexpr int kGroupSortCap = 8192;      // term entries of one query group sorted in LDS
 static_assert(kGroupSortCap < (1 << 15), "union terms pack (entry count << 16 | first entry) into int32");
@@ -259,8 +260,7 @@ template <int WT>
 __global__ void __launch_bounds__(256)
     k_group_terms(const int32_t *__restrict__ qt, const void *__restrict__ qw, const float *__restrict__ scale,
                   int32_t B, int32_t T, int32_t V, int32_t G, int32_t ecap, int32_t *__restrict__ u_term,
-                  int32_t *__restrict__ u_ebeg, int32_t *__restrict__ u_count, int32_t *__restrict__ e_slot,
-                  uint32_t *__restrict__ e_w) {
+                  int32_t *__restrict__ u_ebeg, int32_t *__restrict__ u_count, uint2 *__restrict__ e_sw) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     __shared__ int32_t s_sh[17];
     __shared__ int32_t s_tot;
@@ -336,8 +336,7 @@ __global__ void __launch_bounds__(256)
         const int tot = s_sh[16];
         __syncthreads();
         if (valid) {
-            e_slot[(int64_t)grp * ecap + i] = (int32_t)((kk >> 20) & 0xFFFu);
-            e_w[(int64_t)grp * ecap + i] = wv[i];
+            e_sw[(int64_t)grp * ecap + i] = make_uint2((uint32_t)((kk >> 20) & 0xFFFu), wv[i]);
             if (head) {
                 u_term[(int64_t)grp * ecap + ex] = (int32_t)(kk >> 32);
                 u_ebeg[(int64_t)grp * (ecap + 1) + ex] = i;
@@ -401,8 +400,8 @@ struct UnionArgs {
     int64_t n_docs;
     int32_t V, tile_log2, n_tiles;
     int32_t B, G, n_groups, ecap;
-    const int32_t *u_term, *u_ebeg, *u_count, *e_slot;
-    const uint32_t *e_w;
+    const int32_t *u_term, *u_ebeg, *u_count;
+    const uint2 *e_sw;  // (query slot, scaled query weight) per entry
     int32_t tile_begin, tiles, tiles_per_wg, per_xcd;
     uint32_t *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key;
     const uint32_t *mfix;
@@ -452,16 +451,15 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     int64_t *s_start = reinterpret_cast<int64_t *>(lds_raw + ((size_t)a.G << slice_shift));
     int32_t *s_len = reinterpret_cast<int32_t *>(s_start + kUnionBatch);
     int32_t *s_cst = s_len + kUnionBatch;    // [kUnionBatch + 1], s_cst[nb] = total chunks
-    int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch + 1], (entry count << 16 | first entry) per term
-    int64_t *s_toff = reinterpret_cast<int64_t *>(s_e + kUnionBatch + 2);  // [kUnionBatch] list offsets
+    int32_t *s_e = s_cst + kUnionBatch + 1;  // [kUnionBatch], (entry count << 16 | first entry) per term
+    int64_t *s_toff = reinterpret_cast<int64_t *>(s_e + kUnionBatch + 3);  // [kUnionBatch] list offsets (8-aligned)
     int32_t *s_tid = reinterpret_cast<int32_t *>(s_toff + kUnionBatch);    // [kUnionBatch] term ids
 
     const int64_t row = (int64_t)a.n_tiles + 1;
     const int U = a.u_count[grp];
     const int32_t *uterm = a.u_term + (int64_t)grp * a.ecap;
     const int32_t *uebeg = a.u_ebeg + (int64_t)grp * (a.ecap + 1);
-    const int32_t *eslot = a.e_slot + (int64_t)grp * a.ecap;
-    const uint32_t *ew = a.e_w + (int64_t)grp * a.ecap;
+    const uint2 *esw = a.e_sw + (int64_t)grp * a.ecap;
     const store_t *wall = reinterpret_cast<const store_t *>(a.w);
 
     // A group whose union fits one batch describes its terms in LDS once (term
@@ -553,7 +551,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         // group) and lanes past the chunk's end read 0.
         struct Chunk {
             int n, m;
-            int slot;      // lane j: slot of the term's j-th entry
+            uint32_t badj; // lane j: LDS byte offset of the j-th entry's slice, minus doc0 * 4
             uint32_t my_w; // lane j: its scaled query weight
             int32_t doc[UNROLL];
             store_t wv[UNROLL];
@@ -593,16 +591,18 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                     md_m = s_e[lo] >> 16;
                 }
             }
+            // byte address of doc d in the slice at LDS offset `base`: (d << 2) +
+            // base - (doc0 << 2), in wrapping 32-bit arithmetic (one v_add per add)
+            const uint32_t doc0_4 = (uint32_t)doc0 << 2;
             auto fetch = [&](int j, Chunk &k) {
                 const int64_t p0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(md_p0 >> 32), j) << 32) |
                                              (uint32_t)__builtin_amdgcn_readlane((int)md_p0, j));
                 k.n = __builtin_amdgcn_readlane(md_n, j);
                 k.m = __builtin_amdgcn_readlane(md_m, j);
                 const int e0 = __builtin_amdgcn_readlane(md_e0, j);
-                const auto re = gs_rsrc(eslot + e0, (uint32_t)k.m * 4u);
-                const auto rq = gs_rsrc(ew + e0, (uint32_t)k.m * 4u);
-                k.slot = (int)gs_bload32(re, lane * 4);
-                k.my_w = gs_bload32(rq, lane * 4);
+                const uint2 sw = gs_bload64(gs_rsrc(esw + e0, (uint32_t)k.m * 8u), lane * 8);
+                k.badj = (sw.x << slice_shift) - doc0_4;
+                k.my_w = sw.y;
                 // The resources start at p0 rounded down to 64 postings; the lane
                 // offset carries the remainder.  It changes per chunk, so it is
                 // computed here and the per-group constants fold into the loads'
@@ -618,13 +618,9 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                     k.wv[u] = W::bload(rw, o_w + u * 64 * (int)sizeof(store_t));
                 }
             };
-            // byte address of doc d in the slice at LDS offset `base`: (d << 2) +
-            // base - (doc0 << 2), in wrapping 32-bit arithmetic (one v_lshl_add)
-            const uint32_t doc0_4 = (uint32_t)doc0 << 2;
             // the first NG 64-posting groups of a chunk, added to one query slot
-            auto add_groups = [&](const Chunk &k, auto ngc, int slot, uint32_t wb) {
+            auto add_groups = [&](const Chunk &k, auto ngc, uint32_t badj, uint32_t wb) {
                 constexpr int NG = decltype(ngc)::value;
-                const uint32_t badj = ((uint32_t)slot << slice_shift) - doc0_4;
 #pragma unroll
                 for (int u = 0; u < NG; ++u)
                     lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
@@ -634,26 +630,32 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
             // resolved once per chunk, so the entry loop is straight-line adds
             auto add_entries = [&](const Chunk &k, auto ngc) {
                 for (int e = 0; e < k.m; ++e)
-                    add_groups(k, ngc, __builtin_amdgcn_readlane(k.slot, e), __builtin_amdgcn_readlane(k.my_w, e));
+                    add_groups(k, ngc, (uint32_t)__builtin_amdgcn_readlane((int)k.badj, e),
+                               (uint32_t)__builtin_amdgcn_readlane((int)k.my_w, e));
             };
             auto apply = [&](Chunk &k, int j) {
                 if (k.m > 64) {  // a term held by more than 64 query slots (queries repeating terms)
                     if (k.n < CH)
 #pragma unroll
-                        for (int u = 0; u < UNROLL; ++u) k.doc[u] = max(k.doc[u], (int32_t)doc0);
+                        for (int u = 0; u < UNROLL; ++u)
+                            k.doc[u] = u * 64 + lane < k.n ? k.doc[u] : (int32_t)doc0 + lane;
                     const int e0 = __builtin_amdgcn_readlane(md_e0, j);
                     for (int e = e0; e < e0 + k.m; ++e)
-                        add_groups(k, std::integral_constant<int, UNROLL>{}, eslot[e], ew[e]);
+                        add_groups(k, std::integral_constant<int, UNROLL>{}, (esw[e].x << slice_shift) - doc0_4,
+                                   esw[e].y);
                     return;
                 }
                 if (k.n == CH) {
                     add_entries(k, std::integral_constant<int, UNROLL>{});
                     return;
                 }
-                // last chunk of a term: lanes past its end read doc 0 and weight 0,
-                // moved into the tile; only the 64-posting groups holding postings run
+                // last chunk of a term: lanes past its end read weight 0 and are sent
+                // to doc doc0 + lane, a word of their own (one shared word would
+                // serialise their atomics); only the 64-posting groups holding
+                // postings run
 #pragma unroll
-                for (int u = 0; u < UNROLL; ++u) k.doc[u] = max(k.doc[u], (int32_t)doc0);
+                for (int u = 0; u < UNROLL; ++u)
+                    k.doc[u] = u * 64 + lane < k.n ? k.doc[u] : (int32_t)doc0 + lane;
                 gs_dispatch_upto<UNROLL>((k.n + 63) >> 6, [&](auto ngc) { add_entries(k, ngc); });
             };
             // two chunk buffers in rotation: the loads of the wave's next chunk are
@@ -968,9 +970,7 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
         const bool staged = n <= kRowStage;
         if (staged) {
             for (int e = lane; e < n; e += 64) row[e] = fterm[r0 + e];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            gs_wave_sync();
         }
         auto term_at = [&](int64_t e) { return staged ? row[e] : fterm[r0 + e]; };
         double s = 0.0;
@@ -1013,7 +1013,7 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
             }
         }
         if (lane == 0) resc_key[(int64_t)q * resc_cap + i] = gs_key_f64(s);
-        __builtin_amdgcn_wave_barrier();  // the row stage is reused by the next candidate
+        gs_wave_sync();  // the row stage is reused by the next candidate
     }
 }
 
@@ -1116,8 +1116,8 @@ int launch_union(UnionArgs e, hipStream_t s) {
 
 struct SearchPlan {
     int S, cap, rcap, unroll, G, n_groups, ecap, gt_np, tiles_per_wg;
-    int32_t *u_term, *u_ebeg, *u_count, *e_slot;
-    uint32_t *e_w;
+    int32_t *u_term, *u_ebeg, *u_count;
+    uint2 *e_sw;
     float *scale;
     uint32_t *mfix, *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key, *resc_doc, *resc_cnt;
     uint64_t *resc_key;
@@ -1184,8 +1184,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.u_term = ar.take<int32_t>((size_t)p.n_groups * p.ecap);
     p.u_ebeg = ar.take<int32_t>((size_t)p.n_groups * (p.ecap + 1));
     p.u_count = ar.take<int32_t>((size_t)p.n_groups);
-    p.e_slot = ar.take<int32_t>((size_t)p.n_groups * p.ecap);
-    p.e_w = ar.take<uint32_t>((size_t)p.n_groups * p.ecap);
+    p.e_sw = ar.take<uint2>((size_t)p.n_groups * p.ecap);
     return p;
 }
 
@@ -1238,7 +1237,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
             attr.store(true);
         }
         k_group_terms<WT><<<p.n_groups, 256, (size_t)p.gt_np * 12, s>>>(
-            qt, qw, p.scale, B, T, ix->vocab, p.G, p.ecap, p.u_term, p.u_ebeg, p.u_count, p.e_slot, p.e_w);
+            qt, qw, p.scale, B, T, ix->vocab, p.G, p.ecap, p.u_term, p.u_ebeg, p.u_count, p.e_sw);
         GS_CHECK_LAUNCH();
     }
     if ((rc = phase(1))) return rc;
@@ -1263,13 +1262,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     e.u_term = p.u_term;
     e.u_ebeg = p.u_ebeg;
     e.u_count = p.u_count;
-    e.e_slot = p.e_slot;
-    e.e_w = p.e_w;
-    // default one tile per workgroup: the workgroups of one tile then run at the
-    // same time on one XCD and share its postings in that XCD's L2 (walking
-    // several tiles per workgroup saves per-tile set-up but the groups drift
-    // apart, and the scorer's HBM fetch grows from ~1.3x to ~8x the index at C3)
-    e.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : 1;
+    e.e_sw = p.e_sw;
     e.tau = p.tau;
     e.cnt = p.cnt;
     e.maxbin = p.maxbin;
@@ -1282,6 +1275,15 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     auto run_union = [&](int tile_begin, int tiles) -> int {
         e.tile_begin = tile_begin;
         e.tiles = tiles;
+        // Default: two tiles per workgroup when that still leaves kPairMinWgs
+        // workgroups, else one.  The second tile saves a workgroup launch and the
+        // term set-up (its bounds are loaded while the first is scored); with few
+        // workgroups the last, partly filled round of workgroups costs more.  The
+        // workgroups of one tile run at the same time on one XCD and share its
+        // postings in that XCD's L2; with many tiles per workgroup the groups
+        // drift apart and the HBM fetch grows (~8x the index at 8 tiles).
+        e.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg
+                                            : ((int64_t)((tiles + 1) / 2) * p.n_groups >= kPairMinWgs ? 2 : 1);
         switch (p.unroll) {
             case 1: return launch_union<WT, 1>(e, s);
             case 2: return launch_union<WT, 2>(e, s);

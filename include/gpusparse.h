@@ -76,7 +76,8 @@ typedef struct gs_search_opts {
     int32_t waves;         /* reserved, ignored */
     void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
     void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
-    int32_t tiles_per_wg;  /* consecutive doc tiles walked by one scoring workgroup, 1..64 (default 1) */
+    int32_t tiles_per_wg;  /* consecutive doc tiles walked by one scoring workgroup, 1..64 (default 2
+                              when that leaves at least 32768 workgroups, else 1) */
     void **ev_phases;      /* optional array of GS_SEARCH_PHASES hipEvent_t (entries may be NULL)
                               recorded on `stream` at the phase boundaries of gs_search: start,
                               query prep, threshold seed, scoring, candidate selection, fp64
@@ -163,9 +164,9 @@ int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wty
  *   out_scores_d float32 [B][k] (int32 for GS_W_U8), out_ids_d int64 [B][k]
  *   status_d    int32 [B]: GS_ROW_DONE, or GS_ROW_DENSE when the row has to be
  *               recomputed with gs_search_dense (its outputs are then undefined).
- * Float indexes accumulate fp32 in LDS doc tiles and rescore the selected
- * candidates in fp64 in query-term order, so scores equal the fp64 scatter-add
- * rounded to fp32.  1 <= k <= min(n_docs, 8192). */
+ * Float indexes accumulate fixed-point int32 in LDS doc tiles and rescore the
+ * selected candidates in fp64 in query-term order, so scores equal the fp64
+ * scatter-add rounded to fp32.  1 <= k <= min(n_docs, 8192). */
 int gs_search_workspace(const gs_index *index, int32_t B, int32_t T, int32_t k,
                         const gs_search_opts *opts, size_t *bytes);
 int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d, int32_t B,

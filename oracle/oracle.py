@@ -13,6 +13,7 @@ products, exhaustive sorting, closed forms):
   build_index            pinned: dict-of-lists builder + layout invariants
   chunk_bounds           pinned: linear scan per list + partition invariant
   forward_index          pinned: the CSR rows sorted stably by column
+  tile_bounds            pinned: linear scan per list
   scores_f64 / _u32      pinned: dense Q @ D^T (float64 / int64) on small inputs
   scores_f32_sequential  pinned: scalar float32 loop of gpu_scoring.py:246-251
   topk                   pinned: Python sorted() with the same key
@@ -91,6 +92,20 @@ def forward_index(index: dict):
     row_ptr = np.zeros(N + 1, dtype=np.int64)
     np.cumsum(np.bincount(docs, minlength=N), out=row_ptr[1:])
     return row_ptr, terms[order].astype(np.int32), w[order]
+
+
+def tile_bounds(index: dict, tile_log2: int) -> np.ndarray:
+    """[V][n_tiles + 1] list-relative first posting of each doc tile: the
+    per-(term, chunk) sub-ranges of src/triton_kernel_chunked.py:110-121 at
+    tile granularity (np.searchsorted 'left' of the tile edges)."""
+    V, N = index["vocab_size"], index["num_docs"]
+    n_tiles = (N + (1 << tile_log2) - 1) >> tile_log2
+    edges = np.arange(n_tiles + 1, dtype=np.int64) << tile_log2
+    out = np.zeros((V, n_tiles + 1), dtype=np.int32)
+    for t in range(V):
+        o, n = int(index["offsets"][t]), int(index["lengths"][t])
+        out[t] = np.searchsorted(index["doc_ids"][o:o + n], edges, side="left")
+    return out
 
 
 def chunk_bounds(doc_ids, offsets, lengths, vocab: int, n_docs: int, doc_chunk: int) -> np.ndarray:

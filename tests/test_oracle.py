@@ -88,6 +88,22 @@ def test_forward_index_is_the_csr_sorted_by_column(seed, dtype, dup):
         assert w[b:e].tobytes() == csr.data[order].tobytes()
 
 
+@pytest.mark.parametrize("tile_log2", [4, 8, 11])
+def test_tile_bounds_match_linear_scan(tile_log2):
+    rng = np.random.default_rng(tile_log2)
+    csr = random_csr(rng, 2500, 20, dup_rate=0.1)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 2500, 20)
+    tb = O.tile_bounds(ix, tile_log2)
+    n_tiles = (2500 + (1 << tile_log2) - 1) >> tile_log2
+    assert tb.shape == (20, n_tiles + 1)
+    for t in range(20):
+        o, n = int(ix["offsets"][t]), int(ix["lengths"][t])
+        seg = ix["doc_ids"][o:o + n].tolist()
+        for j in range(n_tiles + 1):
+            edge = j << tile_log2
+            assert tb[t, j] == next((i for i, d in enumerate(seg) if d >= edge), n)
+
+
 @pytest.mark.parametrize("chunk", [1, 3, 17, 64, 1000])
 def test_chunk_bounds_match_linear_scan(chunk):
     rng = np.random.default_rng(chunk)
