@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--n-docs", type=int, default=None, help="override the config's collection size")
     ap.add_argument("--batch", type=int, default=0, help="queries per batch (0: the config's)")
     ap.add_argument("--k", type=int, default=0, help="top-k (0: the config's)")
-    ap.add_argument("--tile-log2", type=int, default=13)
+    ap.add_argument("--tile-log2", type=int, default=12)
     ap.add_argument("--unroll", type=int, default=0, help="postings per lane per chunk (0: library default)")
     ap.add_argument("--waves", type=int, default=0)
     ap.add_argument("--tiles-per-wg", type=int, default=0, help="tiles walked by one scoring workgroup (0: default)")

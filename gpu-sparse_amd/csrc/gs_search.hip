@@ -46,7 +46,7 @@ constexpr int kRescoreCap = 16384;   // candidates rescored per query before the
 constexpr int64_t kSeedMinDocs = 8192;    // fewest docs of the default first tiles scored with tau = 0
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
-constexpr int64_t kPairMinWgs = 32768;    // scoring workgroups (~128 per CU) above which a workgroup scores two tiles
+constexpr int64_t kPairMinWgs = 12288;    // paired workgroups (~48 per CU) needed before a workgroup scores two tiles
 constexpr size_t kTileLds = 128 * 1024;  // LDS of the score slices of one scoring workgroup
 constexpr int kGroupSortCap = 8192;      // term entries of one query group sorted in LDS
 static_assert(kGroupSortCap < (1 << 15), "union terms pack (entry count << 16 | first entry) into int32");

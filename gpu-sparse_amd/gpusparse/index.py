@@ -24,7 +24,7 @@ from . import _lib
 
 BLOCK_SIZE = 32          # posting lists are padded to a multiple of this (gpu_inverted_index.py:18)
 VOCAB_SIZE = 30522       # fixed vocabulary of the harness builder (run_correctness_verification.py:28)
-DEFAULT_TILE_LOG2 = 13   # 8192 docs per LDS tile
+DEFAULT_TILE_LOG2 = 12   # 4096 docs per LDS tile
 
 
 class CSR(NamedTuple):
