@@ -77,24 +77,38 @@ __global__ void k_query_prep(const int32_t *__restrict__ qt, const void *__restr
                              int32_t V, const float *__restrict__ max_abs, const int32_t *__restrict__ dup,
                              float *__restrict__ scale, uint32_t *__restrict__ mfix, uint32_t *__restrict__ tau,
                              uint32_t *__restrict__ cnt, uint32_t *__restrict__ maxbin) {
-    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    // one wave per query; the lanes sum over its terms
+    const int q = (int)((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6);
+    const int lane = gs_lane();
     if (q >= B) return;
-    tau[q] = 0;
-    cnt[q] = 0;
-    maxbin[q] = 0;
+    if (lane == 0) {
+        tau[q] = 0;
+        cnt[q] = 0;
+        maxbin[q] = 0;
+    }
     if (WT == GS_W_U8) {
-        scale[q] = 1.0f;
-        mfix[q] = 0;
+        if (lane == 0) {
+            scale[q] = 1.0f;
+            mfix[q] = 0;
+        }
         return;
     }
+    // M and n as fp64 sums in any order: the factor (1 + 1e-12) below covers the
+    // rounding of a sum of up to 8192 non-negative terms
     double M = 0.0, n = 0.0;
-    for (int j = 0; j < T; ++j) {
+    for (int j = lane; j < T; j += 64) {
         const int32_t t = qt[(int64_t)q * T + j];
         if ((uint32_t)t >= (uint32_t)V) continue;
         const double m = 1.0 + (double)dup[t];
         M += fabs((double)reinterpret_cast<const float *>(qw)[(int64_t)q * T + j]) * (double)max_abs[t] * m;
         n += m;
     }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        M += __shfl_xor(M, d, 64);
+        n += __shfl_xor(n, d, 64);
+    }
+    if (lane != 0) return;
     M *= 1.0 + 1e-12;  // fp64 rounding of the sum itself
     int e = 30;
     if (M > 0.0) {
@@ -941,11 +955,14 @@ __global__ void __launch_bounds__(256)
 }
 
 // The same exact fp64 score from the doc-major copy.  The wave copies the
-// candidate's row of term ids (a few hundred bytes, one coalesced load) into
-// LDS, and lane j binary-searches query term j there instead of in term j's
-// posting list; rows longer than the LDS stage are searched in place.  Rows
-// hold a doc's postings with ascending terms and repeated (doc, term) entries in
-// list order, so products and duplicates are added in the same order as above.
+// candidate's row (term ids and weights: one coalesced load each) into LDS, and
+// lane j binary-searches query term j there instead of in term j's posting list;
+// rows longer than the LDS stage are searched in place.  The row of the wave's
+// next candidate is loaded into registers while the current one is searched,
+// and each lane of a batch of 64 candidates looks up one candidate's row bounds.
+// Rows hold a doc's postings with ascending terms and repeated (doc, term)
+// entries in list order, so products and duplicates are added in the same order
+// as above.
 constexpr int kRescoreWaves = 4;
 constexpr int kRowStage = 512;  // row entries staged in LDS per wave
 
@@ -956,64 +973,99 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
                   const float *__restrict__ qw, int32_t T, const uint32_t *__restrict__ resc_doc,
                   const uint32_t *__restrict__ resc_cnt, int32_t resc_cap, uint64_t *__restrict__ resc_key) {
     using store_t = typename gs_weight<WT>::store_t;
+    constexpr int RU = kRowStage / 64;
     __shared__ int32_t s_row[kRescoreWaves][kRowStage];
+    __shared__ store_t s_rw[kRescoreWaves][kRowStage];
     const int q = blockIdx.y;
     const uint32_t m = resc_cnt[q];
     const int lane = gs_lane();
     const int w = threadIdx.x >> 6;
     int32_t *row = s_row[w];
+    store_t *roww = s_rw[w];
     const store_t *wall = reinterpret_cast<const store_t *>(fw);
-    for (uint32_t i = blockIdx.x * kRescoreWaves + w; i < m; i += gridDim.x * kRescoreWaves) {
-        const int32_t d = (int32_t)resc_doc[(int64_t)q * resc_cap + i];
-        const int64_t r0 = row_ptr[d], r1 = row_ptr[d + 1];
-        const int n = (int)(r1 - r0);
-        const bool staged = n <= kRowStage;
-        if (staged) {
-            for (int e = lane; e < n; e += 64) row[e] = fterm[r0 + e];
-            gs_wave_sync();
+    const uint32_t stride = gridDim.x * kRescoreWaves;
+    // this wave's candidates: first + c * stride, c = 0, 1, ...
+    for (uint32_t first = blockIdx.x * kRescoreWaves + w; first < m; first += 64 * stride) {
+        const int nc = (int)min<uint32_t>(64u, (m - first + stride - 1) / stride);
+        int64_t c_r0 = 0;
+        int c_n = 0;
+        if (lane < nc) {
+            const int32_t d = (int32_t)resc_doc[(int64_t)q * resc_cap + first + (uint32_t)lane * stride];
+            c_r0 = row_ptr[d];
+            c_n = (int)(row_ptr[d + 1] - c_r0);
         }
-        auto term_at = [&](int64_t e) { return staged ? row[e] : fterm[r0 + e]; };
-        double s = 0.0;
-        for (int j0 = 0; j0 < T; j0 += 64) {
-            const int j = j0 + lane;
-            int cnt_p = 0;    // entries of term j in the row (> 1 only for duplicates)
-            int64_t pos = 0;  // the first of them, in the doc-major arrays
-            double wq = 0.0;
-            if (j < T) {
-                const int32_t t = qt[(int64_t)q * T + j];
-                if ((uint32_t)t < (uint32_t)V) {
-                    int lo = 0, len = n;
-                    while (len > 0) {
-                        const int half = len >> 1;
-                        if (term_at(lo + half) < t) {
-                            lo += half + 1;
-                            len -= half + 1;
-                        } else {
-                            len = half;
-                        }
+        int32_t rt[RU];
+        store_t rv[RU];
+        auto fetch = [&](int c) {
+            const int64_t r0 = gs_readlane_i64(c_r0, c);
+            const int n = __builtin_amdgcn_readlane(c_n, c);
+            if (n > kRowStage) return;
+#pragma unroll
+            for (int u = 0; u < RU; ++u) {
+                const int e = u * 64 + lane;
+                rt[u] = e < n ? fterm[r0 + e] : 0;
+                rv[u] = e < n ? wall[r0 + e] : store_t(0);
+            }
+        };
+        fetch(0);
+        for (int c = 0; c < nc; ++c) {
+            const int64_t r0 = gs_readlane_i64(c_r0, c);
+            const int n = __builtin_amdgcn_readlane(c_n, c);
+            const bool staged = n <= kRowStage;
+            if (staged) {
+#pragma unroll
+                for (int u = 0; u < RU; ++u) {
+                    if (u * 64 < n) {
+                        row[u * 64 + lane] = rt[u];
+                        roww[u * 64 + lane] = rv[u];
                     }
-                    while (lo + cnt_p < n && term_at(lo + cnt_p) == t) ++cnt_p;
-                    pos = r0 + lo;
-                    wq = (double)qw[(int64_t)q * T + j];
+                }
+                gs_wave_sync();
+            }
+            if (c + 1 < nc) fetch(c + 1);
+            auto term_at = [&](int64_t e) { return staged ? row[e] : fterm[r0 + e]; };
+            auto weight_at = [&](int64_t e) { return staged ? roww[e] : wall[r0 + e]; };
+            double s = 0.0;
+            for (int j0 = 0; j0 < T; j0 += 64) {
+                const int j = j0 + lane;
+                int cnt_p = 0;  // entries of term j in the row (> 1 only for duplicates)
+                int lo = 0;     // the first of them, within the row
+                double wq = 0.0;
+                if (j < T) {
+                    const int32_t t = qt[(int64_t)q * T + j];
+                    if ((uint32_t)t < (uint32_t)V) {
+                        int len = n;
+                        while (len > 0) {
+                            const int half = len >> 1;
+                            if (term_at(lo + half) < t) {
+                                lo += half + 1;
+                                len -= half + 1;
+                            } else {
+                                len = half;
+                            }
+                        }
+                        while (lo + cnt_p < n && term_at(lo + cnt_p) == t) ++cnt_p;
+                        wq = (double)qw[(int64_t)q * T + j];
+                    }
+                }
+                const double p = cnt_p ? wq * (double)gs_weight<WT>::decode(weight_at(lo)) : 0.0;
+                uint64_t hit = __ballot(cnt_p > 0);
+                const uint64_t dup = __ballot(cnt_p > 1);
+                while (hit) {
+                    const int l = __ffsll((unsigned long long)hit) - 1;
+                    hit &= hit - 1;
+                    s += gs_readlane_f64(p, l);
+                    if ((dup >> l) & 1ull) {
+                        const int cl = __builtin_amdgcn_readlane(cnt_p, l);
+                        const double wl = gs_readlane_f64(wq, l);
+                        const int ll = __builtin_amdgcn_readlane(lo, l);
+                        for (int r = 1; r < cl; ++r) s += wl * (double)gs_weight<WT>::decode(weight_at(ll + r));
+                    }
                 }
             }
-            const double p = cnt_p ? wq * (double)gs_weight<WT>::decode(wall[pos]) : 0.0;
-            uint64_t hit = __ballot(cnt_p > 0);
-            const uint64_t dup = __ballot(cnt_p > 1);
-            while (hit) {
-                const int l = __ffsll((unsigned long long)hit) - 1;
-                hit &= hit - 1;
-                s += gs_readlane_f64(p, l);
-                if ((dup >> l) & 1ull) {
-                    const int cl = __builtin_amdgcn_readlane(cnt_p, l);
-                    const double wl = gs_readlane_f64(wq, l);
-                    const int64_t pl = gs_readlane_i64(pos, l);
-                    for (int r = 1; r < cl; ++r) s += wl * (double)gs_weight<WT>::decode(wall[pl + r]);
-                }
-            }
+            if (lane == 0) resc_key[(int64_t)q * resc_cap + first + (uint32_t)c * stride] = gs_key_f64(s);
+            gs_wave_sync();  // the row stage is reused by the next candidate
         }
-        if (lane == 0) resc_key[(int64_t)q * resc_cap + i] = gs_key_f64(s);
-        gs_wave_sync();  // the row stage is reused by the next candidate
     }
 }
 
@@ -1224,7 +1276,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     };
     int rc = phase(0);
     if (rc) return rc;
-    k_query_prep<WT><<<gs_blocks(B, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d, ix->dup_d, p.scale,
+    k_query_prep<WT><<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d, ix->dup_d, p.scale,
                                                       p.mfix, p.tau, p.cnt, p.maxbin);
     k_fill<uint32_t><<<gs_blocks((int64_t)B * GS_HIST_BINS, 256, 4096), 256, 0, s>>>(
         p.hist, (int64_t)B * GS_HIST_BINS, 0u);
