@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--unroll", type=int, default=0, help="postings per lane per chunk (0: library default)")
     ap.add_argument("--waves", type=int, default=0)
     ap.add_argument("--tiles-per-wg", type=int, default=0, help="tiles walked by one scoring workgroup (0: default)")
+    ap.add_argument("--sample-tiles", type=int, default=0, help="tiles scored with tau = 0 first (0: default)")
     ap.add_argument("--cpu-queries-1", type=int, default=96, help="queries timed on one core")
     ap.add_argument("--cpu-queries-all", type=int, default=512, help="queries timed on all cores")
     ap.add_argument("--cpu-cores", type=int, default=16, help="cap on the cores of the all-core row")
@@ -225,7 +226,7 @@ def main():
         if a.path == "atomic":
             return gs.atomic_fused_score(index, qt, qw, k)
         return gs.search(index, (qt, qw), k, tile_log2=a.tile_log2, path=a.path, unroll=a.unroll,
-                         waves=a.waves, tiles_per_wg=a.tiles_per_wg, timing=timing)
+                         waves=a.waves, tiles_per_wg=a.tiles_per_wg, sample_tiles=a.sample_tiles, timing=timing)
 
     for _ in range(a.warmup):
         step()

@@ -54,7 +54,8 @@ __global__ void __launch_bounds__(kSelThreads)
                        const int32_t *__restrict__ cidx, const float *__restrict__ cval,
                        const int32_t *__restrict__ counts, int32_t max_cand, int32_t k, float *__restrict__ out_v,
                        int64_t *__restrict__ out_i) {
-    __shared__ SelShared sh;
+    __shared__ SelStatic sst;
+    SelShared sh = sel_view(sst, k);
     const int b = blockIdx.x;
     const int32_t cnt = counts ? counts[b] : (int32_t)0x7FFFFFFF;
     if (tau && cnt <= max_cand) {
@@ -151,7 +152,8 @@ extern "C" int gs_compacted_topk(const float *scores_d, int64_t ld, int32_t B, i
         k_fill<int32_t><<<gs_blocks(B, 256), 256, 0, s>>>(counts_d, B, (int32_t)L);
     }
     GS_CHECK_LAUNCH();
-    k_select_compacted<<<B, kSelThreads, 0, s>>>(scores_d, ld, L, tau_d, cidx, cval, tau_d ? counts_d : nullptr,
+    GS_CHECK_HIP(sel_attr((const void *)k_select_compacted, sel_lds_bytes(k)));
+    k_select_compacted<<<B, kSelThreads, sel_lds_bytes(k), s>>>(scores_d, ld, L, tau_d, cidx, cval, tau_d ? counts_d : nullptr,
                                                  max_cand, k, out_values_d, out_idx_d);
     GS_CHECK_LAUNCH();
     return GS_OK;

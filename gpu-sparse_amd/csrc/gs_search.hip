@@ -43,7 +43,7 @@ namespace {
 using namespace gs;
 
 constexpr int kRescoreCap = 16384;   // candidates rescored per query before the dense fallback
-constexpr int64_t kSeedMinDocs = 8192;    // fewest docs of the default first tiles scored with tau = 0
+constexpr int64_t kSeedMinDocs = 4096;    // fewest docs of the default first tiles scored with tau = 0
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
 constexpr int64_t kPairMinWgs = 12288;    // paired workgroups (~48 per CU) needed before a workgroup scores two tiles
@@ -828,7 +828,8 @@ __global__ void __launch_bounds__(kSelThreads)
                    uint32_t *__restrict__ resc_doc, uint32_t *__restrict__ resc_cnt, int32_t resc_cap,
                    void *__restrict__ out_scores, int64_t *__restrict__ out_ids, int32_t *__restrict__ status) {
     constexpr bool FP = WT != GS_W_U8;
-    __shared__ SelShared sh;
+    __shared__ SelStatic sst;
+    SelShared sh = sel_view(sst, k);
     __shared__ uint32_t s_m;
     const int q = blockIdx.x;
     const uint32_t n = cnt[q];
@@ -1075,7 +1076,8 @@ __global__ void __launch_bounds__(kSelThreads)
                    const uint32_t *__restrict__ resc_cnt, int32_t resc_cap, int32_t k,
                    const int32_t *__restrict__ status, float *__restrict__ out_scores,
                    int64_t *__restrict__ out_ids) {
-    __shared__ SelShared sh;
+    __shared__ SelStatic sst;
+    SelShared sh = sel_view(sst, k);
     const int q = blockIdx.x;
     if (status[q] != GS_ROW_DONE) return;
     SrcCand64 src{resc_key + (int64_t)q * resc_cap, resc_doc + (int64_t)q * resc_cap, (int64_t)resc_cnt[q]};
@@ -1092,7 +1094,8 @@ __global__ void __launch_bounds__(kSelThreads)
     k_select_dense(const void *__restrict__ dense, int64_t ld, int64_t n_docs, int32_t k,
                    const int32_t *__restrict__ rows, int32_t r0, void *__restrict__ out_scores,
                    int64_t *__restrict__ out_ids) {
-    __shared__ SelShared sh;
+    __shared__ SelStatic sst;
+    SelShared sh = sel_view(sst, k);
     const int r = blockIdx.x;
     const int q = rows ? rows[r0 + r] : r0 + r;
     if (WT == GS_W_U8) {
@@ -1208,7 +1211,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.n_groups = (B + G - 1) / G;
     p.ecap = G * T;
     p.gt_np = np_of(G);
-    // default first tiles scored with tau = 0: about 4 k docs, at least 8 Ki docs
+    // default first tiles scored with tau = 0: about 4 k docs, at least 4 Ki docs
     // and at most 32 Ki docs (all of their positive docs become candidates)
     const int64_t TILE = 1ll << ix->tile_log2;
     const int64_t s_min = std::max<int64_t>(1, kSeedMinDocs >> ix->tile_log2);
@@ -1356,7 +1359,9 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     if ((rc = phase(3))) return rc;
 
     // 3. selection (+ fp64 rescoring for float weights)
-    k_select_cands<WT><<<B, kSelThreads, 0, s>>>(p.cand_doc, p.cand_key, p.cnt, p.cap, k, p.mfix, p.resc_doc,
+    const size_t sel_lds = sel_lds_bytes(k);
+    GS_CHECK_HIP(sel_attr((const void *)k_select_cands<WT>, sel_lds));
+    k_select_cands<WT><<<B, kSelThreads, sel_lds, s>>>(p.cand_doc, p.cand_key, p.cnt, p.cap, k, p.mfix, p.resc_doc,
                                                  p.resc_cnt, p.rcap, out_scores, out_ids, status);
     GS_CHECK_LAUNCH();
     if ((rc = phase(4))) return rc;
@@ -1375,7 +1380,8 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     }
     if ((rc = phase(5))) return rc;
     if (FP) {
-        k_select_final<WT><<<B, kSelThreads, 0, s>>>(p.resc_doc, p.resc_key, p.resc_cnt, p.rcap, k, status,
+        GS_CHECK_HIP(sel_attr((const void *)k_select_final<WT>, sel_lds));
+        k_select_final<WT><<<B, kSelThreads, sel_lds, s>>>(p.resc_doc, p.resc_key, p.resc_cnt, p.rcap, k, status,
                                                      reinterpret_cast<float *>(out_scores), out_ids);
         GS_CHECK_LAUNCH();
     }
@@ -1413,7 +1419,9 @@ int search_dense_impl(const gs_index *ix, const int32_t *qt, const void *qw, int
         }
         int rc = launch_dense<WT>(a, waves, s);
         if (rc) return rc;
-        k_select_dense<WT><<<n, kSelThreads, 0, s>>>(ws, ld, ix->n_docs, k, rows, r0, out_scores, out_ids);
+        GS_CHECK_HIP(sel_attr((const void *)k_select_dense<WT>, sel_lds_bytes(k)));
+        k_select_dense<WT><<<n, kSelThreads, sel_lds_bytes(k), s>>>(ws, ld, ix->n_docs, k, rows, r0, out_scores,
+                                                                     out_ids);
         GS_CHECK_LAUNCH();
     }
     return GS_OK;

@@ -70,7 +70,7 @@ typedef struct gs_index {
 typedef struct gs_search_opts {
     int32_t sample_tiles;  /* doc tiles scored first with tau = 0 (all their positive docs become
                               candidates) to seed the k-th-score threshold (default: about 4 k
-                              docs, at least 8 Ki and at most 32 Ki docs) */
+                              docs, at least 4 Ki and at most 32 Ki docs) */
     int32_t cand_cap;      /* candidates kept per query before the dense fallback (default 65536) */
     int32_t unroll;        /* postings per lane per chunk of the fused scorer: 1, 2, 4, 8 or 16 (default 8) */
     int32_t waves;         /* reserved, ignored */
