@@ -47,11 +47,20 @@ constexpr int64_t kSeedMinDocs = 4096;    // fewest docs of the default first ti
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
 constexpr int64_t kPairMinWgs = 12288;    // paired workgroups (~48 per CU) needed before a workgroup scores two tiles
-constexpr size_t kTileLds = 128 * 1024;  // LDS of the score slices of one scoring workgroup
+constexpr size_t kTileLds = 144 * 1024;  // LDS of the score slices of one scoring workgroup (9 x 4096 docs)
 constexpr int kGroupSortCap = 8192;      // term entries of one query group sorted in LDS
 static_assert(kGroupSortCap < (1 << 15), "union terms pack (entry count << 16 | first entry) into int32");
 // dynamic-LDS cap requested per kernel: 160 KiB per workgroup minus room for static LDS
-constexpr int kMaxDynLds = 152 * 1024;
+constexpr size_t kLdsPerWg = 160 * 1024;     // gfx950 LDS of one workgroup (static + dynamic)
+constexpr size_t kStaticLdsBudget = 2048;    // static LDS allowed next to the largest dynamic request
+
+// Lets `fn` take all the LDS of a workgroup: 160 KiB minus its static LDS.
+inline hipError_t allow_full_lds(const void *fn) {
+    hipFuncAttributes at;
+    const hipError_t e = hipFuncGetAttributes(&at, fn);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kLdsPerWg - at.sharedSizeBytes));
+}
 
 
 template <class T>
@@ -271,7 +280,7 @@ __global__ void __launch_bounds__(512) k_score_dense(const DenseArgs a) {
 // << 16 | first entry.  Entry weights are stored pre-scaled (q * 2^e_q as fp32
 // bits for float weights, the uint8 weight for impacts).
 template <int WT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(1024)
     k_group_terms(const int32_t *__restrict__ qt, const void *__restrict__ qw, const float *__restrict__ scale,
                   int32_t B, int32_t T, int32_t V, int32_t G, int32_t ecap, int32_t *__restrict__ u_term,
                   int32_t *__restrict__ u_ebeg, int32_t *__restrict__ u_count, uint2 *__restrict__ e_sw) {
@@ -423,12 +432,13 @@ struct UnionArgs {
 };
 
 constexpr int kUnionThreads = 1024;  // 16 waves
-constexpr int kUnionBatch = 512;     // union terms described in LDS at a time
+constexpr int kUnionBatch = 440;     // union terms described in LDS at a time
 constexpr int kEmitChunks = (int)(kTileLds / 4 / 256);  // 256-doc emission chunks of one workgroup
 
 // LDS bytes of k_score_union besides the G score slices
 constexpr size_t kUnionMetaLds =
     (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 2) * 8 + (size_t)kUnionBatch * 12;
+static_assert(kTileLds + kUnionMetaLds + kStaticLdsBudget <= kLdsPerWg, "scoring workgroup LDS exceeds 160 KiB");
 
 // One workgroup = one doc tile x one query group; the G query slices of the
 // tile live in LDS as int32.  Per batch of union terms, every thread fetches one
@@ -1130,7 +1140,7 @@ int launch_dense_u(DenseArgs a, int waves, size_t acc_bytes, hipStream_t s) {
     auto fn = k_score_dense<WT, UNROLL>;
     const size_t lds = (size_t)waves * (size_t(1) << a.tile_log2) * acc_bytes;
     if (!attr_set.load()) {
-        GS_CHECK_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+        GS_CHECK_HIP(allow_full_lds((const void *)fn));
         attr_set.store(true);
     }
     a.groups = (a.R + waves - 1) / waves;
@@ -1155,7 +1165,7 @@ int launch_union(UnionArgs e, hipStream_t s) {
     static std::atomic<bool> attr{false};
     auto fn = k_score_union<WT, UNROLL>;
     if (!attr.load()) {
-        GS_CHECK_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+        GS_CHECK_HIP(allow_full_lds((const void *)fn));
         attr.store(true);
     }
     const size_t lds = ((size_t)e.G << (e.tile_log2 + 2)) + kUnionMetaLds;
@@ -1287,11 +1297,10 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     {  // per group of G queries: the union of their terms (every search runs the fused scorer)
         static std::atomic<bool> attr{false};
         if (!attr.load()) {
-            GS_CHECK_HIP(hipFuncSetAttribute((const void *)k_group_terms<WT>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds));
+            GS_CHECK_HIP(allow_full_lds((const void *)k_group_terms<WT>));
             attr.store(true);
         }
-        k_group_terms<WT><<<p.n_groups, 256, (size_t)p.gt_np * 12, s>>>(
+        k_group_terms<WT><<<p.n_groups, 1024, (size_t)p.gt_np * 12, s>>>(
             qt, qw, p.scale, B, T, ix->vocab, p.G, p.ecap, p.u_term, p.u_ebeg, p.u_count, p.e_sw);
         GS_CHECK_LAUNCH();
     }
