@@ -506,6 +506,31 @@ __global__ void k_tile_bounds(const int32_t *__restrict__ doc, const int64_t *__
     }
 }
 
+// Packed scoring copy of the postings for one tile size: slot i holds the byte
+// offset of its doc's word in a tile slice, (doc mod tile) * 4 < 2^16, in the
+// low 16 bits and the weight's bits above it (fp16 and uint8 weights: one
+// 32-bit word), or the pair (offset, weight bits) for fp32 weights.  Padding
+// slots (doc < 0) hold 0.
+template <int WT>
+__global__ void k_pack_postings(const int32_t *__restrict__ doc, const void *__restrict__ w, int64_t n,
+                                int32_t tile_log2, void *__restrict__ out) {
+    const uint32_t mask = (1u << tile_log2) - 1u;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t d = doc[i];
+        const bool ok = d >= 0;
+        const uint32_t off = ok ? ((uint32_t)d & mask) << 2 : 0u;
+        if (WT == GS_W_F32) {
+            const uint32_t wb = ok ? reinterpret_cast<const uint32_t *>(w)[i] : 0u;
+            reinterpret_cast<uint2 *>(out)[i] = make_uint2(off, wb);
+        } else {
+            const uint32_t wb = !ok ? 0u
+                                : WT == GS_W_F16 ? (uint32_t) reinterpret_cast<const uint16_t *>(w)[i]
+                                                 : (uint32_t) reinterpret_cast<const uint8_t *>(w)[i];
+            reinterpret_cast<uint32_t *>(out)[i] = off | (wb << 16);
+        }
+    }
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -839,6 +864,24 @@ extern "C" int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, 
             k_unpack_rows<GS_W_U8><<<g, 256, 0, s>>>(l.kb[cur], l.tb[cur], l.cb[cur], nnz, n_docs, row_ptr_d,
                                                      fwd_terms_d, fwd_weights_d);
             break;
+    }
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+extern "C" int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, int64_t n_slots,
+                                int32_t tile_log2, void *out_d, void *stream) {
+    GS_REQUIRE(n_slots >= 0, "n_slots %lld is negative", (long long)n_slots);
+    GS_REQUIRE(tile_log2 >= 6 && tile_log2 <= 14, "tile_log2 %d outside [6, 14]", tile_log2);
+    GS_REQUIRE(wtype >= GS_W_F32 && wtype <= GS_W_U8, "unknown weight type %d", wtype);
+    GS_REQUIRE(n_slots == 0 || (doc_ids_d && weights_d && out_d), "null pointer");
+    if (n_slots == 0) return GS_OK;
+    hipStream_t s = gs_stream(stream);
+    const unsigned g = gs_blocks(n_slots, 256, 1 << 16);
+    switch (wtype) {
+        case GS_W_F32: k_pack_postings<GS_W_F32><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, out_d); break;
+        case GS_W_F16: k_pack_postings<GS_W_F16><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, out_d); break;
+        default: k_pack_postings<GS_W_U8><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, out_d); break;
     }
     GS_CHECK_LAUNCH();
     return GS_OK;

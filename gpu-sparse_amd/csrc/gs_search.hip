@@ -418,6 +418,7 @@ __global__ void __launch_bounds__(1024)
 struct UnionArgs {
     const int32_t *doc;
     const void *w;
+    const void *pk;  // packed scoring copy for this tile size, or null
     const int64_t *offsets;
     const int32_t *tb;  // [V][n_tiles + 1]
     int64_t n_docs;
@@ -447,10 +448,18 @@ static_assert(kTileLds + kUnionMetaLds + kStaticLdsBudget <= kLdsPerWg, "scoring
 // Waves then take chunks round-robin, load each posting once and add its
 // fixed-point contribution to every query slot of the term with ds_add_u32.
 // Afterwards the slices are scanned for candidates.
-template <int WT, int UNROLL>
+// the integer type holding a packed weight's bits (fp16 and uint8 weights)
+template <int WT>
+using pk_half_t = std::conditional_t<WT == GS_W_F16, uint16_t, uint8_t>;
+
+// PK: postings come from the packed scoring copy (gs_pack_postings): one word
+// per posting with the doc's byte offset in a slice and the weight bits (fp32:
+// an offset / weight pair), instead of the doc id and weight arrays.
+template <int WT, int UNROLL, bool PK>
 __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a) {
     using W = gs_weight<WT>;
     using store_t = typename W::store_t;
+    using pk_t = std::conditional_t<WT == GS_W_F32, uint2, uint32_t>;
     constexpr int CH = 64 * UNROLL;
     constexpr int NW = kUnionThreads / 64;
 
@@ -485,6 +494,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     const int32_t *uebeg = a.u_ebeg + (int64_t)grp * (a.ecap + 1);
     const uint2 *esw = a.e_sw + (int64_t)grp * a.ecap;
     const store_t *wall = reinterpret_cast<const store_t *>(a.w);
+    const pk_t *pkd = reinterpret_cast<const pk_t *>(a.pk);
 
     // A group whose union fits one batch describes its terms in LDS once (term
     // id, list offset, entry range); thread `term` holds the term's bounds in the
@@ -616,8 +626,9 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 }
             }
             // byte address of doc d in the slice at LDS offset `base`: (d << 2) +
-            // base - (doc0 << 2), in wrapping 32-bit arithmetic (one v_add per add)
-            const uint32_t doc0_4 = (uint32_t)doc0 << 2;
+            // base - (doc0 << 2), in wrapping 32-bit arithmetic (one v_add per add);
+            // packed postings carry (d - doc0) << 2 already
+            const uint32_t doc0_4 = PK ? 0u : (uint32_t)doc0 << 2;
             auto fetch = [&](int j, Chunk &k) {
                 const int64_t p0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(md_p0 >> 32), j) << 32) |
                                              (uint32_t)__builtin_amdgcn_readlane((int)md_p0, j));
@@ -633,22 +644,46 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 // immediate offsets.
                 const int64_t pb = p0 & ~int64_t(63);
                 const int sh = (int)(p0 - pb);
-                const auto rd = gs_rsrc(a.doc + pb, (uint32_t)(sh + k.n) * 4u);
-                const auto rw = gs_rsrc(wall + pb, (uint32_t)(sh + k.n) * (uint32_t)sizeof(store_t));
-                const int o_doc = (lane + sh) * 4, o_w = (lane + sh) * (int)sizeof(store_t);
+                if constexpr (PK) {
+                    const auto rp = gs_rsrc(pkd + pb, (uint32_t)(sh + k.n) * (uint32_t)sizeof(pk_t));
+                    const int o_p = (lane + sh) * (int)sizeof(pk_t);
 #pragma unroll
-                for (int u = 0; u < UNROLL; ++u) {
-                    k.doc[u] = (int32_t)gs_bload32(rd, o_doc + u * 256);
-                    k.wv[u] = W::bload(rw, o_w + u * 64 * (int)sizeof(store_t));
+                    for (int u = 0; u < UNROLL; ++u) {
+                        if constexpr (WT == GS_W_F32) {
+                            const uint2 v = gs_bload64(rp, o_p + u * 64 * 8);
+                            k.doc[u] = (int32_t)v.x;
+                            k.wv[u] = __uint_as_float(v.y);
+                        } else {
+                            k.doc[u] = (int32_t)gs_bload32(rp, o_p + u * 256);
+                        }
+                    }
+                } else {
+                    const auto rd = gs_rsrc(a.doc + pb, (uint32_t)(sh + k.n) * 4u);
+                    const auto rw = gs_rsrc(wall + pb, (uint32_t)(sh + k.n) * (uint32_t)sizeof(store_t));
+                    const int o_doc = (lane + sh) * 4, o_w = (lane + sh) * (int)sizeof(store_t);
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u) {
+                        k.doc[u] = (int32_t)gs_bload32(rd, o_doc + u * 256);
+                        k.wv[u] = W::bload(rw, o_w + u * 64 * (int)sizeof(store_t));
+                    }
                 }
             };
             // the first NG 64-posting groups of a chunk, added to one query slot
             auto add_groups = [&](const Chunk &k, auto ngc, uint32_t badj, uint32_t wb) {
                 constexpr int NG = decltype(ngc)::value;
 #pragma unroll
-                for (int u = 0; u < NG; ++u)
-                    lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (((uint32_t)k.doc[u] << 2) + badj)),
-                                      fixed_contrib<WT>(wb, k.wv[u]));
+                for (int u = 0; u < NG; ++u) {
+                    const uint32_t d = (uint32_t)k.doc[u];
+                    if constexpr (!PK)
+                        lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + ((d << 2) + badj)),
+                                          fixed_contrib<WT>(wb, k.wv[u]));
+                    else if constexpr (WT == GS_W_F32)
+                        lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (d + badj)),
+                                          fixed_contrib<WT>(wb, k.wv[u]));
+                    else
+                        lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + ((d & 0xFFFFu) + badj)),
+                                          fixed_contrib<WT>(wb, __builtin_bit_cast(store_t, (pk_half_t<WT>)(d >> 16))));
+                }
             };
             // every entry (query slot) of the chunk's term; the group count is
             // resolved once per chunk, so the entry loop is straight-line adds
@@ -662,7 +697,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                     if (k.n < CH)
 #pragma unroll
                         for (int u = 0; u < UNROLL; ++u)
-                            k.doc[u] = u * 64 + lane < k.n ? k.doc[u] : (int32_t)doc0 + lane;
+                            k.doc[u] = u * 64 + lane < k.n ? k.doc[u] : (PK ? lane << 2 : (int32_t)doc0 + lane);
                     const int e0 = __builtin_amdgcn_readlane(md_e0, j);
                     for (int e = e0; e < e0 + k.m; ++e)
                         add_groups(k, std::integral_constant<int, UNROLL>{}, (esw[e].x << slice_shift) - doc0_4,
@@ -675,11 +710,11 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 }
                 // last chunk of a term: lanes past its end read weight 0 and are sent
                 // to doc doc0 + lane, a word of their own (one shared word would
-                // serialise their atomics); only the 64-posting groups holding
-                // postings run
+                // serialise their atomics; a packed lane gets offset lane * 4 and
+                // weight 0); only the 64-posting groups holding postings run
 #pragma unroll
                 for (int u = 0; u < UNROLL; ++u)
-                    k.doc[u] = u * 64 + lane < k.n ? k.doc[u] : (int32_t)doc0 + lane;
+                    k.doc[u] = u * 64 + lane < k.n ? k.doc[u] : (PK ? lane << 2 : (int32_t)doc0 + lane);
                 gs_dispatch_upto<UNROLL>((k.n + 63) >> 6, [&](auto ngc) { add_entries(k, ngc); });
             };
             // two chunk buffers in rotation: the loads of the wave's next chunk are
@@ -1163,9 +1198,10 @@ int launch_dense(DenseArgs a, int waves, hipStream_t s) {
 template <int WT, int UNROLL>
 int launch_union(UnionArgs e, hipStream_t s) {
     static std::atomic<bool> attr{false};
-    auto fn = k_score_union<WT, UNROLL>;
+    auto fn = e.pk ? k_score_union<WT, UNROLL, true> : k_score_union<WT, UNROLL, false>;
     if (!attr.load()) {
-        GS_CHECK_HIP(allow_full_lds((const void *)fn));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, true>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, false>));
         attr.store(true);
     }
     const size_t lds = ((size_t)e.G << (e.tile_log2 + 2)) + kUnionMetaLds;
@@ -1233,7 +1269,10 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.cap = (o && o->cand_cap > 0) ? o->cand_cap : kDefaultCandCap;
     if (p.cap < 2 * k) p.cap = 2 * k;
     p.rcap = kRescoreCap;
-    p.unroll = (o && o->unroll > 0) ? o->unroll : 8;
+    // default postings per lane per chunk: 16 on packed one-word postings (their
+    // registers allow it), else 8
+    const bool packed1 = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2 && ix->wtype != GS_W_F32;
+    p.unroll = (o && o->unroll > 0) ? o->unroll : (packed1 ? 16 : 8);
     p.tiles_per_wg = (o && o->tiles_per_wg > 0) ? o->tiles_per_wg : 0;
     p.scale = ar.take<float>(B);
     p.mfix = ar.take<uint32_t>(B);
@@ -1313,6 +1352,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     UnionArgs e{};
     e.doc = ix->doc_ids_d;
     e.w = ix->weights_d;
+    e.pk = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2 ? ix->packed_d : nullptr;
     e.offsets = ix->offsets_d;
     e.tb = ix->tile_bounds_d;
     e.n_docs = ix->n_docs;

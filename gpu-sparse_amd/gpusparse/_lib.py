@@ -22,7 +22,7 @@ GS_W_F32, GS_W_F16, GS_W_U8 = 0, 1, 2
 GS_ROW_DONE, GS_ROW_DENSE = 0, 1
 GS_SEARCH_PHASES = 7
 PHASE_NAMES = ("query_prep", "threshold_seed", "scoring", "candidate_select", "fp64_rescore", "final_sort")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 WTYPE_OF_DTYPE = {torch.float32: GS_W_F32, torch.float16: GS_W_F16, torch.uint8: GS_W_U8}
 
@@ -47,6 +47,8 @@ class GsIndex(C.Structure):
         ("fwd_ptr_d", C.c_void_p),
         ("fwd_terms_d", C.c_void_p),
         ("fwd_weights_d", C.c_void_p),
+        ("packed_d", C.c_void_p),
+        ("packed_tile_log2", C.c_int32),
     ]
 
 
@@ -104,6 +106,7 @@ SIGNATURES = {
     "gs_tile_bounds": (C.c_int, [_P, _P, _P, _I32, _I64, _I32, _P, _P]),
     "gs_forward_fill_workspace": (_SZ, [_I64, _I32]),
     "gs_forward_fill": (C.c_int, [_P, _P, _I32, _P, _P, _I32, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
+    "gs_pack_postings": (C.c_int, [_P, _P, _I32, _I64, _I32, _P, _P]),
     "gs_search_workspace": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts),
                                       C.POINTER(_SZ)]),
     "gs_search": (C.c_int, [C.POINTER(GsIndex), _P, _P, _I32, _I32, _I32, C.POINTER(GsSearchOpts), _P, _P,

@@ -296,8 +296,11 @@ def build_forward(index):
 
 
 def ensure_search_state(index, tile_log2: int = DEFAULT_TILE_LOG2, forward: bool = True) -> dict:
-    """Derived arrays gs_search needs: max |w|, duplicate counts, tile bounds, and
-    for float weights the doc-major copy used by the exact rescoring (skipped when
+    """Derived arrays gs_search needs: max |w|, duplicate counts, tile bounds, for
+    fp16 and uint8 weights the packed scoring copy for this tile size (skipped when
+    the GPU has no room for it: the scorer then reads the index arrays, with the
+    same results), and for
+    float weights the doc-major copy used by the exact rescoring (skipped when
     `forward` is false or the GPU has no room for it: the rescoring then searches
     the term lists, with the same results)."""
     a = index.aux()
@@ -322,12 +325,37 @@ def ensure_search_state(index, tile_log2: int = DEFAULT_TILE_LOG2, forward: bool
         _lib.check(L.gs_tile_bounds(_lib.ptr(index.doc_ids), _lib.ptr(index.offsets), _lib.ptr(index.lengths), V,
                                     N, tile_log2, _lib.ptr(tb), _lib.stream_ptr(dev)), "gs_tile_bounds")
         a[key] = tb
+    key = ("packed", tile_log2)
+    if key not in a and int(index.doc_ids.numel()) > 0 and index.wtype != _lib.GS_W_F32:
+        # fp16 and uint8 postings pack into one word (4 of 6 or 5 bytes); fp32 ones
+        # would stay 8 bytes, and the scorer is faster on the index arrays there.
+        # One packed copy per index: the one for the tile size last searched.
+        for old in [k for k in a if isinstance(k, tuple) and k[0] == "packed"]:
+            del a[old]
+        try:
+            a[key] = build_packed(index, tile_log2)
+        except torch.cuda.OutOfMemoryError:
+            a[key] = None
     if forward and "fwd" not in a and index.wtype != _lib.GS_W_U8 and int(index.num_docs) > 0:
         try:
             a["fwd"] = build_forward(index)
         except torch.cuda.OutOfMemoryError:
             a["fwd"] = None
     return a
+
+
+def build_packed(index, tile_log2: int) -> torch.Tensor:
+    """Packed scoring copy of the postings for one tile size (gs_pack_postings):
+    per slot the byte offset of its doc in a tile slice (bits 0-15) and the weight
+    bits (bits 16-31) as int32 for fp16 and uint8 weights, or (offset, weight
+    bits) int32 pairs for fp32 weights."""
+    dev = _device_of(index)
+    n = int(index.doc_ids.numel())
+    shape = (n, 2) if index.wtype == _lib.GS_W_F32 else (n,)
+    out = torch.empty(shape, dtype=torch.int32, device=dev)
+    _lib.check(_lib.lib().gs_pack_postings(_lib.ptr(index.doc_ids), _lib.ptr(index.scores), index.wtype, n, tile_log2,
+                                           _lib.ptr(out), _lib.stream_ptr(dev)), "gs_pack_postings")
+    return out
 
 
 def gs_index_struct(index, tile_log2: int = DEFAULT_TILE_LOG2) -> _lib.GsIndex:
@@ -350,6 +378,9 @@ def gs_index_struct(index, tile_log2: int = DEFAULT_TILE_LOG2) -> _lib.GsIndex:
     fwd = a.get("fwd")
     if fwd is not None:
         s.fwd_ptr_d, s.fwd_terms_d, s.fwd_weights_d = (t.data_ptr() for t in fwd)
+    pk = a.get(("packed", tile_log2))
+    if pk is not None:
+        s.packed_d, s.packed_tile_log2 = pk.data_ptr(), tile_log2
     return s
 
 

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 3
+#define GS_ABI_VERSION 4
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -64,6 +64,10 @@ typedef struct gs_index {
     const int32_t *fwd_terms_d;   /* rescoring of float indexes: [n_docs + 1] row offsets, [nnz] */
     const void *fwd_weights_d;    /* term ids ascending within a row, [nnz] weights; NULL: the
                                      rescoring searches the term lists instead */
+    const void *packed_d;         /* optional packed scoring copy (gs_pack_postings) read by the
+                                     fused scorer in place of doc_ids_d / weights_d */
+    int32_t packed_tile_log2;     /* the tile size packed_d was made for; used only when it equals
+                                     tile_log2 */
 } gs_index;
 
 /* Tuning knobs of gs_search; zero selects the default. */
@@ -72,7 +76,8 @@ typedef struct gs_search_opts {
                               candidates) to seed the k-th-score threshold (default: about 4 k
                               docs, at least 4 Ki and at most 32 Ki docs) */
     int32_t cand_cap;      /* candidates kept per query before the dense fallback (default 65536) */
-    int32_t unroll;        /* postings per lane per chunk of the fused scorer: 1, 2, 4, 8 or 16 (default 8) */
+    int32_t unroll;        /* postings per lane per chunk of the fused scorer: 1, 2, 4, 8 or 16 (default
+                              16 with a packed fp16 / uint8 copy, else 8) */
     int32_t waves;         /* reserved, ignored */
     void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
     void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
@@ -153,6 +158,15 @@ int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wty
                     const int32_t *lengths_d, int32_t vocab, int64_t n_docs, int64_t nnz, int64_t *row_ptr_d,
                     int32_t *fwd_terms_d, void *fwd_weights_d, void *workspace_d, size_t workspace_bytes,
                     void *stream);
+
+/* Packed scoring copy of the postings (no counterpart in the reference: a layout
+ * of its posting arrays for the LDS scorer).  Slot i of out_d holds the byte
+ * offset of its doc's word in a tile slice, (doc mod 2^tile_log2) * 4, in bits
+ * 0..15 and the weight's bits in bits 16..31 (GS_W_F16, GS_W_U8: uint32 per slot),
+ * or the pair {offset, fp32 weight bits} (GS_W_F32: 2 x uint32 per slot).  Padding
+ * slots (doc id < 0) hold 0.  tile_log2 <= 14. */
+int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, int64_t n_slots,
+                     int32_t tile_log2, void *out_d, void *stream);
 
 /* ------------------------------------------------------------ search
  * Replaces triton_fused_score (src/triton_kernel.py:159-200) and

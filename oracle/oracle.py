@@ -14,6 +14,7 @@ products, exhaustive sorting, closed forms):
   chunk_bounds           pinned: linear scan per list + partition invariant
   forward_index          pinned: the CSR rows sorted stably by column
   tile_bounds            pinned: linear scan per list
+  pack_postings          pinned: per-slot decoding + a scalar loop
   scores_f64 / _u32      pinned: dense Q @ D^T (float64 / int64) on small inputs
   scores_f32_sequential  pinned: scalar float32 loop of gpu_scoring.py:246-251
   topk                   pinned: Python sorted() with the same key
@@ -106,6 +107,21 @@ def tile_bounds(index: dict, tile_log2: int) -> np.ndarray:
         o, n = int(index["offsets"][t]), int(index["lengths"][t])
         out[t] = np.searchsorted(index["doc_ids"][o:o + n], edges, side="left")
     return out
+
+
+def pack_postings(index: dict, tile_log2: int) -> np.ndarray:
+    """Packed scoring copy (gs_pack_postings; no reference counterpart: a layout of
+    its posting arrays): per slot (doc mod 2^tile_log2) * 4 in bits 0-15 and the
+    weight bits in bits 16-31 (fp16, uint8: int32 [n]), or the pair (offset, fp32
+    bits) (int32 [n, 2]); padding slots (doc < 0) are 0."""
+    doc = index["doc_ids"].astype(np.int64)
+    w = index["scores"]
+    ok = doc >= 0
+    off = np.where(ok, (doc & ((1 << tile_log2) - 1)) << 2, 0).astype(np.uint32)
+    if w.dtype == np.float32:
+        return np.stack([off, np.where(ok, w.view(np.uint32), 0).astype(np.uint32)], axis=1).view(np.int32)
+    bits = (w.view(np.uint16) if w.dtype == np.float16 else w).astype(np.uint32)
+    return (off | (np.where(ok, bits, 0).astype(np.uint32) << 16)).view(np.int32)
 
 
 def chunk_bounds(doc_ids, offsets, lengths, vocab: int, n_docs: int, doc_chunk: int) -> np.ndarray:

@@ -72,6 +72,39 @@ def test_forward_index_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
     assert w.cpu().numpy()[:nnz].tobytes() == want[2].tobytes()
 
 
+@pytest.mark.parametrize("seed,dtype,tile_log2", [(0, np.float32, 12), (1, np.float16, 13), (2, np.uint8, 8),
+                                                 (3, np.float16, 10)])
+def test_packed_copy_matches_oracle(device, seed, dtype, tile_log2):
+    from gpusparse.index import build_packed
+    print(f"packed copy seed={seed} {dtype.__name__} tile_log2={tile_log2}", flush=True)
+    csr = random_csr(np.random.default_rng(seed), 20000, 300, dtype=dtype, dup_rate=0.05)
+    ix = gs.build_index(csr, device)
+    got = build_packed(ix, tile_log2).cpu().numpy()
+    assert np.array_equal(got, O.pack_postings(oracle_index(csr), tile_log2))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.uint8])
+def test_search_without_packed_copy(device, dtype):
+    """The scorer reads the index arrays when the packed copy is absent (fp32
+    weights, or no room for it) and gives the same, oracle, answer."""
+    from gpusparse.index import DEFAULT_TILE_LOG2, ensure_search_state
+    rng = np.random.default_rng(5)
+    csr = random_csr(rng, 30000, 60, max_len=12, dtype=dtype, dup_rate=0.02)
+    ix = gs.build_index(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = random_queries(rng, 24, 60, max_len=9, dtype=np.uint8 if dtype == np.uint8 else np.float32)
+    print(f"packed vs plain scorer {dtype.__name__}", flush=True)
+    assert_search_equal(ix, ref, ti, tw, 300, path="fused")
+    a = ensure_search_state(ix, DEFAULT_TILE_LOG2)
+    if dtype == np.float32:
+        assert a.get(("packed", DEFAULT_TILE_LOG2)) is None
+        return
+    assert a[("packed", DEFAULT_TILE_LOG2)] is not None
+    a[("packed", DEFAULT_TILE_LOG2)] = None
+    assert_search_equal(ix, ref, ti, tw, 300, path="fused")
+    assert_search_equal(ix, ref, ti, tw, 300, path="fused", unroll=8)
+
+
 def test_rescoring_without_forward_copy(c1):
     """The rescoring that searches the term lists (used when the doc-major copy is
     absent) gives the same answer."""

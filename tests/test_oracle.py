@@ -104,6 +104,37 @@ def test_tile_bounds_match_linear_scan(tile_log2):
             assert tb[t, j] == next((i for i, d in enumerate(seg) if d >= edge), n)
 
 
+@pytest.mark.parametrize("tile_log2,dtype", [(12, np.float16), (8, np.uint8), (13, np.float32), (14, np.float16)])
+def test_pack_postings_decodes_and_matches_scalar_loop(tile_log2, dtype):
+    rng = np.random.default_rng(tile_log2)
+    csr = random_csr(rng, 40000, 50, dtype=dtype, dup_rate=0.05)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 40000, 50)
+    pk = O.pack_postings(ix, tile_log2)
+    doc, w = ix["doc_ids"], ix["scores"]
+    mask = (1 << tile_log2) - 1
+    # decoding gives back the doc's place in its tile and the weight, padding is 0
+    if dtype == np.float32:
+        off, wb = pk[:, 0].view(np.uint32), pk[:, 1].view(np.uint32)
+        assert np.array_equal(wb[doc >= 0], w[doc >= 0].view(np.uint32))
+    else:
+        u = pk.view(np.uint32)
+        off, wb = u & 0xFFFF, u >> 16
+        bits = w.view(np.uint16) if dtype == np.float16 else w
+        assert np.array_equal(wb[doc >= 0], bits[doc >= 0].astype(np.uint32))
+    assert np.array_equal(off[doc >= 0] >> 2, doc[doc >= 0] & mask) and not np.any(off[doc >= 0] & 3)
+    assert not np.any(pk.reshape(len(doc), -1)[doc < 0])
+    # scalar loop over the first slots
+    for i in range(0, len(doc), 997):
+        d = int(doc[i])
+        o = ((d % (1 << tile_log2)) * 4) if d >= 0 else 0
+        if dtype == np.float32:
+            exp = (o, int(w[i].view(np.uint32)) if d >= 0 else 0)
+            assert (int(pk[i, 0]) & 0xFFFFFFFF, int(pk[i, 1]) & 0xFFFFFFFF) == exp
+        else:
+            b = int(w[i].view(np.uint16)) if dtype == np.float16 else int(w[i])
+            assert int(pk[i]) & 0xFFFFFFFF == (o + (b << 16) if d >= 0 else 0)
+
+
 @pytest.mark.parametrize("chunk", [1, 3, 17, 64, 1000])
 def test_chunk_bounds_match_linear_scan(chunk):
     rng = np.random.default_rng(chunk)
