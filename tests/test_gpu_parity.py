@@ -273,6 +273,28 @@ def test_search_f16_config_reduced(device):
         assert_search_equal(ix, ref, ti, tw, k, path="fused")
 
 
+@pytest.fixture(scope="module")
+def c3_small(device):
+    cfg = synth.scaled(synth.CONFIGS["C3"], n_docs=120_000, n_queries=24)
+    docs, queries = synth.generate(cfg)
+    ix = gs.build_index(docs, device)
+    ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
+    return ix, oracle_index(docs), ti, tw
+
+
+@pytest.mark.parametrize("unroll,tile_log2,tiles_per_wg", [(1, 12, 1), (2, 10, 3), (4, 13, 2), (8, 12, 2),
+                                                           (16, 12, 1), (16, 9, 4), (16, 13, 0)])
+def test_search_packed_launch_shapes(c3_small, unroll, tile_log2, tiles_per_wg):
+    """fp16 postings read from the packed scoring copy, for every chunk length and
+    several tile sizes and tiles per workgroup."""
+    from gpusparse.index import ensure_search_state
+    ix, ref, ti, tw = c3_small
+    print(f"packed unroll={unroll} tile_log2={tile_log2} tiles_per_wg={tiles_per_wg}", flush=True)
+    assert_search_equal(ix, ref, ti, tw, 100, path="fused", unroll=unroll, tile_log2=tile_log2,
+                        tiles_per_wg=tiles_per_wg)
+    assert ensure_search_state(ix, tile_log2)[("packed", tile_log2)] is not None
+
+
 def test_search_u8_config_reduced(device):
     cfg = synth.scaled(synth.CONFIGS["C5"], n_docs=300_000, n_queries=64)
     docs, queries = synth.generate(cfg)
