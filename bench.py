@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--n-docs", type=int, default=None, help="override the config's collection size")
     ap.add_argument("--batch", type=int, default=0, help="queries per batch (0: the config's)")
     ap.add_argument("--k", type=int, default=0, help="top-k (0: the config's)")
-    ap.add_argument("--tile-log2", type=int, default=12)
+    ap.add_argument("--tile-log2", type=int, default=0, help="doc tile size, log2 (0: the library default)")
     ap.add_argument("--unroll", type=int, default=0, help="postings per lane per chunk (0: library default)")
     ap.add_argument("--waves", type=int, default=0)
     ap.add_argument("--tiles-per-wg", type=int, default=0, help="tiles walked by one scoring workgroup (0: default)")
@@ -174,7 +174,9 @@ def main():
         from gpusparse import synth
         cfg = synth.CONFIGS[a.config]
         n_docs = a.n_docs or cfg.docs.n_rows
-        summarize_traffic(a.summarize_traffic, cfg.name, n_docs, a.tile_log2, a.copy_bytes or (1 << 30))
+        from gpusparse.index import DEFAULT_TILE_LOG2, DEFAULT_TILE_LOG2_PACKED
+        tile = a.tile_log2 or (DEFAULT_TILE_LOG2 if cfg.docs.weights == "f32" else DEFAULT_TILE_LOG2_PACKED)
+        summarize_traffic(a.summarize_traffic, cfg.name, n_docs, tile, a.copy_bytes or (1 << 30))
         return
     if a.copy_bytes:
         copy_only(a.copy_bytes)
@@ -188,7 +190,7 @@ def main():
 
     import gpusparse as gs
     from gpusparse import synth
-    from gpusparse.index import ensure_search_state
+    from gpusparse.index import default_tile_log2, ensure_search_state
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -212,6 +214,8 @@ def main():
     torch.cuda.synchronize()
     t_build = time.perf_counter() - t0
     t0 = time.perf_counter()
+    if not a.tile_log2:
+        a.tile_log2 = default_tile_log2(index)
     ensure_search_state(index, a.tile_log2)
     torch.cuda.synchronize()
     t_bounds = time.perf_counter() - t0
@@ -246,11 +250,15 @@ def main():
     wbytes = index.scores.element_size()
     S = 0
     roof = None
+    plan = None
     if a.path == "fused" and timing.get("score_kernel"):
         kern_ms = [e0.elapsed_time(e1) for e0, e1 in timing["score_kernel"]]
         call_ms = [e0.elapsed_time(e1) for e0, e1 in timing["search"]]
         n_tiles = (index.num_docs + (1 << a.tile_log2) - 1) >> a.tile_log2
-        S = min(16, n_tiles)
+        # the main launch scores the tiles after the seed tiles
+        plan = gs.search_plan(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles, unroll=a.unroll,
+                              tiles_per_wg=a.tiles_per_wg)
+        S = min(plan["seed_tiles"], n_tiles)
         tb = index.aux()[("tile_bounds", a.tile_log2)]
         cols = tb[:, [S, n_tiles]].cpu().numpy().astype(np.int64)
         per_term = cols[:, 1] - cols[:, 0]
@@ -324,7 +332,9 @@ def main():
         "config": {"workload": f"{cfg.name}: {cfg.description}", "n_docs": n_docs,
                    "postings": int(index.lengths.sum().item()), "global_batch": B, "k": k, "max_query_terms": T,
                    "weights": str(index.scores.dtype).replace("torch.", ""), "tile_docs": 1 << a.tile_log2,
-                   "path": a.path},
+                   "path": a.path,
+                   "scorer": None if plan is None else {key: plan[key] for key in
+                                                        ("group_size", "unroll", "tiles_per_wg", "seed_tiles", "packed")}},
         "roofline": roof, "cpu_baseline": cpu, "parity": parity, "components_ms": components,
         "index_build_s": round(t_build, 3), "search_state_s": round(t_bounds, 3), "generate_s": round(t_gen, 1),
         "dense_rows": timing.get("dense_rows", 0),

@@ -1238,6 +1238,11 @@ int check_index(const gs_index *ix) {
     return GS_OK;
 }
 
+// default tiles per scoring workgroup of a launch over `tiles` tiles
+int default_tiles_per_wg(int tiles, int n_groups) {
+    return (int64_t)((tiles + 1) / 2) * n_groups >= kPairMinWgs ? 2 : 1;
+}
+
 SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, const gs_search_opts *o,
                        gs_arena &ar) {
     SearchPlan p;
@@ -1386,8 +1391,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         // workgroups of one tile run at the same time on one XCD and share its
         // postings in that XCD's L2; with many tiles per workgroup the groups
         // drift apart and the HBM fetch grows (~8x the index at 8 tiles).
-        e.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg
-                                            : ((int64_t)((tiles + 1) / 2) * p.n_groups >= kPairMinWgs ? 2 : 1);
+        e.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : default_tiles_per_wg(tiles, p.n_groups);
         switch (p.unroll) {
             case 1: return launch_union<WT, 1>(e, s);
             case 2: return launch_union<WT, 2>(e, s);
@@ -1488,6 +1492,22 @@ extern "C" int gs_search_workspace(const gs_index *index, int32_t B, int32_t T, 
     gs_arena ar{nullptr, 0, 0};
     plan_search(index, B, T, k, opts, ar);
     *bytes = ar.used + 256;
+    return GS_OK;
+}
+
+extern "C" int gs_search_plan(const gs_index *index, int32_t B, int32_t T, int32_t k, const gs_search_opts *opts,
+                              gs_search_plan_info *out) {
+    if (int rc = check_index(index)) return rc;
+    GS_REQUIRE(B > 0 && T > 0 && k > 0 && out, "bad search sizes");
+    GS_REQUIRE((int64_t)T <= kGroupSortCap, "query width T=%d exceeds %d terms", T, kGroupSortCap);
+    gs_arena ar{nullptr, 0, 0};
+    const SearchPlan p = plan_search(index, B, T, k, opts, ar);
+    out->seed_tiles = p.S;
+    out->group_size = p.G;
+    out->unroll = p.unroll;
+    const int rest = index->n_tiles - p.S;
+    out->tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : (rest > 0 ? default_tiles_per_wg(rest, p.n_groups) : 1);
+    out->packed = index->packed_d && index->packed_tile_log2 == index->tile_log2;
     return GS_OK;
 }
 

@@ -93,6 +93,13 @@ _P = C.c_void_p
 _I32, _I64, _SZ = C.c_int32, C.c_int64, C.c_size_t
 
 # name -> (restype, argtypes); the exported C ABI of include/gpusparse.h
+class GsSearchPlanInfo(C.Structure):
+    """Mirror of ``struct gs_search_plan_info`` in include/gpusparse.h."""
+
+    _fields_ = [("seed_tiles", C.c_int32), ("group_size", C.c_int32), ("unroll", C.c_int32),
+                ("tiles_per_wg", C.c_int32), ("packed", C.c_int32)]
+
+
 SIGNATURES = {
     "gs_query_version": (C.c_int, []),
     "gs_last_error": (C.c_char_p, []),
@@ -109,6 +116,8 @@ SIGNATURES = {
     "gs_pack_postings": (C.c_int, [_P, _P, _I32, _I64, _I32, _P, _P]),
     "gs_search_workspace": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts),
                                       C.POINTER(_SZ)]),
+    "gs_search_plan": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts),
+                                 C.POINTER(GsSearchPlanInfo)]),
     "gs_search": (C.c_int, [C.POINTER(GsIndex), _P, _P, _I32, _I32, _I32, C.POINTER(GsSearchOpts), _P, _P,
                             _P, _P, _SZ, _P]),
     "gs_search_dense_workspace": (C.c_int, [C.POINTER(GsIndex), _I32, C.POINTER(_SZ)]),

@@ -24,7 +24,15 @@ from . import _lib
 
 BLOCK_SIZE = 32          # posting lists are padded to a multiple of this (gpu_inverted_index.py:18)
 VOCAB_SIZE = 30522       # fixed vocabulary of the harness builder (run_correctness_verification.py:28)
-DEFAULT_TILE_LOG2 = 12   # 4096 docs per LDS tile
+DEFAULT_TILE_LOG2 = 12          # 4096 docs per LDS tile: fp32 postings, read from the index arrays
+DEFAULT_TILE_LOG2_PACKED = 13   # 8192 docs per LDS tile: fp16 / uint8 postings, read from the packed copy
+
+
+def default_tile_log2(index) -> int:
+    """Doc-tile size (log2) used when a search names none: 8192 docs for fp16 and
+    uint8 postings (the scorer reads one packed word per posting and its per-tile
+    set-up weighs more than the 9-query groups of smaller tiles save), 4096 for fp32."""
+    return DEFAULT_TILE_LOG2_PACKED if index.scores.dtype in (torch.float16, torch.uint8) else DEFAULT_TILE_LOG2
 
 
 class CSR(NamedTuple):
@@ -295,7 +303,7 @@ def build_forward(index):
     return row_ptr, terms, w
 
 
-def ensure_search_state(index, tile_log2: int = DEFAULT_TILE_LOG2, forward: bool = True) -> dict:
+def ensure_search_state(index, tile_log2: int | None = None, forward: bool = True) -> dict:
     """Derived arrays gs_search needs: max |w|, duplicate counts, tile bounds, for
     fp16 and uint8 weights the packed scoring copy for this tile size (skipped when
     the GPU has no room for it: the scorer then reads the index arrays, with the
@@ -303,6 +311,8 @@ def ensure_search_state(index, tile_log2: int = DEFAULT_TILE_LOG2, forward: bool
     float weights the doc-major copy used by the exact rescoring (skipped when
     `forward` is false or the GPU has no room for it: the rescoring then searches
     the term lists, with the same results)."""
+    if tile_log2 is None:
+        tile_log2 = default_tile_log2(index)
     a = index.aux()
     dev = _device_of(index)
     L = _lib.lib()
@@ -358,7 +368,9 @@ def build_packed(index, tile_log2: int) -> torch.Tensor:
     return out
 
 
-def gs_index_struct(index, tile_log2: int = DEFAULT_TILE_LOG2) -> _lib.GsIndex:
+def gs_index_struct(index, tile_log2: int | None = None) -> _lib.GsIndex:
+    if tile_log2 is None:
+        tile_log2 = default_tile_log2(index)
     a = ensure_search_state(index, tile_log2)
     N = int(index.num_docs)
     s = _lib.GsIndex()

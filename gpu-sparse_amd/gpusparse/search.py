@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .index import DEFAULT_TILE_LOG2, gs_index_struct, _device_of
+from .index import default_tile_log2, gs_index_struct, _device_of
 
 MAX_K = 8192
 DEFAULT_DENSE_BUDGET = 1 << 30   # bytes of [B, N] score rows below which the dense path is used
@@ -80,11 +80,12 @@ def _dense_rows(index, gidx, qt, qw, k, rows, out_s, out_i, dense_budget):
                "gs_search_dense")
 
 
-def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG2, path: str = "auto",
+def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, path: str = "auto",
            sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 0, waves: int = 0,
            tiles_per_wg: int = 0, dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None):
     """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
 
+    tile_log2: doc-tile size of the scorer (default: index.default_tile_log2).
     path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense".
     timing: optional dict; receives event pairs on the launch stream bracketing the
     fused scoring kernel ("score_kernel") and the whole gs_search call ("search"),
@@ -109,6 +110,8 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG
         qt = torch.full((B, 1), -1, dtype=torch.int32, device=dev)
         qw = torch.zeros((B, 1), dtype=qw.dtype, device=dev)
         T = 1
+    if tile_log2 is None:
+        tile_log2 = default_tile_log2(index)
     gidx = gs_index_struct(index, tile_log2)
     L = _lib.lib()
     acc_bytes = 4 if index.scores.dtype == torch.uint8 else 8
@@ -153,6 +156,22 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int = DEFAULT_TILE_LOG
         rows = torch.from_numpy(bad.astype(np.int32)).to(dev)
         _dense_rows(index, gidx, qt, qw, kk, rows, out_s, out_i, max(dense_budget, 1))
     return out_s, out_i
+
+
+def search_plan(index, B: int, T: int, k: int, *, tile_log2: int | None = None, sample_tiles: int = 0,
+                cand_cap: int = 0, unroll: int = 0, tiles_per_wg: int = 0) -> dict:
+    """How the fused path of `search` runs a batch of B queries of width T
+    (gs_search_plan): seed tiles, queries per group, postings per lane per chunk,
+    tiles per scoring workgroup and whether the packed copy is read."""
+    if tile_log2 is None:
+        tile_log2 = default_tile_log2(index)
+    gidx = gs_index_struct(index, tile_log2)
+    opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, 0, None, None, tiles_per_wg)
+    info = _lib.GsSearchPlanInfo()
+    _lib.check(_lib.lib().gs_search_plan(_lib.C.byref(gidx), int(B), int(T), min(int(k), int(index.num_docs)),
+                                         _lib.C.byref(opts), _lib.C.byref(info)), "gs_search_plan")
+    return {"tile_log2": tile_log2, "seed_tiles": info.seed_tiles, "group_size": info.group_size,
+            "unroll": info.unroll, "tiles_per_wg": info.tiles_per_wg, "packed": bool(info.packed)}
 
 
 def triton_fused_score(index, query_term_ids: torch.Tensor, query_term_scores: torch.Tensor, top_k: int = 10,

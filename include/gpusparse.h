@@ -183,6 +183,18 @@ int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wt
  * scatter-add rounded to fp32.  1 <= k <= min(n_docs, 8192). */
 int gs_search_workspace(const gs_index *index, int32_t B, int32_t T, int32_t k,
                         const gs_search_opts *opts, size_t *bytes);
+
+/* How gs_search would run a batch (no counterpart in the reference: an
+ * introspection call for benchmarks and tests). */
+typedef struct gs_search_plan_info {
+    int32_t seed_tiles;    /* doc tiles scored first with tau = 0 */
+    int32_t group_size;    /* queries per scoring group (their slices share one LDS tile) */
+    int32_t unroll;        /* postings per lane per chunk */
+    int32_t tiles_per_wg;  /* doc tiles per scoring workgroup after the seed tiles */
+    int32_t packed;        /* 1 when the scorer reads the packed copy */
+} gs_search_plan_info;
+int gs_search_plan(const gs_index *index, int32_t B, int32_t T, int32_t k, const gs_search_opts *opts,
+                   gs_search_plan_info *out);
 int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d, int32_t B,
               int32_t T, int32_t k, const gs_search_opts *opts, void *out_scores_d,
               int64_t *out_ids_d, int32_t *status_d, void *workspace_d, size_t workspace_bytes,

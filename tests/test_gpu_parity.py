@@ -87,7 +87,7 @@ def test_packed_copy_matches_oracle(device, seed, dtype, tile_log2):
 def test_search_without_packed_copy(device, dtype):
     """The scorer reads the index arrays when the packed copy is absent (fp32
     weights, or no room for it) and gives the same, oracle, answer."""
-    from gpusparse.index import DEFAULT_TILE_LOG2, ensure_search_state
+    from gpusparse.index import default_tile_log2, ensure_search_state
     rng = np.random.default_rng(5)
     csr = random_csr(rng, 30000, 60, max_len=12, dtype=dtype, dup_rate=0.02)
     ix = gs.build_index(csr, device)
@@ -95,12 +95,13 @@ def test_search_without_packed_copy(device, dtype):
     ti, tw = random_queries(rng, 24, 60, max_len=9, dtype=np.uint8 if dtype == np.uint8 else np.float32)
     print(f"packed vs plain scorer {dtype.__name__}", flush=True)
     assert_search_equal(ix, ref, ti, tw, 300, path="fused")
-    a = ensure_search_state(ix, DEFAULT_TILE_LOG2)
+    tl = default_tile_log2(ix)
+    a = ensure_search_state(ix, tl)
     if dtype == np.float32:
-        assert a.get(("packed", DEFAULT_TILE_LOG2)) is None
+        assert a.get(("packed", tl)) is None
         return
-    assert a[("packed", DEFAULT_TILE_LOG2)] is not None
-    a[("packed", DEFAULT_TILE_LOG2)] = None
+    assert a[("packed", tl)] is not None
+    a[("packed", tl)] = None
     assert_search_equal(ix, ref, ti, tw, 300, path="fused")
     assert_search_equal(ix, ref, ti, tw, 300, path="fused", unroll=8)
 
@@ -293,6 +294,19 @@ def test_search_packed_launch_shapes(c3_small, unroll, tile_log2, tiles_per_wg):
     assert_search_equal(ix, ref, ti, tw, 100, path="fused", unroll=unroll, tile_log2=tile_log2,
                         tiles_per_wg=tiles_per_wg)
     assert ensure_search_state(ix, tile_log2)[("packed", tile_log2)] is not None
+
+
+def test_search_plan_reports_defaults(c1, c3_small):
+    """The plan of the default fused search: fp32 postings from the index arrays in
+    4096-doc tiles, fp16 postings from the packed copy in 8192-doc tiles."""
+    ix32, _, ti, _ = c1
+    p32 = gs.search_plan(ix32, 32, ti.shape[1], 100)
+    assert p32["tile_log2"] == 12 and not p32["packed"] and p32["unroll"] == 8 and 1 <= p32["group_size"] <= 32
+    assert p32["seed_tiles"] >= 1 and p32["tiles_per_wg"] in (1, 2)
+    ix16, _, ti16, _ = c3_small
+    p16 = gs.search_plan(ix16, 24, ti16.shape[1], 1000)
+    assert p16["tile_log2"] == 13 and p16["packed"] and p16["unroll"] == 16 and p16["group_size"] == 4
+    assert gs.search_plan(ix16, 24, ti16.shape[1], 1000, sample_tiles=3, unroll=4)["seed_tiles"] == 3
 
 
 def test_search_u8_config_reduced(device):
