@@ -174,8 +174,8 @@ def main():
         from gpusparse import synth
         cfg = synth.CONFIGS[a.config]
         n_docs = a.n_docs or cfg.docs.n_rows
-        from gpusparse.index import DEFAULT_TILE_LOG2, DEFAULT_TILE_LOG2_PACKED
-        tile = a.tile_log2 or (DEFAULT_TILE_LOG2 if cfg.docs.weights == "f32" else DEFAULT_TILE_LOG2_PACKED)
+        from gpusparse.index import DEFAULT_TILE_LOG2_PACKED
+        tile = a.tile_log2 or DEFAULT_TILE_LOG2_PACKED
         summarize_traffic(a.summarize_traffic, cfg.name, n_docs, tile, a.copy_bytes or (1 << 30))
         return
     if a.copy_bytes:

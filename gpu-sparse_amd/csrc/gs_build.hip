@@ -13,6 +13,8 @@
 // and the last pass writes straight into the padded slot of each posting.
 #include <stdarg.h>
 
+#include <cmath>
+
 #include "gs_common.h"
 
 static thread_local char g_err[512];
@@ -506,28 +508,32 @@ __global__ void k_tile_bounds(const int32_t *__restrict__ doc, const int64_t *__
     }
 }
 
-// Packed scoring copy of the postings for one tile size: slot i holds the byte
-// offset of its doc's word in a tile slice, (doc mod tile) * 4 < 2^16, in the
-// low 16 bits and the weight's bits above it (fp16 and uint8 weights: one
-// 32-bit word), or the pair (offset, weight bits) for fp32 weights.  Padding
-// slots (doc < 0) hold 0.
+// Packed scoring copy of the postings for one tile size, one 32-bit word per
+// slot: the byte offset of its doc's word in a tile slice, (doc mod tile) * 4 <
+// 2^16, in the low 16 bits and the weight above it -- the uint8 weight, or for
+// float weights the int16 rint(w * 2^shift) (w * 2^shift is exact in fp64 and
+// rounded once, half to even; clamped to +-32767).  Padding slots (doc < 0) hold 0.
 template <int WT>
 __global__ void k_pack_postings(const int32_t *__restrict__ doc, const void *__restrict__ w, int64_t n,
-                                int32_t tile_log2, void *__restrict__ out) {
+                                int32_t tile_log2, int32_t shift, uint32_t *__restrict__ out) {
     const uint32_t mask = (1u << tile_log2) - 1u;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
         const int32_t d = doc[i];
-        const bool ok = d >= 0;
-        const uint32_t off = ok ? ((uint32_t)d & mask) << 2 : 0u;
-        if (WT == GS_W_F32) {
-            const uint32_t wb = ok ? reinterpret_cast<const uint32_t *>(w)[i] : 0u;
-            reinterpret_cast<uint2 *>(out)[i] = make_uint2(off, wb);
-        } else {
-            const uint32_t wb = !ok ? 0u
-                                : WT == GS_W_F16 ? (uint32_t) reinterpret_cast<const uint16_t *>(w)[i]
-                                                 : (uint32_t) reinterpret_cast<const uint8_t *>(w)[i];
-            reinterpret_cast<uint32_t *>(out)[i] = off | (wb << 16);
+        if (d < 0) {
+            out[i] = 0u;
+            continue;
         }
+        const uint32_t off = ((uint32_t)d & mask) << 2;
+        uint32_t wq;
+        if (WT == GS_W_U8) {
+            wq = reinterpret_cast<const uint8_t *>(w)[i];
+        } else {
+            const double x = gs_weight<WT>::decode(reinterpret_cast<const typename gs_weight<WT>::store_t *>(w)[i]);
+            const double r = rint(ldexp(x, shift));
+            const int32_t q = (int32_t)fmin(fmax(r, -32767.0), 32767.0);
+            wq = (uint32_t)(uint16_t)(int16_t)q;
+        }
+        out[i] = off | (wq << 16);
     }
 }
 
@@ -870,19 +876,40 @@ extern "C" int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, 
 }
 
 extern "C" int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, int64_t n_slots,
-                                int32_t tile_log2, void *out_d, void *stream) {
+                                int32_t tile_log2, int32_t w_shift, void *out_d, void *stream) {
     GS_REQUIRE(n_slots >= 0, "n_slots %lld is negative", (long long)n_slots);
     GS_REQUIRE(tile_log2 >= 6 && tile_log2 <= 14, "tile_log2 %d outside [6, 14]", tile_log2);
     GS_REQUIRE(wtype >= GS_W_F32 && wtype <= GS_W_U8, "unknown weight type %d", wtype);
+    GS_REQUIRE(wtype == GS_W_U8 || (w_shift >= -200 && w_shift <= 200), "w_shift %d outside [-200, 200]", w_shift);
     GS_REQUIRE(n_slots == 0 || (doc_ids_d && weights_d && out_d), "null pointer");
     if (n_slots == 0) return GS_OK;
     hipStream_t s = gs_stream(stream);
     const unsigned g = gs_blocks(n_slots, 256, 1 << 16);
+    uint32_t *out = reinterpret_cast<uint32_t *>(out_d);
     switch (wtype) {
-        case GS_W_F32: k_pack_postings<GS_W_F32><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, out_d); break;
-        case GS_W_F16: k_pack_postings<GS_W_F16><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, out_d); break;
-        default: k_pack_postings<GS_W_U8><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, out_d); break;
+        case GS_W_F32:
+            k_pack_postings<GS_W_F32><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, w_shift, out);
+            break;
+        case GS_W_F16:
+            k_pack_postings<GS_W_F16><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, w_shift, out);
+            break;
+        default: k_pack_postings<GS_W_U8><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, 0, out); break;
     }
     GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+extern "C" int gs_pack_shift(float max_abs, int32_t *shift) {
+    GS_REQUIRE(shift, "null pointer");
+    GS_REQUIRE(std::isfinite(max_abs) && max_abs >= 0.0f, "max_abs %g must be finite and >= 0", (double)max_abs);
+    if (max_abs == 0.0f) {
+        *shift = 0;
+        return GS_OK;
+    }
+    // max_abs * 2^s is exact in double for every float max_abs and |s| <= 300
+    int sh = (int)std::floor(std::log2(8191.0 / (double)max_abs));
+    while (std::ldexp((double)max_abs, sh) > 8191.0) --sh;
+    while (std::ldexp((double)max_abs, sh + 1) <= 8191.0) ++sh;
+    *shift = sh;
     return GS_OK;
 }

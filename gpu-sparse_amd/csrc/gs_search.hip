@@ -81,11 +81,22 @@ __global__ void k_fill(T *p, int64_t n, T v) {
 // rescoring is within g64(2n) M of exact.  Any doc of the fp64 top k then has a
 // fixed-point score >= tau' - 2 (E + g64 M) S, which is the margin `mfix`.
 // uint8 impacts: S = 1, exact, margin 0.
+//
+// With the packed copy (pk != 0) of float weights, the products are integers
+// qi * wq with wq = rint(w 2^s) (s = pk_shift, |wq| <= W_t = rint(max|w(t)| 2^s))
+// and qi = rint(q 2^f); `scale` then holds 2^f and the fixed-point scale is
+// S = 2^(f+s).  Per product |qi wq - q w S| <= |qi - q 2^f| |wq| + |q| 2^f |wq -
+// w 2^s| <= W_t / 2 + |q| 2^f / 2, so with Bw = sum_j W_j (1 + dup) and Q = sum_j
+// |q_j| (1 + dup):  |sum - exact S| <= Bw / 2 + Q 2^f / 2.  f is the largest
+// exponent with sum |qi wq| <= A 2^f + Bw / 2 < 2^31 (A = sum_j |q_j| W_j (1 +
+// dup)) and |qi| < 2^23 (the operand width of v_mul_i32_i24).  A term with W_t >
+// 32767 (a copy packed with too large a shift), or no feasible f, gets the
+// margin 2^31 - 1: the row is then finished by the dense path.
 template <int WT>
 __global__ void k_query_prep(const int32_t *__restrict__ qt, const void *__restrict__ qw, int32_t B, int32_t T,
                              int32_t V, const float *__restrict__ max_abs, const int32_t *__restrict__ dup,
-                             float *__restrict__ scale, uint32_t *__restrict__ mfix, uint32_t *__restrict__ tau,
-                             uint32_t *__restrict__ cnt, uint32_t *__restrict__ maxbin) {
+                             int32_t pk, int32_t pk_shift, float *__restrict__ scale, uint32_t *__restrict__ mfix,
+                             uint32_t *__restrict__ tau, uint32_t *__restrict__ cnt, uint32_t *__restrict__ maxbin) {
     // one wave per query; the lanes sum over its terms
     const int q = (int)((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6);
     const int lane = gs_lane();
@@ -104,21 +115,56 @@ __global__ void k_query_prep(const int32_t *__restrict__ qt, const void *__restr
     }
     // M and n as fp64 sums in any order: the factor (1 + 1e-12) below covers the
     // rounding of a sum of up to 8192 non-negative terms
-    double M = 0.0, n = 0.0;
+    double M = 0.0, n = 0.0, A = 0.0, Bw = 0.0, Q = 0.0, qmax = 0.0, Wmax = 0.0;
     for (int j = lane; j < T; j += 64) {
         const int32_t t = qt[(int64_t)q * T + j];
         if ((uint32_t)t >= (uint32_t)V) continue;
         const double m = 1.0 + (double)dup[t];
-        M += fabs((double)reinterpret_cast<const float *>(qw)[(int64_t)q * T + j]) * (double)max_abs[t] * m;
+        const double aq = fabs((double)reinterpret_cast<const float *>(qw)[(int64_t)q * T + j]);
+        M += aq * (double)max_abs[t] * m;
         n += m;
+        if (pk) {
+            const double W = rint(ldexp((double)max_abs[t], pk_shift));
+            A += aq * W * m;
+            Bw += W * m;
+            Q += aq * m;
+            qmax = fmax(qmax, aq);
+            Wmax = fmax(Wmax, W);
+        }
     }
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
         M += __shfl_xor(M, d, 64);
         n += __shfl_xor(n, d, 64);
+        A += __shfl_xor(A, d, 64);
+        Bw += __shfl_xor(Bw, d, 64);
+        Q += __shfl_xor(Q, d, 64);
+        qmax = fmax(qmax, __shfl_xor(qmax, d, 64));
+        Wmax = fmax(Wmax, __shfl_xor(Wmax, d, 64));
     }
     if (lane != 0) return;
     M *= 1.0 + 1e-12;  // fp64 rounding of the sum itself
+    const double g64 = (2.0 * n + 2.0) * 0x1p-53 / (1.0 - (2.0 * n + 2.0) * 0x1p-53);
+    if (pk) {
+        A *= 1.0 + 1e-12;
+        Bw *= 1.0 + 1e-12;
+        Q *= 1.0 + 1e-12;
+        const double room = 2147483646.0 - 0.5 * Bw;
+        int f = 100;
+        if (A > 0.0) f = (int)floor(log2(room / A));
+        if (qmax > 0.0) f = min(f, (int)floor(log2(8388607.0 / qmax)));
+        f = f > 100 ? 100 : (f < -100 ? -100 : f);
+        // the floors above are in fp64; step down while a bound is not met exactly
+        while (f > -100 && (A * ldexp(1.0, f) >= room || qmax * ldexp(1.0, f) + 0.5 >= 8388608.0)) --f;
+        const bool ok = room > 0.0 && Wmax <= 32767.0 && A * ldexp(1.0, f) < room &&
+                        qmax * ldexp(1.0, f) + 0.5 < 8388608.0;
+        const double Ef = 0.5 * Bw + 0.5 * Q * ldexp(1.0, f);  // fixed-point units
+        double mf = ceil(2.0 * (Ef * (1.0 + 1e-9) + g64 * M * ldexp(1.0, f + pk_shift))) + 2.0;
+        if (!ok || mf > 2147483647.0) mf = 2147483647.0;
+        scale[q] = (float)ldexp(1.0, f);
+        mfix[q] = (uint32_t)mf;
+        return;
+    }
     int e = 30;
     if (M > 0.0) {
         const double lim = (2147483647.0 - n - 2.0) / (M * (1.0 + 0x1p-23));
@@ -126,7 +172,6 @@ __global__ void k_query_prep(const int32_t *__restrict__ qt, const void *__restr
         e = e > 100 ? 100 : (e < -100 ? -100 : e);
     }
     const double S = ldexp(1.0, e);
-    const double g64 = (2.0 * n + 2.0) * 0x1p-53 / (1.0 - (2.0 * n + 2.0) * 0x1p-53);
     const double E = 0x1p-24 * M * (1.0 + 1e-9) + n / S + g64 * M;
     double mf = ceil(2.0 * E * S) + 2.0;
     if (mf > 2147483647.0) mf = 2147483647.0;
@@ -173,11 +218,22 @@ __device__ __forceinline__ void lds_add(A *p, A v) {
 }
 
 // Fixed-point contribution of one posting: trunc(fl32(qs * w)) with qs = q * 2^e
-// (one multiply and one v_cvt_i32_f32).
+// (one multiply and one v_cvt_i32_f32); uint8: the exact product (both factors
+// < 2^8, one full-rate v_mul_u32_u24).
 template <int WT>
 __device__ __forceinline__ uint32_t fixed_contrib(uint32_t qbits, typename gs_weight<WT>::store_t w) {
-    if (WT == GS_W_U8) return qbits * (uint32_t)w;
+    if (WT == GS_W_U8) return __umul24(qbits, (uint32_t)w);
     return (uint32_t)(int32_t)(__uint_as_float(qbits) * (float)gs_weight<WT>::decode(w));
+}
+
+// Contribution of one packed posting word (offset in bits 0-15, weight above):
+// uint8 weight times the uint8 query weight, or int16 rint(w 2^s) times the
+// integer query weight rint(q 2^f) (|.| < 2^23); exact 32-bit products either way
+// (v_mul_{u32_u24,i32_i24} reading the weight half-word through SDWA).
+template <int WT>
+__device__ __forceinline__ uint32_t packed_contrib(uint32_t qv, uint32_t word) {
+    if (WT == GS_W_U8) return __umul24(qv, (word >> 16) & 0xFFu);
+    return (uint32_t)__mul24((int32_t)qv, (int32_t)word >> 16);
 }
 
 // ---------------------------------------------------------------------- dense per-query tiles
@@ -277,12 +333,13 @@ __global__ void __launch_bounds__(512) k_score_dense(const DenseArgs a) {
 // weight) entries of its valid query terms are sorted by (term, slot, position)
 // so that each distinct term owns a contiguous entry range; u_term / u_ebeg list
 // the distinct terms (see the reordering at the end) with u_ebeg = entry count
-// << 16 | first entry.  Entry weights are stored pre-scaled (q * 2^e_q as fp32
-// bits for float weights, the uint8 weight for impacts).
+// << 16 | first entry.  Entry weights are stored pre-scaled: q * 2^e_q as fp32
+// bits for float weights, or with the packed copy (pk != 0) the integer rint(q *
+// 2^f) (k_query_prep), and the uint8 weight for impacts.
 template <int WT>
 __global__ void __launch_bounds__(1024)
     k_group_terms(const int32_t *__restrict__ qt, const void *__restrict__ qw, const float *__restrict__ scale,
-                  int32_t B, int32_t T, int32_t V, int32_t G, int32_t ecap, int32_t *__restrict__ u_term,
+                  int32_t pk, int32_t B, int32_t T, int32_t V, int32_t G, int32_t ecap, int32_t *__restrict__ u_term,
                   int32_t *__restrict__ u_ebeg, int32_t *__restrict__ u_count, uint2 *__restrict__ e_sw) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     __shared__ int32_t s_sh[17];
@@ -304,8 +361,12 @@ __global__ void __launch_bounds__(1024)
             const int32_t t = qt[src];
             if ((uint32_t)t < (uint32_t)V) {
                 kk = ((uint64_t)(uint32_t)t << 32) | ((uint64_t)g << 20) | (uint64_t)j;
-                w = WT == GS_W_U8 ? (uint32_t) reinterpret_cast<const uint8_t *>(qw)[src]
-                                  : __float_as_uint(reinterpret_cast<const float *>(qw)[src] * scale[q]);
+                if (WT == GS_W_U8) {
+                    w = (uint32_t) reinterpret_cast<const uint8_t *>(qw)[src];
+                } else {
+                    const float x = reinterpret_cast<const float *>(qw)[src] * scale[q];  // exact: scale = 2^f
+                    w = pk ? (uint32_t)(int32_t)rintf(x) : __float_as_uint(x);
+                }
             }
         }
         key[i] = kk;
@@ -448,18 +509,14 @@ static_assert(kTileLds + kUnionMetaLds + kStaticLdsBudget <= kLdsPerWg, "scoring
 // Waves then take chunks round-robin, load each posting once and add its
 // fixed-point contribution to every query slot of the term with ds_add_u32.
 // Afterwards the slices are scanned for candidates.
-// the integer type holding a packed weight's bits (fp16 and uint8 weights)
-template <int WT>
-using pk_half_t = std::conditional_t<WT == GS_W_F16, uint16_t, uint8_t>;
-
 // PK: postings come from the packed scoring copy (gs_pack_postings): one word
-// per posting with the doc's byte offset in a slice and the weight bits (fp32:
-// an offset / weight pair), instead of the doc id and weight arrays.
+// per posting with the doc's byte offset in a slice and the integer weight,
+// instead of the doc id and weight arrays.
 template <int WT, int UNROLL, bool PK>
 __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a) {
     using W = gs_weight<WT>;
     using store_t = typename W::store_t;
-    using pk_t = std::conditional_t<WT == GS_W_F32, uint2, uint32_t>;
+    using pk_t = uint32_t;
     constexpr int CH = 64 * UNROLL;
     constexpr int NW = kUnionThreads / 64;
 
@@ -648,15 +705,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                     const auto rp = gs_rsrc(pkd + pb, (uint32_t)(sh + k.n) * (uint32_t)sizeof(pk_t));
                     const int o_p = (lane + sh) * (int)sizeof(pk_t);
 #pragma unroll
-                    for (int u = 0; u < UNROLL; ++u) {
-                        if constexpr (WT == GS_W_F32) {
-                            const uint2 v = gs_bload64(rp, o_p + u * 64 * 8);
-                            k.doc[u] = (int32_t)v.x;
-                            k.wv[u] = __uint_as_float(v.y);
-                        } else {
-                            k.doc[u] = (int32_t)gs_bload32(rp, o_p + u * 256);
-                        }
-                    }
+                    for (int u = 0; u < UNROLL; ++u) k.doc[u] = (int32_t)gs_bload32(rp, o_p + u * 256);
                 } else {
                     const auto rd = gs_rsrc(a.doc + pb, (uint32_t)(sh + k.n) * 4u);
                     const auto rw = gs_rsrc(wall + pb, (uint32_t)(sh + k.n) * (uint32_t)sizeof(store_t));
@@ -677,12 +726,9 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                     if constexpr (!PK)
                         lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + ((d << 2) + badj)),
                                           fixed_contrib<WT>(wb, k.wv[u]));
-                    else if constexpr (WT == GS_W_F32)
-                        lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + (d + badj)),
-                                          fixed_contrib<WT>(wb, k.wv[u]));
                     else
                         lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + ((d & 0xFFFFu) + badj)),
-                                          fixed_contrib<WT>(wb, __builtin_bit_cast(store_t, (pk_half_t<WT>)(d >> 16))));
+                                          packed_contrib<WT>(wb, d));
                 }
             };
             // every entry (query slot) of the chunk's term; the group count is
@@ -1235,6 +1281,8 @@ int check_index(const gs_index *ix) {
                "index has a null device array");
     GS_REQUIRE(!ix->fwd_ptr_d || (ix->fwd_terms_d && ix->fwd_weights_d) || ix->n_slots == 0,
                "doc-major copy without term or weight array");
+    GS_REQUIRE(!ix->packed_d || ix->wtype == GS_W_U8 || (ix->packed_shift >= -200 && ix->packed_shift <= 200),
+               "packed_shift %d outside [-200, 200]", ix->packed_shift);
     return GS_OK;
 }
 
@@ -1276,7 +1324,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.rcap = kRescoreCap;
     // default postings per lane per chunk: 16 on packed one-word postings (their
     // registers allow it), else 8
-    const bool packed1 = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2 && ix->wtype != GS_W_F32;
+    const bool packed1 = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2;
     p.unroll = (o && o->unroll > 0) ? o->unroll : (packed1 ? 16 : 8);
     p.tiles_per_wg = (o && o->tiles_per_wg > 0) ? o->tiles_per_wg : 0;
     p.scale = ar.take<float>(B);
@@ -1333,8 +1381,12 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     };
     int rc = phase(0);
     if (rc) return rc;
-    k_query_prep<WT><<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d, ix->dup_d, p.scale,
-                                                      p.mfix, p.tau, p.cnt, p.maxbin);
+    // the fused scorer reads the packed copy when it was made for this tile size
+    const void *pk = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2 ? ix->packed_d : nullptr;
+    const int32_t pkf = pk && WT != GS_W_U8 ? 1 : 0;  // integer products of the packed float weights
+    k_query_prep<WT><<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d, ix->dup_d,
+                                                                     pkf, ix->packed_shift, p.scale, p.mfix, p.tau,
+                                                                     p.cnt, p.maxbin);
     k_fill<uint32_t><<<gs_blocks((int64_t)B * GS_HIST_BINS, 256, 4096), 256, 0, s>>>(
         p.hist, (int64_t)B * GS_HIST_BINS, 0u);
     GS_CHECK_LAUNCH();
@@ -1345,7 +1397,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
             attr.store(true);
         }
         k_group_terms<WT><<<p.n_groups, 1024, (size_t)p.gt_np * 12, s>>>(
-            qt, qw, p.scale, B, T, ix->vocab, p.G, p.ecap, p.u_term, p.u_ebeg, p.u_count, p.e_sw);
+            qt, qw, p.scale, pkf, B, T, ix->vocab, p.G, p.ecap, p.u_term, p.u_ebeg, p.u_count, p.e_sw);
         GS_CHECK_LAUNCH();
     }
     if ((rc = phase(1))) return rc;
@@ -1357,7 +1409,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     UnionArgs e{};
     e.doc = ix->doc_ids_d;
     e.w = ix->weights_d;
-    e.pk = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2 ? ix->packed_d : nullptr;
+    e.pk = pk;
     e.offsets = ix->offsets_d;
     e.tb = ix->tile_bounds_d;
     e.n_docs = ix->n_docs;

@@ -17,6 +17,9 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import Any, NamedTuple
 
+import ctypes as C
+import math
+
 import numpy as np
 import torch
 
@@ -24,15 +27,15 @@ from . import _lib
 
 BLOCK_SIZE = 32          # posting lists are padded to a multiple of this (gpu_inverted_index.py:18)
 VOCAB_SIZE = 30522       # fixed vocabulary of the harness builder (run_correctness_verification.py:28)
-DEFAULT_TILE_LOG2 = 12          # 4096 docs per LDS tile: fp32 postings, read from the index arrays
-DEFAULT_TILE_LOG2_PACKED = 13   # 8192 docs per LDS tile: fp16 / uint8 postings, read from the packed copy
+DEFAULT_TILE_LOG2 = 12          # 4096 docs per LDS tile: postings read from the index arrays
+DEFAULT_TILE_LOG2_PACKED = 13   # 8192 docs per LDS tile: postings read from the packed copy
 
 
 def default_tile_log2(index) -> int:
-    """Doc-tile size (log2) used when a search names none: 8192 docs for fp16 and
-    uint8 postings (the scorer reads one packed word per posting and its per-tile
-    set-up weighs more than the 9-query groups of smaller tiles save), 4096 for fp32."""
-    return DEFAULT_TILE_LOG2_PACKED if index.scores.dtype in (torch.float16, torch.uint8) else DEFAULT_TILE_LOG2
+    """Doc-tile size (log2) used when a search names none: 8192 docs (the scorer
+    reads one packed word per posting, and its per-tile set-up weighs more than the
+    9-query groups of 4096-doc tiles save)."""
+    return DEFAULT_TILE_LOG2_PACKED
 
 
 class CSR(NamedTuple):
@@ -303,10 +306,26 @@ def build_forward(index):
     return row_ptr, terms, w
 
 
+def list_max_abs(index) -> torch.Tensor:
+    """max |w| per posting list (gs_list_max), cached with the index."""
+    a = index.aux()
+    if "max_abs" not in a:
+        dev = _device_of(index)
+        V = int(index.vocab_size)
+        ms = torch.empty(V, dtype=torch.float32, device=dev)
+        ma = torch.empty(V, dtype=torch.float32, device=dev)
+        ws = torch.empty(8 * V, dtype=torch.uint8, device=dev)
+        _lib.check(_lib.lib().gs_list_max(_lib.ptr(index.scores), index.wtype, _lib.ptr(index.offsets),
+                                          _lib.ptr(index.lengths), V, _lib.ptr(ms), _lib.ptr(ma), _lib.ptr(ws),
+                                          ws.numel(), _lib.stream_ptr(dev)), "gs_list_max")
+        a["max_abs"] = ma
+    return a["max_abs"]
+
+
 def ensure_search_state(index, tile_log2: int | None = None, forward: bool = True) -> dict:
-    """Derived arrays gs_search needs: max |w|, duplicate counts, tile bounds, for
-    fp16 and uint8 weights the packed scoring copy for this tile size (skipped when
-    the GPU has no room for it: the scorer then reads the index arrays, with the
+    """Derived arrays gs_search needs: max |w|, duplicate counts, tile bounds, the
+    packed scoring copy for this tile size (skipped when the GPU has no room for it
+    or a weight is not finite: the scorer then reads the index arrays, with the
     same results), and for
     float weights the doc-major copy used by the exact rescoring (skipped when
     `forward` is false or the GPU has no room for it: the rescoring then searches
@@ -319,14 +338,7 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
     V = int(index.vocab_size)
     if "dup" not in a:
         require_ascending(index)
-    if "max_abs" not in a:
-        ms = torch.empty(V, dtype=torch.float32, device=dev)
-        ma = torch.empty(V, dtype=torch.float32, device=dev)
-        ws = torch.empty(8 * V, dtype=torch.uint8, device=dev)
-        _lib.check(L.gs_list_max(_lib.ptr(index.scores), index.wtype, _lib.ptr(index.offsets),
-                                 _lib.ptr(index.lengths), V, _lib.ptr(ms), _lib.ptr(ma), _lib.ptr(ws),
-                                 ws.numel(), _lib.stream_ptr(dev)), "gs_list_max")
-        a["max_abs"] = ma
+    list_max_abs(index)
     key = ("tile_bounds", tile_log2)
     if key not in a:
         N = int(index.num_docs)
@@ -336,10 +348,9 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
                                     N, tile_log2, _lib.ptr(tb), _lib.stream_ptr(dev)), "gs_tile_bounds")
         a[key] = tb
     key = ("packed", tile_log2)
-    if key not in a and int(index.doc_ids.numel()) > 0 and index.wtype != _lib.GS_W_F32:
-        # fp16 and uint8 postings pack into one word (4 of 6 or 5 bytes); fp32 ones
-        # would stay 8 bytes, and the scorer is faster on the index arrays there.
-        # One packed copy per index: the one for the tile size last searched.
+    if key not in a and int(index.doc_ids.numel()) > 0:
+        # One word per posting (4 of 8, 6 or 5 bytes).  One packed copy per index:
+        # the one for the tile size last searched.
         for old in [k for k in a if isinstance(k, tuple) and k[0] == "packed"]:
             del a[old]
         try:
@@ -354,18 +365,38 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
     return a
 
 
-def build_packed(index, tile_log2: int) -> torch.Tensor:
+def pack_shift(index) -> int | None:
+    """Weight scale 2^shift of the packed copy (gs_pack_shift of the largest |w|
+    of the index; 0 for uint8), or None when a weight is not finite."""
+    if index.wtype == _lib.GS_W_U8:
+        return 0
+    m = float(list_max_abs(index).max().item())
+    if not math.isfinite(m):
+        return None
+    sh = C.c_int32(0)
+    _lib.check(_lib.lib().gs_pack_shift(C.c_float(m), C.byref(sh)), "gs_pack_shift")
+    return int(sh.value)
+
+
+class Packed(NamedTuple):
+    words: torch.Tensor   # int32 [n_slots]
+    shift: int
+
+
+def build_packed(index, tile_log2: int) -> Packed | None:
     """Packed scoring copy of the postings for one tile size (gs_pack_postings):
     per slot the byte offset of its doc in a tile slice (bits 0-15) and the weight
-    bits (bits 16-31) as int32 for fp16 and uint8 weights, or (offset, weight
-    bits) int32 pairs for fp32 weights."""
+    (bits 16-31): the uint8 weight, or int16 rint(w * 2^shift) for float weights.
+    None when a weight is not finite."""
+    shift = pack_shift(index)
+    if shift is None:
+        return None
     dev = _device_of(index)
     n = int(index.doc_ids.numel())
-    shape = (n, 2) if index.wtype == _lib.GS_W_F32 else (n,)
-    out = torch.empty(shape, dtype=torch.int32, device=dev)
+    out = torch.empty(n, dtype=torch.int32, device=dev)
     _lib.check(_lib.lib().gs_pack_postings(_lib.ptr(index.doc_ids), _lib.ptr(index.scores), index.wtype, n, tile_log2,
-                                           _lib.ptr(out), _lib.stream_ptr(dev)), "gs_pack_postings")
-    return out
+                                           shift, _lib.ptr(out), _lib.stream_ptr(dev)), "gs_pack_postings")
+    return Packed(out, shift)
 
 
 def gs_index_struct(index, tile_log2: int | None = None) -> _lib.GsIndex:
@@ -392,7 +423,7 @@ def gs_index_struct(index, tile_log2: int | None = None) -> _lib.GsIndex:
         s.fwd_ptr_d, s.fwd_terms_d, s.fwd_weights_d = (t.data_ptr() for t in fwd)
     pk = a.get(("packed", tile_log2))
     if pk is not None:
-        s.packed_d, s.packed_tile_log2 = pk.data_ptr(), tile_log2
+        s.packed_d, s.packed_tile_log2, s.packed_shift = pk.words.data_ptr(), tile_log2, pk.shift
     return s
 
 

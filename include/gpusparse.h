@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 4
+#define GS_ABI_VERSION 5
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -68,6 +68,7 @@ typedef struct gs_index {
                                      fused scorer in place of doc_ids_d / weights_d */
     int32_t packed_tile_log2;     /* the tile size packed_d was made for; used only when it equals
                                      tile_log2 */
+    int32_t packed_shift;         /* the w_shift packed_d was made with (float weights) */
 } gs_index;
 
 /* Tuning knobs of gs_search; zero selects the default. */
@@ -77,7 +78,7 @@ typedef struct gs_search_opts {
                               docs, at least 4 Ki and at most 32 Ki docs) */
     int32_t cand_cap;      /* candidates kept per query before the dense fallback (default 65536) */
     int32_t unroll;        /* postings per lane per chunk of the fused scorer: 1, 2, 4, 8 or 16 (default
-                              16 with a packed fp16 / uint8 copy, else 8) */
+                              16 with a packed copy, else 8) */
     int32_t waves;         /* reserved, ignored */
     void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
     void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
@@ -160,13 +161,18 @@ int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wty
                     void *stream);
 
 /* Packed scoring copy of the postings (no counterpart in the reference: a layout
- * of its posting arrays for the LDS scorer).  Slot i of out_d holds the byte
- * offset of its doc's word in a tile slice, (doc mod 2^tile_log2) * 4, in bits
- * 0..15 and the weight's bits in bits 16..31 (GS_W_F16, GS_W_U8: uint32 per slot),
- * or the pair {offset, fp32 weight bits} (GS_W_F32: 2 x uint32 per slot).  Padding
- * slots (doc id < 0) hold 0.  tile_log2 <= 14. */
+ * of its posting arrays for the LDS scorer), one uint32 per slot: the byte offset
+ * of its doc's word in a tile slice, (doc mod 2^tile_log2) * 4, in bits 0..15 and
+ * the weight in bits 16..31 -- for GS_W_U8 the uint8 weight, for float weights
+ * the int16 rint(w * 2^w_shift) (clamped to +-32767; w_shift from gs_pack_shift
+ * keeps every |value| <= 8191).  Padding slots (doc id < 0) hold 0.
+ * tile_log2 <= 14; w_shift in [-200, 200] (ignored for GS_W_U8). */
 int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, int64_t n_slots,
-                     int32_t tile_log2, void *out_d, void *stream);
+                     int32_t tile_log2, int32_t w_shift, void *out_d, void *stream);
+/* Weight scale of a packed copy of float weights: the largest `shift` with
+ * max_abs * 2^shift <= 8191, for max_abs = the largest |weight| of the index (0 for
+ * max_abs == 0).  GS_EINVAL for a negative or non-finite max_abs. */
+int gs_pack_shift(float max_abs, int32_t *shift);
 
 /* ------------------------------------------------------------ search
  * Replaces triton_fused_score (src/triton_kernel.py:159-200) and
@@ -178,7 +184,8 @@ int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wt
  *   out_scores_d float32 [B][k] (int32 for GS_W_U8), out_ids_d int64 [B][k]
  *   status_d    int32 [B]: GS_ROW_DONE, or GS_ROW_DENSE when the row has to be
  *               recomputed with gs_search_dense (its outputs are then undefined).
- * Float indexes accumulate fixed-point int32 in LDS doc tiles and rescore the
+ * Float indexes accumulate fixed-point int32 in LDS doc tiles (from the packed
+ * copy: integer products of rint(q * 2^f) and the packed weights) and rescore the
  * selected candidates in fp64 in query-term order, so scores equal the fp64
  * scatter-add rounded to fp32.  1 <= k <= min(n_docs, 8192). */
 int gs_search_workspace(const gs_index *index, int32_t B, int32_t T, int32_t k,

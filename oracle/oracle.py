@@ -14,7 +14,9 @@ products, exhaustive sorting, closed forms):
   chunk_bounds           pinned: linear scan per list + partition invariant
   forward_index          pinned: the CSR rows sorted stably by column
   tile_bounds            pinned: linear scan per list
-  pack_postings          pinned: per-slot decoding + a scalar loop
+  pack_shift             pinned: closed forms at powers of two and scaled cases
+  pack_postings          pinned: per-slot decoding + a scalar loop with exact
+                         rational rounding (fractions.Fraction, half to even)
   scores_f64 / _u32      pinned: dense Q @ D^T (float64 / int64) on small inputs
   scores_f32_sequential  pinned: scalar float32 loop of gpu_scoring.py:246-251
   topk                   pinned: Python sorted() with the same key
@@ -109,18 +111,40 @@ def tile_bounds(index: dict, tile_log2: int) -> np.ndarray:
     return out
 
 
-def pack_postings(index: dict, tile_log2: int) -> np.ndarray:
+def pack_shift(max_abs: float) -> int:
+    """gs_pack_shift (no reference counterpart): the largest s with
+    max_abs * 2^s <= 8191, 0 for max_abs == 0."""
+    m = float(max_abs)
+    if not np.isfinite(m) or m < 0:
+        raise ValueError(f"max_abs {m} must be finite and >= 0")
+    if m == 0:
+        return 0
+    s = 0
+    while np.ldexp(m, s) > 8191.0:
+        s -= 1
+    while np.ldexp(m, s + 1) <= 8191.0:
+        s += 1
+    return s
+
+
+def pack_postings(index: dict, tile_log2: int, shift: int | None = None) -> np.ndarray:
     """Packed scoring copy (gs_pack_postings; no reference counterpart: a layout of
-    its posting arrays): per slot (doc mod 2^tile_log2) * 4 in bits 0-15 and the
-    weight bits in bits 16-31 (fp16, uint8: int32 [n]), or the pair (offset, fp32
-    bits) (int32 [n, 2]); padding slots (doc < 0) are 0."""
+    its posting arrays), int32 [n]: per slot (doc mod 2^tile_log2) * 4 in bits 0-15
+    and the weight in bits 16-31 -- the uint8 weight, or for float weights the
+    int16 rint(w * 2^shift) (half to even, clamped to +-32767), shift defaulting to
+    pack_shift of the largest |w|; padding slots (doc < 0) are 0."""
     doc = index["doc_ids"].astype(np.int64)
     w = index["scores"]
     ok = doc >= 0
     off = np.where(ok, (doc & ((1 << tile_log2) - 1)) << 2, 0).astype(np.uint32)
-    if w.dtype == np.float32:
-        return np.stack([off, np.where(ok, w.view(np.uint32), 0).astype(np.uint32)], axis=1).view(np.int32)
-    bits = (w.view(np.uint16) if w.dtype == np.float16 else w).astype(np.uint32)
+    if w.dtype == np.uint8:
+        bits = w.astype(np.uint32)
+    else:
+        wf = w.astype(np.float64)
+        if shift is None:
+            shift = pack_shift(np.max(np.abs(wf[ok])) if ok.any() else 0.0)
+        q = np.clip(np.rint(np.ldexp(wf, shift)), -32767, 32767).astype(np.int16)
+        bits = q.view(np.uint16).astype(np.uint32)
     return (off | (np.where(ok, bits, 0).astype(np.uint32) << 16)).view(np.int32)
 
 

@@ -73,20 +73,27 @@ def test_forward_index_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
 
 
 @pytest.mark.parametrize("seed,dtype,tile_log2", [(0, np.float32, 12), (1, np.float16, 13), (2, np.uint8, 8),
-                                                 (3, np.float16, 10)])
+                                                 (3, np.float16, 10), (4, np.float32, 14)])
 def test_packed_copy_matches_oracle(device, seed, dtype, tile_log2):
     from gpusparse.index import build_packed
     print(f"packed copy seed={seed} {dtype.__name__} tile_log2={tile_log2}", flush=True)
     csr = random_csr(np.random.default_rng(seed), 20000, 300, dtype=dtype, dup_rate=0.05)
+    if dtype != np.uint8:  # signed weights and ties at half units of the scale
+        csr.data[::5] *= -1
+        csr.data[3::13] = ((np.arange(len(csr.data[3::13])) % 7) + 0.5).astype(dtype) / 2
     ix = gs.build_index(csr, device)
-    got = build_packed(ix, tile_log2).cpu().numpy()
-    assert np.array_equal(got, O.pack_postings(oracle_index(csr), tile_log2))
+    ref = oracle_index(csr)
+    pk = build_packed(ix, tile_log2)
+    want_shift = 0 if dtype == np.uint8 else O.pack_shift(float(np.abs(csr.data.astype(np.float64)).max()))
+    assert pk.shift == want_shift
+    assert np.array_equal(pk.words.cpu().numpy(), O.pack_postings(ref, tile_log2))
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, np.uint8])
 def test_search_without_packed_copy(device, dtype):
-    """The scorer reads the index arrays when the packed copy is absent (fp32
-    weights, or no room for it) and gives the same, oracle, answer."""
+    """The scorer reads the index arrays when the packed copy is absent (no room
+    for it, a non-finite weight, or another tile size) and gives the same,
+    oracle, answer."""
     from gpusparse.index import default_tile_log2, ensure_search_state
     rng = np.random.default_rng(5)
     csr = random_csr(rng, 30000, 60, max_len=12, dtype=dtype, dup_rate=0.02)
@@ -97,9 +104,6 @@ def test_search_without_packed_copy(device, dtype):
     assert_search_equal(ix, ref, ti, tw, 300, path="fused")
     tl = default_tile_log2(ix)
     a = ensure_search_state(ix, tl)
-    if dtype == np.float32:
-        assert a.get(("packed", tl)) is None
-        return
     assert a[("packed", tl)] is not None
     a[("packed", tl)] = None
     assert_search_equal(ix, ref, ti, tw, 300, path="fused")
@@ -297,16 +301,54 @@ def test_search_packed_launch_shapes(c3_small, unroll, tile_log2, tiles_per_wg):
 
 
 def test_search_plan_reports_defaults(c1, c3_small):
-    """The plan of the default fused search: fp32 postings from the index arrays in
-    4096-doc tiles, fp16 postings from the packed copy in 8192-doc tiles."""
+    """The plan of the default fused search: postings from the packed copy in
+    8192-doc tiles, 16 per lane per chunk; 4 queries per group."""
     ix32, _, ti, _ = c1
     p32 = gs.search_plan(ix32, 32, ti.shape[1], 100)
-    assert p32["tile_log2"] == 12 and not p32["packed"] and p32["unroll"] == 8 and 1 <= p32["group_size"] <= 32
+    assert p32["tile_log2"] == 13 and p32["packed"] and p32["unroll"] == 16 and p32["group_size"] == 4
     assert p32["seed_tiles"] >= 1 and p32["tiles_per_wg"] in (1, 2)
+    assert gs.search_plan(ix32, 32, ti.shape[1], 100, tile_log2=12)["group_size"] == 9
     ix16, _, ti16, _ = c3_small
     p16 = gs.search_plan(ix16, 24, ti16.shape[1], 1000)
     assert p16["tile_log2"] == 13 and p16["packed"] and p16["unroll"] == 16 and p16["group_size"] == 4
     assert gs.search_plan(ix16, 24, ti16.shape[1], 1000, sample_tiles=3, unroll=4)["seed_tiles"] == 3
+
+
+@pytest.mark.parametrize("dtype,pattern", [(np.float32, "fine"), (np.float16, "coarse"), (np.float32, "coarse")])
+def test_packed_scores_exact_under_near_ties(device, dtype, pattern):
+    """The packed copy holds rounded weights, so many docs share one fixed-point
+    score while their fp64 scores differ: 'fine' weights 1 + j 2^-20 all round to
+    a few values of the 2^-12 grid; 'coarse' puts one weight of 600 in the index,
+    so the others (in [0.01, 1)) round to multiples of 1/8.  The margin must send every doc that
+    can reach the top k to the fp64 rescoring, and the answer must equal the
+    oracle's, ties by doc id included (equal-weight docs are planted too)."""
+    rng = np.random.default_rng(11)
+    n_docs, vocab = 6000, 8
+    rows = []
+    for d in range(n_docs):
+        terms = np.sort(rng.choice(6, size=rng.integers(2, 6), replace=False))
+        if pattern == "fine":
+            w = 1.0 + rng.integers(0, 2000, size=len(terms)) * 2.0 ** -20
+        else:
+            w = rng.uniform(0.01, 1.0, size=len(terms))
+            if dtype == np.float32:
+                w *= np.where(rng.random(len(terms)) < 0.2, -1.0, 1.0)
+        if d % 97 == 0 and d:  # exact duplicates of an earlier doc: ties broken by doc id
+            terms, w = rows[d - 1]
+        rows.append((terms, w))
+    rows[4321] = (np.array([6, 7]), np.array([600.0, 1.0]) if pattern == "coarse" else np.array([1.5, 1.0]))
+    indptr = np.cumsum([0] + [len(t) for t, _ in rows]).astype(np.int64)
+    csr = CSR(indptr, np.concatenate([t for t, _ in rows]).astype(np.int32),
+              np.concatenate([w for _, w in rows]).astype(dtype), (n_docs, vocab))
+    ix = gs.build_index(csr, device)
+    ref = oracle_index(csr)
+    ti = np.array([[0, 1, 2, 3, 4, 5], [2, 3, 5, -1, -1, -1], [0, 0, 1, 4, -1, -1], [5, 4, 3, 2, 1, 0]], np.int32)
+    tw = np.array([[0.7, 1.3, 0.9, 2.1, 0.4, 1.0], [1.0, 1.0, 1.0, 0, 0, 0], [0.5, 0.25, 3.0, 1.0, 0, 0],
+                   [1e-3, 2.0, 0.3, 0.3, 7.0, 0.11]], np.float32)
+    print(f"near ties {dtype.__name__} {pattern}", flush=True)
+    assert gs.search_plan(ix, 4, ti.shape[1], 200)["packed"]
+    for k in (1, 50, 200):
+        assert_search_equal(ix, ref, ti, tw, k, path="fused")
 
 
 def test_search_u8_config_reduced(device):

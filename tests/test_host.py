@@ -45,6 +45,21 @@ def test_argument_errors_map_to_python_exceptions():
         _lib.check(rc, "gs_search")
 
 
+def test_pack_shift_matches_oracle():
+    """gs_pack_shift is host code: the C ABI and the oracle agree on random,
+    power-of-two and extreme magnitudes, and reject negative / non-finite input."""
+    L = _lib.lib()
+    rng = np.random.default_rng(3)
+    vals = list(np.float32(rng.lognormal(0.0, 6.0, 300))) + [np.float32(2.0) ** e for e in range(-149, 128, 7)]
+    vals += [np.float32(0.0), np.finfo(np.float32).max, np.float32(8191.0), np.float32(8191.5), np.float32(4095.75)]
+    for v in vals:
+        sh = ctypes.c_int32(99)
+        assert L.gs_pack_shift(ctypes.c_float(float(v)), ctypes.byref(sh)) == _lib.GS_OK
+        assert sh.value == O.pack_shift(float(v)), float(v)
+    for bad in (-1.0, float("inf"), float("nan")):
+        assert L.gs_pack_shift(ctypes.c_float(bad), ctypes.byref(ctypes.c_int32())) == _lib.GS_EINVAL
+
+
 def test_no_gpu_raises_runtime_error():
     import torch
     if torch.cuda.is_available():

@@ -104,35 +104,59 @@ def test_tile_bounds_match_linear_scan(tile_log2):
             assert tb[t, j] == next((i for i, d in enumerate(seg) if d >= edge), n)
 
 
+@pytest.mark.parametrize("max_abs,want", [(1.0, 12), (3.0, 11), (8191.0, 0), (8192.0, -1), (0.5, 13),
+                                          (1e-3, 22), (0.0, 0), (float(np.finfo(np.float32).max), -116),
+                                          (float(np.float32(2.0 ** -149)), 161), (4095.75, 0), (4095.5, 1),
+                                          (4096.0, 0)])
+def test_pack_shift_closed_forms(max_abs, want):
+    """Largest s with max_abs * 2^s <= 8191: at powers of two 8191 / 2^s falls
+    between consecutive powers, so s = 12 - log2(max_abs); checked by hand for the
+    others (1e-3 * 2^22 = 4194.3, * 2^23 = 8388.6; 4095.75 * 2 = 8191.5, 4095.5 * 2 = 8191; FLT_MAX =
+    (2 - 2^-23) 2^127, so FLT_MAX * 2^-115 = 8192 - 2^-11 > 8191)."""
+    assert O.pack_shift(max_abs) == want
+    with pytest.raises(ValueError):
+        O.pack_shift(-1.0)
+    with pytest.raises(ValueError):
+        O.pack_shift(float("inf"))
+
+
 @pytest.mark.parametrize("tile_log2,dtype", [(12, np.float16), (8, np.uint8), (13, np.float32), (14, np.float16)])
 def test_pack_postings_decodes_and_matches_scalar_loop(tile_log2, dtype):
+    from fractions import Fraction
     rng = np.random.default_rng(tile_log2)
     csr = random_csr(rng, 40000, 50, dtype=dtype, dup_rate=0.05)
+    if dtype != np.uint8:  # signed weights and exact ties at half units
+        csr.data[::7] *= -1
+        csr.data[5::11] = (np.arange(len(csr.data[5::11])) % 9 + 0.5).astype(dtype) / 4
     ix = O.build_index(csr.indptr, csr.indices, csr.data, 40000, 50)
     pk = O.pack_postings(ix, tile_log2)
     doc, w = ix["doc_ids"], ix["scores"]
     mask = (1 << tile_log2) - 1
-    # decoding gives back the doc's place in its tile and the weight, padding is 0
-    if dtype == np.float32:
-        off, wb = pk[:, 0].view(np.uint32), pk[:, 1].view(np.uint32)
-        assert np.array_equal(wb[doc >= 0], w[doc >= 0].view(np.uint32))
-    else:
-        u = pk.view(np.uint32)
-        off, wb = u & 0xFFFF, u >> 16
-        bits = w.view(np.uint16) if dtype == np.float16 else w
-        assert np.array_equal(wb[doc >= 0], bits[doc >= 0].astype(np.uint32))
+    u = pk.view(np.uint32)
+    off, wb = u & 0xFFFF, u >> 16
     assert np.array_equal(off[doc >= 0] >> 2, doc[doc >= 0] & mask) and not np.any(off[doc >= 0] & 3)
-    assert not np.any(pk.reshape(len(doc), -1)[doc < 0])
-    # scalar loop over the first slots
-    for i in range(0, len(doc), 997):
+    assert not np.any(pk[doc < 0])
+    if dtype == np.uint8:
+        assert np.array_equal(wb[doc >= 0], w[doc >= 0].astype(np.uint32))
+        shift = 0
+    else:
+        shift = O.pack_shift(float(np.abs(w[doc >= 0].astype(np.float64)).max()))
+        q = wb.astype(np.uint16).view(np.int16).astype(np.int64)
+        assert np.abs(q).max() <= 8191
+        err = np.abs(q[doc >= 0] - np.ldexp(w[doc >= 0].astype(np.float64), shift))
+        assert err.max() <= 0.5
+    # scalar loop with exact rational rounding (Python's round: half to even)
+    for i in range(0, len(doc), 97):
         d = int(doc[i])
-        o = ((d % (1 << tile_log2)) * 4) if d >= 0 else 0
-        if dtype == np.float32:
-            exp = (o, int(w[i].view(np.uint32)) if d >= 0 else 0)
-            assert (int(pk[i, 0]) & 0xFFFFFFFF, int(pk[i, 1]) & 0xFFFFFFFF) == exp
+        if d < 0:
+            assert int(pk[i]) == 0
+            continue
+        o = (d % (1 << tile_log2)) * 4
+        if dtype == np.uint8:
+            b = int(w[i])
         else:
-            b = int(w[i].view(np.uint16)) if dtype == np.float16 else int(w[i])
-            assert int(pk[i]) & 0xFFFFFFFF == (o + (b << 16) if d >= 0 else 0)
+            b = round(Fraction(float(w[i])) * Fraction(2) ** shift) & 0xFFFF
+        assert int(pk[i]) & 0xFFFFFFFF == o + (b << 16)
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 17, 64, 1000])
