@@ -546,9 +546,17 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     int32_t *s_tid = reinterpret_cast<int32_t *>(s_toff + kUnionBatch);    // [kUnionBatch] term ids
 
     const int64_t row = (int64_t)a.n_tiles + 1;
-    const int U = a.u_count[grp];
     const int32_t *uterm = a.u_term + (int64_t)grp * a.ecap;
     const int32_t *uebeg = a.u_ebeg + (int64_t)grp * (a.ecap + 1);
+    // The group's first union terms are loaded together with their count (the
+    // loads stay inside the group's rows; entries past the count are not used),
+    // so the bounds below wait for one load instead of two in a row.
+    int32_t t_first = 0, e_first = 0;
+    if (tid < min(kUnionBatch, a.ecap)) {
+        t_first = uterm[tid];
+        e_first = uebeg[tid];
+    }
+    const int U = a.u_count[grp];
     const uint2 *esw = a.e_sw + (int64_t)grp * a.ecap;
     const store_t *wall = reinterpret_cast<const store_t *>(a.w);
     const pk_t *pkd = reinterpret_cast<const pk_t *>(a.pk);
@@ -559,10 +567,10 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     const bool single = U <= kUnionBatch;
     int my_lo = 0, my_hi = 0;
     if (single && tid < U) {
-        const int32_t t = uterm[tid];
+        const int32_t t = t_first;
         s_tid[tid] = t;
         s_toff[tid] = a.offsets[t];
-        s_e[tid] = uebeg[tid];
+        s_e[tid] = e_first;
         my_lo = a.tb[(int64_t)t * row + tile_lo];
         my_hi = a.tb[(int64_t)t * row + tile_lo + 1];
     }
@@ -652,14 +660,17 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         // its issue priority as its share of the chunks completes (3 for the
         // first quarter, then 2, 1, 0): waves that are behind are served first.
         const int my_total = (total - wave + NW - 1) / NW;  // chunks of this wave in the batch
-        int level = 0;
+        // level = floor(4 done / my_total), i.e. level >= L once done >= ceil(L
+        // my_total / 4); only the next boundary is compared per chunk
+        auto quarter = [&](int L) { return (L * my_total + 3) >> 2; };
+        int level = 0, next_at = quarter(1);
         __builtin_amdgcn_s_setprio(3);
         auto progress = [&](int done) {
-            const int lv = (4 * done) / max(my_total, 1);
-            if (lv == level) return;
-            level = lv;
-            if (lv == 1) __builtin_amdgcn_s_setprio(2);
-            else if (lv == 2) __builtin_amdgcn_s_setprio(1);
+            if (done < next_at) return;
+            while (level < 3 && done >= quarter(level + 1)) ++level;
+            next_at = level < 3 ? quarter(level + 1) : 0x7FFFFFFF;
+            if (level == 1) __builtin_amdgcn_s_setprio(2);
+            else if (level == 2) __builtin_amdgcn_s_setprio(1);
             else __builtin_amdgcn_s_setprio(0);
         };
         for (int cb = wave; cb < total; cb += 64 * NW) {
@@ -754,14 +765,16 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                     add_entries(k, std::integral_constant<int, UNROLL>{});
                     return;
                 }
-                // last chunk of a term: lanes past its end read weight 0 and are sent
-                // to doc doc0 + lane, a word of their own (one shared word would
-                // serialise their atomics; a packed lane gets offset lane * 4 and
-                // weight 0); only the 64-posting groups holding postings run
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u)
-                    k.doc[u] = u * 64 + lane < k.n ? k.doc[u] : (PK ? lane << 2 : (int32_t)doc0 + lane);
-                gs_dispatch_upto<UNROLL>((k.n + 63) >> 6, [&](auto ngc) { add_entries(k, ngc); });
+                // last chunk of a term: only the 64-posting groups holding postings
+                // run, and in the last of them lanes past the end read weight 0 and
+                // are sent to doc doc0 + lane, a word of their own (one shared word
+                // would serialise their atomics; a packed lane gets offset lane * 4
+                // and weight 0)
+                gs_dispatch_upto<UNROLL>((k.n + 63) >> 6, [&](auto ngc) {
+                    constexpr int L = decltype(ngc)::value - 1;
+                    k.doc[L] = L * 64 + lane < k.n ? k.doc[L] : (PK ? lane << 2 : (int32_t)doc0 + lane);
+                    add_entries(k, ngc);
+                });
             };
             // two chunk buffers in rotation: the loads of the wave's next chunk are
             // in flight while the current one is applied.  Fetches past the end
@@ -791,9 +804,10 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     // 256-doc chunks, 4 docs per lane (one 16-byte LDS read).  Slices are zeroed
     // whole and docs past n_docs get no adds, so no bound check is needed, and
     // thr >= 1 makes the signed compare also reject zero and negative sums.
-    // Pass 1 counts each chunk's candidates; a per-slot scan gives every chunk
-    // its offset and one global atomic per slot reserves the slot's range; pass
-    // 2 revisits only the chunks holding candidates.
+    // Pass 1 counts each chunk's candidates; one wave per slot scans the slot's
+    // chunk counts (one per lane) and reserves the slot's range with one global
+    // atomic; pass 2 revisits only the chunks holding candidates (a wave reads
+    // its chunk counts at once, one per lane).
     const int cps_log2 = a.tile_log2 - 8;  // 256-doc chunks per slice = 1 << cps_log2
     const int cps = 1 << cps_log2;
     const int nce = nq << cps_log2;        // <= kEmitChunks (G * TILE <= kTileLds / 4)
@@ -832,20 +846,23 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
         }
     }
     __syncthreads();
-    if (tid < nq) {
-        uint32_t run = 0;
-        for (int i = 0; i < cps; ++i) {
-            const uint32_t t = s_off[(tid << cps_log2) + i];
-            s_off[(tid << cps_log2) + i] = run;
-            run += t;
+    for (int g = wave; g < nq; g += NW) {
+        const uint32_t c = lane < cps ? s_off[(g << cps_log2) + lane] : 0u;
+        const uint32_t inc = gs_wave_incl_scan(c);
+        const uint32_t run = (uint32_t)__shfl((int)inc, 63, 64);
+        if (lane < cps) s_off[(g << cps_log2) + lane] = inc - c;
+        if (lane == 0) {
+            s_base[g] = run ? atomicAdd(a.cnt + grp * a.G + g, run) : 0u;
+            s_emit[g] = run;
+            s_maxb[g] = 0;
         }
-        s_base[tid] = run ? atomicAdd(a.cnt + grp * a.G + tid, run) : 0u;
-        s_emit[tid] = run;
-        s_maxb[tid] = 0;
     }
     __syncthreads();
-    for (int ch = wave; ch < nce; ch += NW) {
-        if (s_ccnt[ch] == 0) continue;
+    const int my_ch = wave + lane * NW;
+    uint64_t live = __ballot(my_ch < nce && s_ccnt[min(my_ch, kEmitChunks - 1)] != 0);
+    while (live) {
+        const int ch = wave + (__ffsll((unsigned long long)live) - 1) * NW;
+        live &= live - 1;
         uint32_t vv[4];
         bool keep[4];
         uint64_t mk[4];
