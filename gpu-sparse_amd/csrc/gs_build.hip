@@ -537,6 +537,116 @@ __global__ void k_pack_postings(const int32_t *__restrict__ doc, const void *__r
     }
 }
 
+// Block-wide exclusive prefix sum over 1024 threads (one value each); returns
+// the thread's offset and writes the total to *total.  Uses sh[16].
+__device__ uint32_t block_excl_scan_1024(uint32_t v, uint32_t *sh, uint32_t *total) {
+    const int lane = gs_lane(), wave = threadIdx.x >> 6;
+    const uint32_t inc = gs_wave_incl_scan(v);
+    if (lane == 63) sh[wave] = inc;
+    __syncthreads();
+    uint32_t base = 0, tot = 0;
+    for (int w = 0; w < 16; ++w) {
+        const uint32_t x = sh[w];
+        base += w < wave ? x : 0u;
+        tot += x;
+    }
+    __syncthreads();
+    *total = tot;
+    return base + inc - v;
+}
+
+// The kHeavyTerms non-empty lists with the most postings, by (length
+// descending, term ascending), -1 past the number of non-empty lists.  One
+// workgroup of 1024 threads: an 8-bit-per-pass radix select finds the
+// kHeavyTerms-th largest length L; the lists longer than L and the first lists
+// (by term id) of length L are collected, then sorted by one wave.
+__global__ void __launch_bounds__(1024) k_heavy_terms(const int32_t *__restrict__ len, int32_t V,
+                                                      int32_t *__restrict__ heavy) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t sh[16];
+    __shared__ uint32_t s_pref, s_need;
+    __shared__ int32_t s_sel[kHeavyTerms];
+    const int tid = threadIdx.x, lane = gs_lane();
+    const int per = (V + 1023) / 1024;
+    const int t0 = tid * per, t1 = min(V, t0 + per);
+    // non-empty lists
+    uint32_t nz = 0;
+    for (int t = t0; t < t1; ++t) nz += len[t] > 0;
+    uint32_t n_nz;
+    block_excl_scan_1024(nz, sh, &n_nz);
+    // L = the kHeavyTerms-th largest length (1 when there are fewer non-empty lists)
+    uint32_t L = 1;
+    if (n_nz > (uint32_t)kHeavyTerms) {
+        if (tid == 0) {
+            s_pref = 0;
+            s_need = kHeavyTerms;
+        }
+        uint32_t mask = 0;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            if (tid < 256) hist[tid] = 0;
+            __syncthreads();
+            const uint32_t pref = s_pref;
+            for (int t = t0; t < t1; ++t) {
+                const uint32_t v = (uint32_t)max(len[t], 0);
+                if (v && (v & mask) == pref) atomicAdd(&hist[(v >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid < 64) {  // lane l holds digits 255 - 4l .. 252 - 4l, highest first
+                uint32_t c[4], sum = 0;
+                for (int j = 0; j < 4; ++j) sum += (c[j] = hist[255 - 4 * lane - j]);
+                const uint32_t inc = gs_wave_incl_scan(sum);
+                const uint32_t need = s_need;
+                const uint64_t hit = __ballot(inc >= need);
+                const int l = __ffsll((unsigned long long)hit) - 1;  // exists: the prefix holds >= need values
+                if (lane == l) {
+                    uint32_t cum = inc - sum;
+                    int j = 0;
+                    while (cum + c[j] < need) cum += c[j++];
+                    s_pref = pref | ((uint32_t)(255 - 4 * lane - j) << shift);
+                    s_need = need - cum;
+                }
+            }
+            mask |= 255u << shift;
+            __syncthreads();
+        }
+        L = s_pref;
+    }
+    // collect the lists longer than L, then the first `need` lists of length L
+    uint32_t gt = 0, eq = 0;
+    for (int t = t0; t < t1; ++t) {
+        const uint32_t v = (uint32_t)max(len[t], 0);
+        gt += v > L;
+        eq += v == L;
+    }
+    uint32_t n_gt, n_eq;
+    uint32_t o_gt = block_excl_scan_1024(gt, sh, &n_gt);
+    uint32_t o_eq = block_excl_scan_1024(eq, sh, &n_eq);
+    const uint32_t need_eq = min(n_eq, (uint32_t)kHeavyTerms - min(n_gt, (uint32_t)kHeavyTerms));
+    if (tid < kHeavyTerms) s_sel[tid] = -1;
+    __syncthreads();
+    for (int t = t0; t < t1; ++t) {
+        const uint32_t v = (uint32_t)max(len[t], 0);
+        if (v > L && o_gt < (uint32_t)kHeavyTerms) s_sel[o_gt++] = t;
+        if (v == L) {
+            if (o_eq < need_eq) s_sel[n_gt + o_eq] = t;
+            ++o_eq;
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {  // bitonic sort of the 64 picks by (length desc, term asc); -1 last
+        const int32_t t = s_sel[lane];
+        uint64_t key = t < 0 ? 0ull : ((uint64_t)(uint32_t)len[t] << 32) | (uint32_t)(0x7FFFFFFF - t);
+        for (int size = 2; size <= 64; size <<= 1)
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const uint64_t o = __shfl_xor(key, stride, 64);
+                const bool desc = (lane & size) == 0;
+                const bool lower = (lane & stride) == 0;
+                key = (lower == desc) ? (key > o ? key : o) : (key < o ? key : o);
+            }
+        heavy[lane] = key ? (int32_t)(0x7FFFFFFF - (uint32_t)key) : -1;
+    }
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -895,6 +1005,14 @@ extern "C" int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d,
             break;
         default: k_pack_postings<GS_W_U8><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, 0, out); break;
     }
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+extern "C" int gs_heavy_terms(const int32_t *lengths_d, int32_t vocab, int32_t *heavy_d, void *stream) {
+    GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
+    GS_REQUIRE(lengths_d && heavy_d, "null pointer");
+    k_heavy_terms<<<1, 1024, 0, gs_stream(stream)>>>(lengths_d, vocab, heavy_d);
     GS_CHECK_LAUNCH();
     return GS_OK;
 }

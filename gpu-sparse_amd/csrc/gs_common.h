@@ -58,6 +58,7 @@ struct gs_arena {
 // ------------------------------------------------------------------ device helpers
 
 constexpr int GS_WAVE = 64;
+constexpr int kHeavyTerms = GS_HEAVY_TERMS;  // most frequent terms that sign a query for grouping
 
 __device__ __forceinline__ int gs_lane() { return (int)(threadIdx.x & (GS_WAVE - 1)); }
 

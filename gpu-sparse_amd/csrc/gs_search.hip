@@ -474,6 +474,100 @@ __global__ void __launch_bounds__(1024)
     }
 }
 
+// ---------------------------------------------------------------------- query grouping
+
+// Each posting is loaded once per (doc tile, query group) and added to every slot
+// of the group holding its term, so groups whose queries share long lists load
+// fewer postings.  A query's signature is the set of the index's kHeavyTerms most
+// frequent terms it holds: a 64-bit mask, bit 63 = the most frequent term.  Per
+// block of NB = G floor(1024 / G) queries: masks from all (query, term) entries
+// at once (LDS atomic or), then the queries sorted by mask (descending, then
+// query index), so that queries holding the same most frequent terms become
+// neighbours and share groups.  perm[slot] = query.  The order only moves
+// queries between groups: every query's result is the same in any order.
+__global__ void __launch_bounds__(1024)
+    k_group_order(const int32_t *__restrict__ qt, int32_t B, int32_t T, int32_t V, const int32_t *__restrict__ heavy,
+                  int32_t G, int32_t *__restrict__ perm) {
+    __shared__ int32_t h_term[256];  // open-addressing table: heavy term -> mask bit
+    __shared__ int32_t h_bit[256];
+    __shared__ uint64_t s_mask[1024];
+    __shared__ uint32_t s_idx[1024];
+    const int tid = threadIdx.x;
+    const int NB = G * (1024 / G);
+    const int base = blockIdx.x * NB;
+    const int n = min(NB, B - base);
+    int np = 1;
+    while (np < n) np <<= 1;
+    if (tid < 256) h_term[tid] = -1;
+    s_mask[tid] = 0;
+    s_idx[tid] = (uint32_t)tid;  // entries past n sort last: mask 0, larger index
+    __syncthreads();
+    if (tid < kHeavyTerms) {
+        const int32_t t = heavy[tid];
+        if (t >= 0) {
+            uint32_t h = ((uint32_t)t * 2654435761u) >> 24;
+            while (atomicCAS(&h_term[h], -1, t) != -1) h = (h + 1) & 255u;
+            h_bit[h] = 63 - tid;
+        }
+    }
+    __syncthreads();
+    // masks from the block's (query, term) entries: each thread loads 8 entries
+    // at a time (coalesced, all in flight together), then looks them up
+    const int ne = n * T;
+    const int32_t *rows = qt + (int64_t)base * T;
+    for (int e0 = 0; e0 < ne; e0 += 8 * 1024) {
+        int32_t tv[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int e = e0 + r * 1024 + tid;
+            tv[r] = e < ne ? rows[e] : -1;
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int32_t t = tv[r];
+            if ((uint32_t)t >= (uint32_t)V) continue;
+            uint32_t h = ((uint32_t)t * 2654435761u) >> 24;
+            int32_t x;
+            while ((x = h_term[h]) != t && x >= 0) h = (h + 1) & 255u;
+            if (x == t)
+                __hip_atomic_fetch_or(&s_mask[(uint32_t)(e0 + r * 1024 + tid) / (uint32_t)T], 1ull << h_bit[h],
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+    for (int size = 2; size <= np; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            const int j = tid ^ stride;
+            if (tid < np && j > tid) {
+                const uint64_t mi = s_mask[tid], mj = s_mask[j];
+                const uint32_t ii = s_idx[tid], ij = s_idx[j];
+                const bool j_first = mj > mi || (mj == mi && ij < ii);
+                if (j_first == ((tid & size) == 0)) {
+                    s_mask[tid] = mj;
+                    s_mask[j] = mi;
+                    s_idx[tid] = ij;
+                    s_idx[j] = ii;
+                }
+            }
+        }
+    __syncthreads();
+    if (tid < n) perm[base + tid] = base + (int)s_idx[tid];
+}
+
+// qt_p / qw_p rows in slot order: row s is query perm[s]
+template <int WT>
+__global__ void k_permute_queries(const int32_t *__restrict__ qt, const void *__restrict__ qw,
+                                  const int32_t *__restrict__ perm, int32_t B, int32_t T, int32_t *__restrict__ qt_p,
+                                  void *__restrict__ qw_p) {
+    using qw_t = typename gs_weight<WT>::qw_t;
+    const int64_t n = (int64_t)B * T;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t src = (int64_t)perm[i / T] * T + i % T;
+        qt_p[i] = qt[src];
+        reinterpret_cast<qw_t *>(qw_p)[i] = reinterpret_cast<const qw_t *>(qw)[src];
+    }
+}
+
 // ---------------------------------------------------------------------- group-tile scoring
 
 struct UnionArgs {
@@ -934,16 +1028,18 @@ __global__ void __launch_bounds__(kSelThreads)
     k_select_cands(const uint32_t *__restrict__ cand_doc, const uint32_t *__restrict__ cand_key,
                    const uint32_t *__restrict__ cnt, int32_t cap, int32_t k, const uint32_t *__restrict__ mfix,
                    uint32_t *__restrict__ resc_doc, uint32_t *__restrict__ resc_cnt, int32_t resc_cap,
-                   void *__restrict__ out_scores, int64_t *__restrict__ out_ids, int32_t *__restrict__ status) {
+                   const int32_t *__restrict__ perm, void *__restrict__ out_scores, int64_t *__restrict__ out_ids,
+                   int32_t *__restrict__ status) {
     constexpr bool FP = WT != GS_W_U8;
     __shared__ SelStatic sst;
     SelShared sh = sel_view(sst, k);
     __shared__ uint32_t s_m;
-    const int q = blockIdx.x;
+    const int q = blockIdx.x;                 // slot
+    const int row = perm ? perm[q] : q;       // query: output row
     const uint32_t n = cnt[q];
     if (n > (uint32_t)cap || n < (uint32_t)k) {
         if (threadIdx.x == 0) {
-            status[q] = GS_ROW_DENSE;
+            status[row] = GS_ROW_DENSE;
             if (FP) resc_cnt[q] = 0;
         }
         return;
@@ -952,17 +1048,17 @@ __global__ void __launch_bounds__(kSelThreads)
     block_topk<32>(src, k, sh, false);
     if (!FP) {
         for (int i = threadIdx.x; i < k; i += blockDim.x) {
-            reinterpret_cast<int32_t *>(out_scores)[(int64_t)q * k + i] = (int32_t)sh.key[i];
-            out_ids[(int64_t)q * k + i] = (int64_t)sh.doc[i];
+            reinterpret_cast<int32_t *>(out_scores)[(int64_t)row * k + i] = (int32_t)sh.key[i];
+            out_ids[(int64_t)row * k + i] = (int64_t)sh.doc[i];
         }
-        if (threadIdx.x == 0) status[q] = GS_ROW_DONE;
+        if (threadIdx.x == 0) status[row] = GS_ROW_DONE;
         return;
     }
     const uint32_t kth = (uint32_t)sh.key[k - 1];
     const uint32_t mf = mfix[q];
     if (kth <= mf) {  // k-th score not clear of zero by the margin
         if (threadIdx.x == 0) {
-            status[q] = GS_ROW_DENSE;
+            status[row] = GS_ROW_DENSE;
             resc_cnt[q] = 0;
         }
         return;
@@ -982,10 +1078,10 @@ __global__ void __launch_bounds__(kSelThreads)
     if (threadIdx.x == 0) {
         const uint32_t m = s_m;
         if (m > (uint32_t)resc_cap) {
-            status[q] = GS_ROW_DENSE;
+            status[row] = GS_ROW_DENSE;
             resc_cnt[q] = 0;
         } else {
-            status[q] = GS_ROW_DONE;
+            status[row] = GS_ROW_DONE;
             resc_cnt[q] = m;
         }
     }
@@ -1182,17 +1278,18 @@ template <int WT>
 __global__ void __launch_bounds__(kSelThreads)
     k_select_final(const uint32_t *__restrict__ resc_doc, const uint64_t *__restrict__ resc_key,
                    const uint32_t *__restrict__ resc_cnt, int32_t resc_cap, int32_t k,
-                   const int32_t *__restrict__ status, float *__restrict__ out_scores,
-                   int64_t *__restrict__ out_ids) {
+                   const int32_t *__restrict__ perm, const int32_t *__restrict__ status,
+                   float *__restrict__ out_scores, int64_t *__restrict__ out_ids) {
     __shared__ SelStatic sst;
     SelShared sh = sel_view(sst, k);
-    const int q = blockIdx.x;
-    if (status[q] != GS_ROW_DONE) return;
+    const int q = blockIdx.x;            // slot
+    const int row = perm ? perm[q] : q;  // query: output row
+    if (status[row] != GS_ROW_DONE) return;
     SrcCand64 src{resc_key + (int64_t)q * resc_cap, resc_doc + (int64_t)q * resc_cap, (int64_t)resc_cnt[q]};
     block_topk<64>(src, k, sh, false);
     for (int i = threadIdx.x; i < k; i += blockDim.x) {
-        out_scores[(int64_t)q * k + i] = (float)gs_unkey_f64(sh.key[i]);
-        out_ids[(int64_t)q * k + i] = (int64_t)sh.doc[i];
+        out_scores[(int64_t)row * k + i] = (float)gs_unkey_f64(sh.key[i]);
+        out_ids[(int64_t)row * k + i] = (int64_t)sh.doc[i];
     }
 }
 
@@ -1285,6 +1382,8 @@ struct SearchPlan {
     float *scale;
     uint32_t *mfix, *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key, *resc_doc, *resc_cnt;
     uint64_t *resc_key;
+    int32_t *perm, *qt_p;  // query order of the scoring groups and the queries in that order
+    void *qw_p;
 };
 
 int check_index(const gs_index *ix) {
@@ -1359,6 +1458,9 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.u_ebeg = ar.take<int32_t>((size_t)p.n_groups * (p.ecap + 1));
     p.u_count = ar.take<int32_t>((size_t)p.n_groups);
     p.e_sw = ar.take<uint2>((size_t)p.n_groups * p.ecap);
+    p.perm = ar.take<int32_t>((size_t)B);
+    p.qt_p = ar.take<int32_t>((size_t)B * T);
+    p.qw_p = ar.take<float>((size_t)B * T);  // room for fp32 or uint8 query weights
     return p;
 }
 
@@ -1398,6 +1500,20 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     };
     int rc = phase(0);
     if (rc) return rc;
+    // Scoring groups take queries that share frequent terms when the index names
+    // them (heavy_d): the queries are copied in slot order and every kernel below
+    // works on slots; outputs and status go to the query's own row.
+    const int32_t *perm = nullptr;
+    if (ix->heavy_d && !(o && o->batch_order) && p.G > 1 && B > p.G) {
+        const int NB = p.G * (1024 / p.G);
+        k_group_order<<<(B + NB - 1) / NB, 1024, 0, s>>>(qt, B, T, ix->vocab, ix->heavy_d, p.G, p.perm);
+        k_permute_queries<WT><<<gs_blocks((int64_t)B * T, 256, 4096), 256, 0, s>>>(qt, qw, p.perm, B, T, p.qt_p,
+                                                                                     p.qw_p);
+        GS_CHECK_LAUNCH();
+        perm = p.perm;
+        qt = p.qt_p;
+        qw = p.qw_p;
+    }
     // the fused scorer reads the packed copy when it was made for this tile size
     const void *pk = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2 ? ix->packed_d : nullptr;
     const int32_t pkf = pk && WT != GS_W_U8 ? 1 : 0;  // integer products of the packed float weights
@@ -1484,7 +1600,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     const size_t sel_lds = sel_lds_bytes(k);
     GS_CHECK_HIP(sel_attr((const void *)k_select_cands<WT>, sel_lds));
     k_select_cands<WT><<<B, kSelThreads, sel_lds, s>>>(p.cand_doc, p.cand_key, p.cnt, p.cap, k, p.mfix, p.resc_doc,
-                                                 p.resc_cnt, p.rcap, out_scores, out_ids, status);
+                                                 p.resc_cnt, p.rcap, perm, out_scores, out_ids, status);
     GS_CHECK_LAUNCH();
     if ((rc = phase(4))) return rc;
     if (FP) {
@@ -1503,8 +1619,8 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     if ((rc = phase(5))) return rc;
     if (FP) {
         GS_CHECK_HIP(sel_attr((const void *)k_select_final<WT>, sel_lds));
-        k_select_final<WT><<<B, kSelThreads, sel_lds, s>>>(p.resc_doc, p.resc_key, p.resc_cnt, p.rcap, k, status,
-                                                     reinterpret_cast<float *>(out_scores), out_ids);
+        k_select_final<WT><<<B, kSelThreads, sel_lds, s>>>(p.resc_doc, p.resc_key, p.resc_cnt, p.rcap, k, perm,
+                                                           status, reinterpret_cast<float *>(out_scores), out_ids);
         GS_CHECK_LAUNCH();
     }
     return phase(6);

@@ -22,7 +22,7 @@ GS_W_F32, GS_W_F16, GS_W_U8 = 0, 1, 2
 GS_ROW_DONE, GS_ROW_DENSE = 0, 1
 GS_SEARCH_PHASES = 7
 PHASE_NAMES = ("query_prep", "threshold_seed", "scoring", "candidate_select", "fp64_rescore", "final_sort")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 WTYPE_OF_DTYPE = {torch.float32: GS_W_F32, torch.float16: GS_W_F16, torch.uint8: GS_W_U8}
 
@@ -50,7 +50,10 @@ class GsIndex(C.Structure):
         ("packed_d", C.c_void_p),
         ("packed_tile_log2", C.c_int32),
         ("packed_shift", C.c_int32),
+        ("heavy_d", C.c_void_p),
     ]
+
+HEAVY_TERMS = 64  # GS_HEAVY_TERMS
 
 
 class GsSearchOpts(C.Structure):
@@ -65,6 +68,7 @@ class GsSearchOpts(C.Structure):
         ("ev_score_end", C.c_void_p),
         ("tiles_per_wg", C.c_int32),
         ("ev_phases", C.POINTER(C.c_void_p)),
+        ("batch_order", C.c_int32),
     ]
 
 
@@ -116,6 +120,7 @@ SIGNATURES = {
     "gs_forward_fill": (C.c_int, [_P, _P, _I32, _P, _P, _I32, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
     "gs_pack_postings": (C.c_int, [_P, _P, _I32, _I64, _I32, _I32, _P, _P]),
     "gs_pack_shift": (C.c_int, [C.c_float, C.POINTER(C.c_int32)]),
+    "gs_heavy_terms": (C.c_int, [_P, _I32, _P, _P]),
     "gs_search_workspace": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts),
                                       C.POINTER(_SZ)]),
     "gs_search_plan": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts),

@@ -322,8 +322,20 @@ def list_max_abs(index) -> torch.Tensor:
     return a["max_abs"]
 
 
+def heavy_terms(index) -> torch.Tensor:
+    """The index's 64 longest posting lists (gs_heavy_terms), int32 term ids by
+    (length desc, term asc), -1 past the non-empty lists; gs_search groups the
+    queries of a batch by which of these terms they hold."""
+    dev = _device_of(index)
+    out = torch.empty(_lib.HEAVY_TERMS, dtype=torch.int32, device=dev)
+    _lib.check(_lib.lib().gs_heavy_terms(_lib.ptr(index.lengths), int(index.vocab_size), _lib.ptr(out),
+                                         _lib.stream_ptr(dev)), "gs_heavy_terms")
+    return out
+
+
 def ensure_search_state(index, tile_log2: int | None = None, forward: bool = True) -> dict:
-    """Derived arrays gs_search needs: max |w|, duplicate counts, tile bounds, the
+    """Derived arrays gs_search needs: max |w|, duplicate counts, the most frequent
+    terms (query grouping), tile bounds, the
     packed scoring copy for this tile size (skipped when the GPU has no room for it
     or a weight is not finite: the scorer then reads the index arrays, with the
     same results), and for
@@ -339,6 +351,8 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
     if "dup" not in a:
         require_ascending(index)
     list_max_abs(index)
+    if "heavy" not in a:
+        a["heavy"] = heavy_terms(index)
     key = ("tile_bounds", tile_log2)
     if key not in a:
         N = int(index.num_docs)
@@ -421,6 +435,7 @@ def gs_index_struct(index, tile_log2: int | None = None) -> _lib.GsIndex:
     fwd = a.get("fwd")
     if fwd is not None:
         s.fwd_ptr_d, s.fwd_terms_d, s.fwd_weights_d = (t.data_ptr() for t in fwd)
+    s.heavy_d = a["heavy"].data_ptr()
     pk = a.get(("packed", tile_log2))
     if pk is not None:
         s.packed_d, s.packed_tile_log2, s.packed_shift = pk.words.data_ptr(), tile_log2, pk.shift

@@ -82,7 +82,8 @@ def _dense_rows(index, gidx, qt, qw, k, rows, out_s, out_i, dense_budget):
 
 def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, path: str = "auto",
            sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 0, waves: int = 0,
-           tiles_per_wg: int = 0, dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None):
+           tiles_per_wg: int = 0, dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None,
+           batch_order: bool = False):
     """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
 
     tile_log2: doc-tile size of the scorer (default: index.default_tile_log2).
@@ -91,7 +92,9 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     fused scoring kernel ("score_kernel") and the whole gs_search call ("search"),
     the GS_SEARCH_PHASES events of each call ("phases": start, query prep,
     threshold seed, scoring, candidate selection, fp64 rescoring, final sort) and
-    the number of rows finished by the dense path ("dense_rows")."""
+    the number of rows finished by the dense path ("dense_rows").
+    batch_order: score queries in groups of consecutive queries instead of groups of
+    queries sharing frequent terms (same results; for comparisons)."""
     dev = _lib.require_gpu(_device_of(index))
     N = int(index.num_docs)
     kk = min(int(k), N)
@@ -123,6 +126,7 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
         _dense_rows(index, gidx, qt, qw, kk, None, out_s, out_i, max(dense_budget, 1))
         return out_s, out_i
     opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, waves, None, None, tiles_per_wg)
+    opts.batch_order = int(bool(batch_order))
     need = _lib.C.c_size_t()
     _lib.check(L.gs_search_workspace(_lib.C.byref(gidx), B, T, kk, _lib.C.byref(opts), _lib.C.byref(need)),
                "gs_search_workspace")

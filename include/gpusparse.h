@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 5
+#define GS_ABI_VERSION 6
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -69,7 +69,11 @@ typedef struct gs_index {
     int32_t packed_tile_log2;     /* the tile size packed_d was made for; used only when it equals
                                      tile_log2 */
     int32_t packed_shift;         /* the w_shift packed_d was made with (float weights) */
+    const int32_t *heavy_d;       /* optional [GS_HEAVY_TERMS] most frequent terms (gs_heavy_terms):
+                                     gs_search then groups queries that share them; NULL: batch order */
 } gs_index;
+
+#define GS_HEAVY_TERMS 64
 
 /* Tuning knobs of gs_search; zero selects the default. */
 typedef struct gs_search_opts {
@@ -88,6 +92,8 @@ typedef struct gs_search_opts {
                               recorded on `stream` at the phase boundaries of gs_search: start,
                               query prep, threshold seed, scoring, candidate selection, fp64
                               rescoring, final sort; may be NULL */
+    int32_t batch_order;   /* 1: score queries in groups of consecutive queries even when the
+                              index has heavy_d (default 0: group by shared frequent terms) */
 } gs_search_opts;
 
 #define GS_SEARCH_PHASES 7
@@ -169,6 +175,12 @@ int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wty
  * tile_log2 <= 14; w_shift in [-200, 200] (ignored for GS_W_U8). */
 int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, int64_t n_slots,
                      int32_t tile_log2, int32_t w_shift, void *out_d, void *stream);
+/* The GS_HEAVY_TERMS non-empty posting lists with the most postings (no
+ * counterpart in the reference: gs_search's query grouping reads them), as term
+ * ids by (length descending, term ascending); -1 past the number of non-empty
+ * lists.  lengths_d int32 [vocab] (gs_index.lengths_d), heavy_d int32
+ * [GS_HEAVY_TERMS]. */
+int gs_heavy_terms(const int32_t *lengths_d, int32_t vocab, int32_t *heavy_d, void *stream);
 /* Weight scale of a packed copy of float weights: the largest `shift` with
  * max_abs * 2^shift <= 8191, for max_abs = the largest |weight| of the index (0 for
  * max_abs == 0).  GS_EINVAL for a negative or non-finite max_abs. */

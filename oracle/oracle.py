@@ -14,6 +14,7 @@ products, exhaustive sorting, closed forms):
   chunk_bounds           pinned: linear scan per list + partition invariant
   forward_index          pinned: the CSR rows sorted stably by column
   tile_bounds            pinned: linear scan per list
+  heavy_terms            pinned: Python sorted() over all terms on small vocabularies
   pack_shift             pinned: closed forms at powers of two and scaled cases
   pack_postings          pinned: per-slot decoding + a scalar loop with exact
                          rational rounding (fractions.Fraction, half to even)
@@ -108,6 +109,17 @@ def tile_bounds(index: dict, tile_log2: int) -> np.ndarray:
     for t in range(V):
         o, n = int(index["offsets"][t]), int(index["lengths"][t])
         out[t] = np.searchsorted(index["doc_ids"][o:o + n], edges, side="left")
+    return out
+
+
+def heavy_terms(lengths, n: int = 64) -> np.ndarray:
+    """gs_heavy_terms (no reference counterpart): the n non-empty posting lists
+    with the most postings, as term ids by (length desc, term asc), -1 padded."""
+    L = np.asarray(lengths, dtype=np.int64)
+    nz = np.nonzero(L > 0)[0]
+    order = nz[np.lexsort((nz, -L[nz]))][:n]
+    out = np.full(n, -1, np.int32)
+    out[:len(order)] = order
     return out
 
 

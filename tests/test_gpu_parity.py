@@ -314,6 +314,42 @@ def test_search_plan_reports_defaults(c1, c3_small):
     assert gs.search_plan(ix16, 24, ti16.shape[1], 1000, sample_tiles=3, unroll=4)["seed_tiles"] == 3
 
 
+@pytest.mark.parametrize("vocab,seed", [(20, 0), (65, 1), (3000, 2), (30522, 3)])
+def test_heavy_terms_matches_oracle(device, vocab, seed):
+    from gpusparse.index import heavy_terms
+    rng = np.random.default_rng(seed)
+    print(f"heavy terms vocab={vocab}", flush=True)
+    csr = random_csr(rng, 4000, vocab, max_len=12, dtype=np.float32)
+    ix = gs.build_index(csr, device)
+    assert np.array_equal(heavy_terms(ix).cpu().numpy(), O.heavy_terms(ix.lengths.cpu().numpy()))
+
+
+@pytest.mark.parametrize("B,k", [(24, 1000), (7, 10)])
+def test_grouped_queries_equal_batch_order(c3_small, B, k):
+    """Scoring groups of queries that share frequent terms (the default) and of
+    consecutive queries give the same, oracle, answer."""
+    ix, ref, ti, tw = c3_small
+    ti, tw = ti[:B], tw[:B]
+    print(f"grouped vs batch order B={B} k={k}", flush=True)
+    s0, i0 = assert_search_equal(ix, ref, ti, tw, k, path="fused")
+    s1, i1 = assert_search_equal(ix, ref, ti, tw, k, path="fused", batch_order=True)
+    assert np.array_equal(i0, i1) and np.array_equal(s0, s1)
+
+
+def test_grouped_queries_many_blocks(device):
+    """More queries than one ordering block (1024 at G = 4), a batch that is not a
+    multiple of the group size, and queries repeating terms."""
+    rng = np.random.default_rng(7)
+    csr = random_csr(rng, 6000, 200, max_len=20, dtype=np.float16, dup_rate=0.02)
+    ix = gs.build_index(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = random_queries(rng, 1503, 200, max_len=10)
+    ti[::11, 1] = ti[::11, 0]
+    print("grouped queries, 1503 queries", flush=True)
+    assert gs.search_plan(ix, 1503, ti.shape[1], 20)["group_size"] == 4
+    assert_search_equal(ix, ref, ti, tw, 20, path="fused")
+
+
 @pytest.mark.parametrize("dtype,pattern", [(np.float32, "fine"), (np.float16, "coarse"), (np.float32, "coarse")])
 def test_packed_scores_exact_under_near_ties(device, dtype, pattern):
     """The packed copy holds rounded weights, so many docs share one fixed-point

@@ -104,6 +104,18 @@ def test_tile_bounds_match_linear_scan(tile_log2):
             assert tb[t, j] == next((i for i, d in enumerate(seg) if d >= edge), n)
 
 
+@pytest.mark.parametrize("vocab,seed", [(20, 0), (64, 1), (65, 2), (3000, 3), (30522, 4)])
+def test_heavy_terms_matches_sorted(vocab, seed):
+    """Ties of equal length (lengths drawn from a few values) and empty lists."""
+    rng = np.random.default_rng(seed)
+    lengths = rng.choice([0, 0, 1, 2, 3, 7, 7, 50], size=vocab).astype(np.int32)
+    if vocab > 100:
+        lengths[rng.choice(vocab, 90, replace=False)] = rng.integers(100, 130, 90)
+    want = [t for t in sorted(range(vocab), key=lambda t: (-int(lengths[t]), t)) if lengths[t] > 0][:64]
+    got = O.heavy_terms(lengths)
+    assert got.tolist() == want + [-1] * (64 - len(want))
+
+
 @pytest.mark.parametrize("max_abs,want", [(1.0, 12), (3.0, 11), (8191.0, 0), (8192.0, -1), (0.5, 13),
                                           (1e-3, 22), (0.0, 0), (float(np.finfo(np.float32).max), -116),
                                           (float(np.float32(2.0 ** -149)), 161), (4095.75, 0), (4095.5, 1),
