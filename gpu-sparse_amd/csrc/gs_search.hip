@@ -655,6 +655,14 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     const store_t *wall = reinterpret_cast<const store_t *>(a.w);
     const pk_t *pkd = reinterpret_cast<const pk_t *>(a.pk);
 
+    // the first tile's slices are zeroed while the term loads are in flight
+    auto zero_slices = [&]() {
+        uint4 *z = reinterpret_cast<uint4 *>(acc);
+        const int n16 = (nq << slice_shift) >> 4;
+        for (int i = tid; i < n16; i += kUnionThreads) z[i] = make_uint4(0, 0, 0, 0);
+    };
+    zero_slices();
+
     // A group whose union fits one batch describes its terms in LDS once (term
     // id, list offset, entry range); thread `term` holds the term's bounds in the
     // current tile and loads the next tile's while the current one is scored.
@@ -676,11 +684,9 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     // scoring (tau only rises: an older value admits more candidates, never fewer)
     uint32_t r_tau = 0;
     if (tid < nq) r_tau = gs_load_relaxed(a.tau + grp * a.G + tid);
-    __syncthreads();  // the previous tile's emission is done with the slices
-    {
-        uint4 *z = reinterpret_cast<uint4 *>(acc);
-        const int n16 = (nq << slice_shift) >> 4;
-        for (int i = tid; i < n16; i += kUnionThreads) z[i] = make_uint4(0, 0, 0, 0);
+    if (tile > tile_lo) {
+        __syncthreads();  // the previous tile's emission is done with the slices
+        zero_slices();
     }
 
     for (int b0 = 0; b0 < U; b0 += kUnionBatch) {
@@ -1189,6 +1195,16 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
     store_t *roww = s_rw[w];
     const store_t *wall = reinterpret_cast<const store_t *>(fw);
     const uint32_t stride = gridDim.x * kRescoreWaves;
+    // the query's first 128 terms and weights stay in registers (lane j: terms j
+    // and j + 64) for all of the wave's candidates
+    int32_t qt_r[2];
+    double qw_r[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int j = h * 64 + lane;
+        qt_r[h] = j < T ? qt[(int64_t)q * T + j] : -1;
+        qw_r[h] = j < T ? (double)qw[(int64_t)q * T + j] : 0.0;
+    }
     // this wave's candidates: first + c * stride, c = 0, 1, ...
     for (uint32_t first = blockIdx.x * kRescoreWaves + w; first < m; first += 64 * stride) {
         const int nc = (int)min<uint32_t>(64u, (m - first + stride - 1) / stride);
@@ -1237,7 +1253,7 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
                 int lo = 0;     // the first of them, within the row
                 double wq = 0.0;
                 if (j < T) {
-                    const int32_t t = qt[(int64_t)q * T + j];
+                    const int32_t t = j0 == 0 ? qt_r[0] : j0 == 64 ? qt_r[1] : qt[(int64_t)q * T + j];
                     if ((uint32_t)t < (uint32_t)V) {
                         int len = n;
                         while (len > 0) {
@@ -1250,7 +1266,7 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
                             }
                         }
                         while (lo + cnt_p < n && term_at(lo + cnt_p) == t) ++cnt_p;
-                        wq = (double)qw[(int64_t)q * T + j];
+                        wq = j0 == 0 ? qw_r[0] : j0 == 64 ? qw_r[1] : (double)qw[(int64_t)q * T + j];
                     }
                 }
                 const double p = cnt_p ? wq * (double)gs_weight<WT>::decode(weight_at(lo)) : 0.0;
