@@ -47,7 +47,11 @@ constexpr int64_t kSeedMinDocs = 4096;    // fewest docs of the default first ti
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
 constexpr int64_t kPairMinWgs = 12288;    // paired workgroups (~48 per CU) needed before a workgroup scores two tiles
-constexpr size_t kTileLds = 144 * 1024;  // LDS of the score slices of one scoring workgroup (9 x 4096 docs)
+constexpr size_t kTileLds = 144 * 1024;  // LDS of the fp64 / uint32 row tiles of one dense-path workgroup
+// LDS of the score slices of one fused-scoring workgroup (2 queries x 8192 docs):
+// two such workgroups share a CU, so one's set-up and emission (latency-bound)
+// overlap the other's adds
+constexpr size_t kUnionTileLds = 64 * 1024;
 constexpr int kGroupSortCap = 8192;      // term entries of one query group sorted in LDS
 static_assert(kGroupSortCap < (1 << 15), "union terms pack (entry count << 16 | first entry) into int32");
 // dynamic-LDS cap requested per kernel: 160 KiB per workgroup minus room for static LDS
@@ -587,14 +591,15 @@ struct UnionArgs {
     int32_t cap, k;
 };
 
-constexpr int kUnionThreads = 1024;  // 16 waves
-constexpr int kUnionBatch = 440;     // union terms described in LDS at a time
-constexpr int kEmitChunks = (int)(kTileLds / 4 / 256);  // 256-doc emission chunks of one workgroup
+constexpr int kUnionThreads = 512;  // 8 waves; two workgroups per CU
+constexpr int kUnionBatch = 220;    // union terms described in LDS at a time
+constexpr int kEmitChunks = (int)(kUnionTileLds / 4 / 256);  // 256-doc emission chunks of one workgroup
 
 // LDS bytes of k_score_union besides the G score slices
 constexpr size_t kUnionMetaLds =
     (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 2) * 8 + (size_t)kUnionBatch * 12;
-static_assert(kTileLds + kUnionMetaLds + kStaticLdsBudget <= kLdsPerWg, "scoring workgroup LDS exceeds 160 KiB");
+static_assert(kUnionTileLds + kUnionMetaLds + kStaticLdsBudget <= kLdsPerWg / 2,
+              "two scoring workgroups must fit the 160 KiB of LDS of a CU");
 
 // One workgroup = one doc tile x one query group; the G query slices of the
 // tile live in LDS as int32.  Per batch of union terms, every thread fetches one
@@ -607,7 +612,7 @@ static_assert(kTileLds + kUnionMetaLds + kStaticLdsBudget <= kLdsPerWg, "scoring
 // per posting with the doc's byte offset in a slice and the integer weight,
 // instead of the doc id and weight arrays.
 template <int WT, int UNROLL, bool PK>
-__global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a) {
+__global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArgs a) {
     using W = gs_weight<WT>;
     using store_t = typename W::store_t;
     using pk_t = uint32_t;
@@ -615,7 +620,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     constexpr int NW = kUnionThreads / 64;
 
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    __shared__ int32_t s_scan[17];
+    __shared__ int32_t s_scan[kUnionThreads / 64 + 1];
     __shared__ uint32_t s_thr[32], s_emit[32], s_maxb[32], s_base[32], s_mfix[32];
     __shared__ uint32_t s_off[kEmitChunks], s_ccnt[kEmitChunks];
 
@@ -731,11 +736,11 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
                 s_scan[w] = accs;
                 accs += s;
             }
-            s_scan[16] = accs;
+            s_scan[NW] = accs;
         }
         __syncthreads();
         if (tid < nb) s_cst[tid] = s_scan[wave] + x - nch;
-        const int total = s_scan[16];
+        const int total = s_scan[NW];
         if (tid == 0) s_cst[nb] = total;
         __syncthreads();
 
@@ -910,7 +915,7 @@ __global__ void __launch_bounds__(kUnionThreads) k_score_union(const UnionArgs a
     // its chunk counts at once, one per lane).
     const int cps_log2 = a.tile_log2 - 8;  // 256-doc chunks per slice = 1 << cps_log2
     const int cps = 1 << cps_log2;
-    const int nce = nq << cps_log2;        // <= kEmitChunks (G * TILE <= kTileLds / 4)
+    const int nce = nq << cps_log2;        // <= kEmitChunks (G * TILE <= kUnionTileLds / 4)
     if (tid < nq) s_thr[tid] = emit_threshold(r_tau, s_mfix[tid]);
     __syncthreads();
     auto scan4 = [&](int ch, uint32_t vv[4], bool keep[4], uint64_t mk[4]) {
@@ -1426,9 +1431,9 @@ int default_tiles_per_wg(int tiles, int n_groups) {
 SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, const gs_search_opts *o,
                        gs_arena &ar) {
     SearchPlan p;
-    // queries per group: G int32 slices of one tile fill kTileLds; the group's
+    // queries per group: G int32 slices of one tile fill kUnionTileLds; the group's
     // sorted term entries (next_pow2(G * T) of them) must fit the LDS sort
-    int G = (int)(kTileLds / 4) >> ix->tile_log2;
+    int G = (int)(kUnionTileLds / 4) >> ix->tile_log2;
     if (G > 32) G = 32;
     if (G < 1) G = 1;
     if (G > B) G = B;

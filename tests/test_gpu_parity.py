@@ -302,15 +302,15 @@ def test_search_packed_launch_shapes(c3_small, unroll, tile_log2, tiles_per_wg):
 
 def test_search_plan_reports_defaults(c1, c3_small):
     """The plan of the default fused search: postings from the packed copy in
-    8192-doc tiles, 16 per lane per chunk; 4 queries per group."""
+    8192-doc tiles, 16 per lane per chunk; 2 queries per group (64 KiB of LDS)."""
     ix32, _, ti, _ = c1
     p32 = gs.search_plan(ix32, 32, ti.shape[1], 100)
-    assert p32["tile_log2"] == 13 and p32["packed"] and p32["unroll"] == 16 and p32["group_size"] == 4
+    assert p32["tile_log2"] == 13 and p32["packed"] and p32["unroll"] == 16 and p32["group_size"] == 2
     assert p32["seed_tiles"] >= 1 and p32["tiles_per_wg"] in (1, 2)
-    assert gs.search_plan(ix32, 32, ti.shape[1], 100, tile_log2=12)["group_size"] == 9
+    assert gs.search_plan(ix32, 32, ti.shape[1], 100, tile_log2=12)["group_size"] == 4
     ix16, _, ti16, _ = c3_small
     p16 = gs.search_plan(ix16, 24, ti16.shape[1], 1000)
-    assert p16["tile_log2"] == 13 and p16["packed"] and p16["unroll"] == 16 and p16["group_size"] == 4
+    assert p16["tile_log2"] == 13 and p16["packed"] and p16["unroll"] == 16 and p16["group_size"] == 2
     assert gs.search_plan(ix16, 24, ti16.shape[1], 1000, sample_tiles=3, unroll=4)["seed_tiles"] == 3
 
 
@@ -337,8 +337,8 @@ def test_grouped_queries_equal_batch_order(c3_small, B, k):
 
 
 def test_grouped_queries_many_blocks(device):
-    """More queries than one ordering block (1024 at G = 4), a batch that is not a
-    multiple of the group size, and queries repeating terms."""
+    """More queries than one ordering block (1024 at G = 2), an odd batch (not a
+    multiple of the group size), and queries repeating terms."""
     rng = np.random.default_rng(7)
     csr = random_csr(rng, 6000, 200, max_len=20, dtype=np.float16, dup_rate=0.02)
     ix = gs.build_index(csr, device)
@@ -346,7 +346,7 @@ def test_grouped_queries_many_blocks(device):
     ti, tw = random_queries(rng, 1503, 200, max_len=10)
     ti[::11, 1] = ti[::11, 0]
     print("grouped queries, 1503 queries", flush=True)
-    assert gs.search_plan(ix, 1503, ti.shape[1], 20)["group_size"] == 4
+    assert gs.search_plan(ix, 1503, ti.shape[1], 20)["group_size"] == 2
     assert_search_equal(ix, ref, ti, tw, 20, path="fused")
 
 
