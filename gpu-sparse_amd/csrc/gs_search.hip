@@ -56,7 +56,7 @@ constexpr int kGroupSortCap = 8192;      // term entries of one query group sort
 static_assert(kGroupSortCap < (1 << 15), "union terms pack (entry count << 16 | first entry) into int32");
 // dynamic-LDS cap requested per kernel: 160 KiB per workgroup minus room for static LDS
 constexpr size_t kLdsPerWg = 160 * 1024;     // gfx950 LDS of one workgroup (static + dynamic)
-constexpr size_t kStaticLdsBudget = 2048;    // static LDS allowed next to the largest dynamic request
+constexpr size_t kStaticLdsBudget = 6144;    // static LDS allowed next to the largest dynamic request
 
 // Lets `fn` take all the LDS of a workgroup: 160 KiB minus its static LDS.
 inline hipError_t allow_full_lds(const void *fn) {
@@ -589,11 +589,14 @@ struct UnionArgs {
     uint32_t *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key;
     const uint32_t *mfix;
     int32_t cap, k;
+    int32_t local_k;  // > 0: threshold each slot at its tile's local k-th score too (seed launch)
 };
 
 constexpr int kUnionThreads = 512;  // 8 waves; two workgroups per CU
 constexpr int kUnionBatch = 220;    // union terms described in LDS at a time
 constexpr int kEmitChunks = (int)(kUnionTileLds / 4 / 256);  // 256-doc emission chunks of one workgroup
+constexpr int kLocalBins = 256;  // bins of the per-slot score histogram of the seed launch
+constexpr int kLocalSlots = 4;   // slots per workgroup that get a local threshold
 
 // LDS bytes of k_score_union besides the G score slices
 constexpr size_t kUnionMetaLds =
@@ -622,6 +625,7 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
     extern __shared__ __align__(16) unsigned char lds_raw[];
     __shared__ int32_t s_scan[kUnionThreads / 64 + 1];
     __shared__ uint32_t s_thr[32], s_emit[32], s_maxb[32], s_base[32], s_mfix[32];
+    __shared__ uint32_t s_lhist[kLocalSlots][kLocalBins];
     __shared__ uint32_t s_off[kEmitChunks], s_ccnt[kEmitChunks];
 
     const int tid = threadIdx.x, lane = gs_lane();
@@ -917,6 +921,55 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
     const int cps = 1 << cps_log2;
     const int nce = nq << cps_log2;        // <= kEmitChunks (G * TILE <= kUnionTileLds / 4)
     if (tid < nq) s_thr[tid] = emit_threshold(r_tau, s_mfix[tid]);
+    if (a.local_k > 0 && nq <= kLocalSlots) {
+        // Seed launch (tau = 0): every positive doc would be a candidate.  Any k
+        // docs of this tile scoring >= X bound the query's k-th score from below
+        // by X, so the slot's local k-th score L gives the threshold L - margin.
+        // L is bounded from below by the lower edge of the histogram bin (linear
+        // over (0, slot max]) where the count from the top reaches k.
+        if (tid < nq) s_maxb[tid] = 0;
+        for (int i = tid; i < kLocalSlots * kLocalBins; i += kUnionThreads) (&s_lhist[0][0])[i] = 0;
+        __syncthreads();
+        for (int ch = wave; ch < nce; ch += NW) {
+            const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
+            const int mx = max(max((int32_t)v4.x, (int32_t)v4.y), max((int32_t)v4.z, (int32_t)v4.w));
+            const uint32_t wm = gs_wave_max_u32((uint32_t)max(mx, 0));
+            if (lane == 0 && wm) atomicMax(&s_maxb[ch >> cps_log2], wm);
+        }
+        __syncthreads();
+        for (int ch = wave; ch < nce; ch += NW) {
+            const int g = ch >> cps_log2;
+            const uint64_t span = (uint64_t)s_maxb[g] + 1;
+            const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
+            const uint32_t vs[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if ((int32_t)vs[u] > 0) atomicAdd(&s_lhist[g][(uint64_t)vs[u] * kLocalBins / span], 1u);
+        }
+        __syncthreads();
+        for (int g = wave; g < nq; g += NW) {  // lane l: bins 255 - 4l .. 252 - 4l
+            uint32_t c[4], sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum += (c[j] = s_lhist[g][kLocalBins - 1 - 4 * lane - j]);
+            const uint32_t inc = gs_wave_incl_scan(sum);
+            const uint64_t hit = __ballot(inc >= (uint32_t)a.local_k);
+            if (hit) {
+                const int l = __ffsll((unsigned long long)hit) - 1;
+                if (lane == l) {
+                    uint32_t cum = inc - sum;
+                    int j = 0;
+                    while (cum + c[j] < (uint32_t)a.local_k) cum += c[j++];
+                    const uint64_t b = (uint64_t)(kLocalBins - 1 - 4 * lane - j);
+                    const uint64_t span = (uint64_t)s_maxb[g] + 1;
+                    const uint32_t edge = (uint32_t)((b * span + kLocalBins - 1) / kLocalBins);  // least v of bin b
+                    const uint32_t t = emit_threshold(edge, s_mfix[g]);
+                    if (t > s_thr[g]) s_thr[g] = t;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < nq) s_maxb[tid] = 0;
+    }
     __syncthreads();
     auto scan4 = [&](int ch, uint32_t vv[4], bool keep[4], uint64_t mk[4]) {
         const int g = ch >> cps_log2;
@@ -1606,7 +1659,9 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
             default: return launch_union<WT, 8>(e, s);
         }
     };
+    e.local_k = k;  // seed launch: local k-th score thresholds
     if ((rc = run_union(0, p.S))) return rc;
+    e.local_k = 0;
     k_tau_seed<<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(p.tau, p.maxbin, p.hist, B, k);
     GS_CHECK_LAUNCH();
     if ((rc = phase(2))) return rc;
