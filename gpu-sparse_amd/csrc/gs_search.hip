@@ -758,9 +758,8 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
         // same byte offset register (lane * size, plus an immediate per posting
         // group) and lanes past the chunk's end read 0.
         struct Chunk {
-            int n, m;
-            uint32_t badj; // lane j: LDS byte offset of the j-th entry's slice, minus doc0 * 4
-            uint32_t my_w; // lane j: its scaled query weight
+            int n, m, e0;
+            uint32_t b0, w0, b1, w1;  // the term's first two entries: slice byte offset - doc0 * 4, weight
             int32_t doc[UNROLL];
             store_t wv[UNROLL];
         };
@@ -811,10 +810,17 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
                                              (uint32_t)__builtin_amdgcn_readlane((int)md_p0, j));
                 k.n = __builtin_amdgcn_readlane(md_n, j);
                 k.m = __builtin_amdgcn_readlane(md_m, j);
-                const int e0 = __builtin_amdgcn_readlane(md_e0, j);
-                const uint2 sw = gs_bload64(gs_rsrc(esw + e0, (uint32_t)k.m * 8u), lane * 8);
-                k.badj = (sw.x << slice_shift) - doc0_4;
-                k.my_w = sw.y;
+                // The term's first two (slot, weight) entries arrive in SGPRs by one
+                // scalar load (read-only here; the entry array has one entry of
+                // padding, so the pair never leaves it); further entries are read
+                // one by one in add_entries.
+                k.e0 = __builtin_amdgcn_readlane(md_e0, j);
+                typedef const __attribute__((address_space(4))) uint32_t *const_u32_p;
+                const const_u32_p ep = (const_u32_p)(uintptr_t)(esw + k.e0);
+                k.b0 = (ep[0] << slice_shift) - doc0_4;
+                k.w0 = ep[1];
+                k.b1 = (ep[2] << slice_shift) - doc0_4;
+                k.w1 = ep[3];
                 // The resources start at p0 rounded down to 64 postings; the lane
                 // offset carries the remainder.  It changes per chunk, so it is
                 // computed here and the per-group constants fold into the loads'
@@ -854,9 +860,12 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
             // every entry (query slot) of the chunk's term; the group count is
             // resolved once per chunk, so the entry loop is straight-line adds
             auto add_entries = [&](const Chunk &k, auto ngc) {
-                for (int e = 0; e < k.m; ++e)
-                    add_groups(k, ngc, (uint32_t)__builtin_amdgcn_readlane((int)k.badj, e),
-                               (uint32_t)__builtin_amdgcn_readlane((int)k.my_w, e));
+                add_groups(k, ngc, k.b0, k.w0);
+                if (k.m > 1) add_groups(k, ngc, k.b1, k.w1);
+                for (int e = 2; e < k.m; ++e) {
+                    const uint2 sw = esw[k.e0 + e];
+                    add_groups(k, ngc, (sw.x << slice_shift) - doc0_4, sw.y);
+                }
             };
             auto apply = [&](Chunk &k, int j) {
                 if (k.m > 64) {  // a term held by more than 64 query slots (queries repeating terms)
@@ -1531,7 +1540,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.u_term = ar.take<int32_t>((size_t)p.n_groups * p.ecap);
     p.u_ebeg = ar.take<int32_t>((size_t)p.n_groups * (p.ecap + 1));
     p.u_count = ar.take<int32_t>((size_t)p.n_groups);
-    p.e_sw = ar.take<uint2>((size_t)p.n_groups * p.ecap);
+    p.e_sw = ar.take<uint2>((size_t)p.n_groups * p.ecap + 1);  // + 1: the scorer reads entries in pairs
     p.perm = ar.take<int32_t>((size_t)B);
     p.qt_p = ar.take<int32_t>((size_t)B * T);
     p.qw_p = ar.take<float>((size_t)B * T);  // room for fp32 or uint8 query weights
