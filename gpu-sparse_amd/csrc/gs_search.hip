@@ -614,7 +614,7 @@ static_assert(kUnionTileLds + kUnionMetaLds + kStaticLdsBudget <= kLdsPerWg / 2,
 // PK: postings come from the packed scoring copy (gs_pack_postings): one word
 // per posting with the doc's byte offset in a slice and the integer weight,
 // instead of the doc id and weight arrays.
-template <int WT, int UNROLL, bool PK>
+template <int WT, int UNROLL, bool PK, bool SE>
 __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArgs a) {
     using W = gs_weight<WT>;
     using store_t = typename W::store_t;
@@ -759,7 +759,8 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
         // group) and lanes past the chunk's end read 0.
         struct Chunk {
             int n, m, e0;
-            uint32_t b0, w0, b1, w1;  // the term's first two entries: slice byte offset - doc0 * 4, weight
+            uint32_t b0, w0, b1, w1;  // SE: the term's first two entries: slice byte offset - doc0 * 4, weight
+            uint32_t badj, my_w;      // !SE: lane j: the j-th entry's slice byte offset - doc0 * 4, weight
             int32_t doc[UNROLL];
             store_t wv[UNROLL];
         };
@@ -810,17 +811,25 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
                                              (uint32_t)__builtin_amdgcn_readlane((int)md_p0, j));
                 k.n = __builtin_amdgcn_readlane(md_n, j);
                 k.m = __builtin_amdgcn_readlane(md_m, j);
-                // The term's first two (slot, weight) entries arrive in SGPRs by one
-                // scalar load (read-only here; the entry array has one entry of
-                // padding, so the pair never leaves it); further entries are read
-                // one by one in add_entries.
                 k.e0 = __builtin_amdgcn_readlane(md_e0, j);
-                typedef const __attribute__((address_space(4))) uint32_t *const_u32_p;
-                const const_u32_p ep = (const_u32_p)(uintptr_t)(esw + k.e0);
-                k.b0 = (ep[0] << slice_shift) - doc0_4;
-                k.w0 = ep[1];
-                k.b1 = (ep[2] << slice_shift) - doc0_4;
-                k.w1 = ep[3];
+                if constexpr (SE) {
+                    // Groups of at most 4 slots: the term's first two (slot, weight)
+                    // entries arrive in SGPRs by one scalar load (read-only here; the
+                    // entry array has one entry of padding, so the pair never leaves
+                    // it); further ones are read one by one in add_entries.
+                    typedef const __attribute__((address_space(4))) uint32_t *const_u32_p;
+                    const const_u32_p ep = (const_u32_p)(uintptr_t)(esw + k.e0);
+                    k.b0 = (ep[0] << slice_shift) - doc0_4;
+                    k.w0 = ep[1];
+                    k.b1 = (ep[2] << slice_shift) - doc0_4;
+                    k.w1 = ep[3];
+                } else {
+                    // larger groups: lane j loads entry j (a scalar load per entry
+                    // would wait on the LDS adds issued before it)
+                    const uint2 sw = gs_bload64(gs_rsrc(esw + k.e0, (uint32_t)k.m * 8u), lane * 8);
+                    k.badj = (sw.x << slice_shift) - doc0_4;
+                    k.my_w = sw.y;
+                }
                 // The resources start at p0 rounded down to 64 postings; the lane
                 // offset carries the remainder.  It changes per chunk, so it is
                 // computed here and the per-group constants fold into the loads'
@@ -860,11 +869,17 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
             // every entry (query slot) of the chunk's term; the group count is
             // resolved once per chunk, so the entry loop is straight-line adds
             auto add_entries = [&](const Chunk &k, auto ngc) {
-                add_groups(k, ngc, k.b0, k.w0);
-                if (k.m > 1) add_groups(k, ngc, k.b1, k.w1);
-                for (int e = 2; e < k.m; ++e) {
-                    const uint2 sw = esw[k.e0 + e];
-                    add_groups(k, ngc, (sw.x << slice_shift) - doc0_4, sw.y);
+                if constexpr (SE) {
+                    add_groups(k, ngc, k.b0, k.w0);
+                    if (k.m > 1) add_groups(k, ngc, k.b1, k.w1);
+                    for (int e = 2; e < k.m; ++e) {
+                        const uint2 sw = esw[k.e0 + e];
+                        add_groups(k, ngc, (sw.x << slice_shift) - doc0_4, sw.y);
+                    }
+                } else {
+                    for (int e = 0; e < k.m; ++e)
+                        add_groups(k, ngc, (uint32_t)__builtin_amdgcn_readlane((int)k.badj, e),
+                                   (uint32_t)__builtin_amdgcn_readlane((int)k.my_w, e));
                 }
             };
             auto apply = [&](Chunk &k, int j) {
@@ -1441,10 +1456,16 @@ int launch_dense(DenseArgs a, int waves, hipStream_t s) {
 template <int WT, int UNROLL>
 int launch_union(UnionArgs e, hipStream_t s) {
     static std::atomic<bool> attr{false};
-    auto fn = e.pk ? k_score_union<WT, UNROLL, true> : k_score_union<WT, UNROLL, false>;
+    // scalar entry loads for groups of up to 4 slots (terms then have at most
+    // 4 entries unless queries repeat terms)
+    const bool se = e.G <= 4;
+    auto fn = e.pk ? (se ? k_score_union<WT, UNROLL, true, true> : k_score_union<WT, UNROLL, true, false>)
+                   : (se ? k_score_union<WT, UNROLL, false, true> : k_score_union<WT, UNROLL, false, false>);
     if (!attr.load()) {
-        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, true>));
-        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, false>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, true, true>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, true, false>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, false, true>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, false, false>));
         attr.store(true);
     }
     const size_t lds = ((size_t)e.G << (e.tile_log2 + 2)) + kUnionMetaLds;
