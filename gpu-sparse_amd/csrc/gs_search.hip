@@ -752,10 +752,11 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
         // term inside the tile; wave w takes chunks w, w + NW, ...  Each wave first
         // describes its next 64 chunks, one per lane (term found by binary search
         // over the chunk scan), so the loop itself reads no LDS: chunk fields come
-        // from v_readlane, and the postings and the term's (slot, weight) entries
-        // come from buffer loads issued two chunks ahead.  The loads go through
-        // per-chunk buffer resources sized to the chunk, so every lane uses the
-        // same byte offset register (lane * size, plus an immediate per posting
+        // from v_readlane, and the postings come from buffer loads issued one chunk
+        // ahead (the term's (slot, weight) entries from scalar loads, or for groups
+        // of more than 4 queries a buffer load, issued with them).  The loads go
+        // through per-chunk buffer resources sized to the chunk, so every lane uses
+        // the same byte offset register (lane * size, plus an immediate per posting
         // group) and lanes past the chunk's end read 0.
         struct Chunk {
             int n, m, e0;
