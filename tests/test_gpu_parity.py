@@ -399,6 +399,24 @@ def test_search_u8_config_reduced(device):
     assert_search_equal(ix, ref, ti, tw, 1000, path="fused")
 
 
+@pytest.mark.parametrize("tile_log2", [10, 12, 13])
+def test_search_queries_repeating_terms(device, tile_log2):
+    """Queries that repeat a term: every occurrence adds its own product, as in
+    the reference's scatter-add, so a term can have more (slot, weight) entries
+    than its query group has queries (groups of 16, 4 and 2 queries here)."""
+    rng = np.random.default_rng(31)
+    csr = random_csr(rng, 30000, 40, max_len=12)
+    ix = gs.build_index(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = random_queries(rng, 24, 40, max_len=6)
+    # column 0 three times, columns 1 and 2 twice, with other weights
+    ti = np.ascontiguousarray(np.concatenate([ti, ti[:, :3], ti[:, :1]], axis=1))
+    tw = np.ascontiguousarray(np.concatenate([tw, tw[:, :3] * 0.5, tw[:, :1] * 2.0], axis=1).astype(np.float32))
+    print(f"repeated query terms tile_log2={tile_log2} T={ti.shape[1]}", flush=True)
+    for k in (10, 300):
+        assert_search_equal(ix, ref, ti, tw, k, path="fused", tile_log2=tile_log2)
+
+
 @pytest.mark.parametrize("tile_log2,tiles_per_wg", [(8, 0), (10, 0), (12, 0), (13, 0), (10, 4), (13, 2)])
 def test_search_head_heavy_reduced(device, tile_log2, tiles_per_wg):
     """Wide head-heavy queries: group unions above one LDS batch of terms."""
