@@ -1270,6 +1270,7 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
     constexpr int RU = kRowStage / 64;
     __shared__ int32_t s_row[kRescoreWaves][kRowStage];
     __shared__ store_t s_rw[kRescoreWaves][kRowStage];
+    __shared__ double s_prod[kRescoreWaves][64];
     const int q = blockIdx.y;
     const uint32_t m = resc_cnt[q];
     const int lane = gs_lane();
@@ -1355,6 +1356,21 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
                 const double p = cnt_p ? wq * (double)gs_weight<WT>::decode(weight_at(lo)) : 0.0;
                 uint64_t hit = __ballot(cnt_p > 0);
                 const uint64_t dup = __ballot(cnt_p > 1);
+                if (!dup) {
+                    // The hits' products, compacted into LDS in lane order, are
+                    // added in that order by every lane: the same additions as
+                    // reading them lane by lane, at one broadcast LDS read and one
+                    // add per hit.
+                    double *prod = s_prod[w];
+                    const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(hit >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)hit, 0u));
+                    if (cnt_p > 0) prod[pos] = p;
+                    gs_wave_sync();
+                    const int nh = __popcll(hit);
+                    for (int i = 0; i < nh; ++i) s += prod[i];
+                    gs_wave_sync();  // read before the next block's products are written
+                    continue;
+                }
                 while (hit) {
                     const int l = __ffsll((unsigned long long)hit) - 1;
                     hit &= hit - 1;
