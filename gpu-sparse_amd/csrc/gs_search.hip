@@ -787,6 +787,11 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
             const int nmine = min(64, (total - cb + NW - 1) / NW);  // chunks of this wave in the block
             int64_t md_p0 = 0;
             int md_n = 0, md_e0 = 0, md_m = 0;
+            // packed copy: lane c also holds its chunk's load window as the
+            // fetch needs it (base address of the 64-posting-aligned window, the
+            // chunk's offset in it, its posting and entry counts), so the fetch
+            // does no 64-bit address arithmetic
+            uint32_t md_blo = 0, md_bx = 0, md_nm = 0;
             {
                 const int c = cb + lane * NW;
                 if (c < total) {
@@ -801,6 +806,13 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
                     md_n = min(CH, s_len[lo] - ci * CH);
                     md_e0 = s_e[lo] & 0xFFFF;
                     md_m = s_e[lo] >> 16;
+                    if constexpr (PK) {
+                        const int64_t pb = md_p0 & ~int64_t(63);
+                        const uint64_t addr = (uint64_t)(uintptr_t)(pkd + pb);  // < 2^48
+                        md_blo = (uint32_t)addr;
+                        md_bx = (uint32_t)(addr >> 32) | ((uint32_t)(md_p0 - pb) << 16);
+                        md_nm = (uint32_t)md_n | ((uint32_t)md_m << 16);
+                    }
                 }
             }
             // byte address of doc d in the slice at LDS offset `base`: (d << 2) +
@@ -808,6 +820,27 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
             // packed postings carry (d - doc0) << 2 already
             const uint32_t doc0_4 = PK ? 0u : (uint32_t)doc0 << 2;
             auto fetch = [&](int j, Chunk &k) {
+                if constexpr (PK && SE) {
+                    const uint32_t blo = (uint32_t)__builtin_amdgcn_readlane((int)md_blo, j);
+                    const uint32_t bx = (uint32_t)__builtin_amdgcn_readlane((int)md_bx, j);
+                    const uint32_t nm = (uint32_t)__builtin_amdgcn_readlane((int)md_nm, j);
+                    k.n = (int)(nm & 0xFFFFu);
+                    k.m = (int)(nm >> 16);
+                    k.e0 = __builtin_amdgcn_readlane(md_e0, j);
+                    typedef const __attribute__((address_space(4))) uint32_t *const_u32_p;
+                    const const_u32_p ep = (const_u32_p)(uintptr_t)(esw + k.e0);
+                    k.b0 = ep[0] << slice_shift;
+                    k.w0 = ep[1];
+                    k.b1 = ep[2] << slice_shift;
+                    k.w1 = ep[3];
+                    const int sh = (int)(bx >> 16);
+                    const pk_t *base = reinterpret_cast<const pk_t *>((uintptr_t)(((uint64_t)(bx & 0xFFFFu) << 32) | blo));
+                    const auto rp = gs_rsrc(base, (uint32_t)(sh + k.n) * (uint32_t)sizeof(pk_t));
+                    const int o_p = (lane + sh) * (int)sizeof(pk_t);
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u) k.doc[u] = (int32_t)gs_bload32(rp, o_p + u * 256);
+                    return;
+                }
                 const int64_t p0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(md_p0 >> 32), j) << 32) |
                                              (uint32_t)__builtin_amdgcn_readlane((int)md_p0, j));
                 k.n = __builtin_amdgcn_readlane(md_n, j);
