@@ -820,19 +820,25 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
             // packed postings carry (d - doc0) << 2 already
             const uint32_t doc0_4 = PK ? 0u : (uint32_t)doc0 << 2;
             auto fetch = [&](int j, Chunk &k) {
-                if constexpr (PK && SE) {
+                if constexpr (PK) {
                     const uint32_t blo = (uint32_t)__builtin_amdgcn_readlane((int)md_blo, j);
                     const uint32_t bx = (uint32_t)__builtin_amdgcn_readlane((int)md_bx, j);
                     const uint32_t nm = (uint32_t)__builtin_amdgcn_readlane((int)md_nm, j);
                     k.n = (int)(nm & 0xFFFFu);
                     k.m = (int)(nm >> 16);
                     k.e0 = __builtin_amdgcn_readlane(md_e0, j);
-                    typedef const __attribute__((address_space(4))) uint32_t *const_u32_p;
-                    const const_u32_p ep = (const_u32_p)(uintptr_t)(esw + k.e0);
-                    k.b0 = ep[0] << slice_shift;
-                    k.w0 = ep[1];
-                    k.b1 = ep[2] << slice_shift;
-                    k.w1 = ep[3];
+                    if constexpr (SE) {  // entries as in the general path below (packed: doc0_4 = 0)
+                        typedef const __attribute__((address_space(4))) uint32_t *const_u32_p;
+                        const const_u32_p ep = (const_u32_p)(uintptr_t)(esw + k.e0);
+                        k.b0 = ep[0] << slice_shift;
+                        k.w0 = ep[1];
+                        k.b1 = ep[2] << slice_shift;
+                        k.w1 = ep[3];
+                    } else {
+                        const uint2 sw = gs_bload64(gs_rsrc(esw + k.e0, (uint32_t)k.m * 8u), lane * 8);
+                        k.badj = sw.x << slice_shift;
+                        k.my_w = sw.y;
+                    }
                     const int sh = (int)(bx >> 16);
                     const pk_t *base = reinterpret_cast<const pk_t *>((uintptr_t)(((uint64_t)(bx & 0xFFFFu) << 32) | blo));
                     const auto rp = gs_rsrc(base, (uint32_t)(sh + k.n) * (uint32_t)sizeof(pk_t));
