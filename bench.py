@@ -8,18 +8,24 @@ and the status check.  Inputs (index and query batch) are resident in HBM before
 the timed region.
 
 Prints one JSON line.  ``roofline`` is for the dominant kernel (the fused tile
-scoring kernel), timed with HIP events on its launch stream: algorithmic bytes =
-sum over queries and valid terms of the postings that launch streams x (4 B doc
-id + weight bytes).  ``cpu_baseline`` times the reference CPU path
-(cpu_sequential_score, restated in C) on a bounded sample of the same batch,
-pinned to C cores.
+scoring kernel), timed with HIP events on its launch stream.  Its unit of work
+is one scored posting (a (query, posting of a valid query term) pair), which is
+one LDS atomic add, and its bound is the LDS atomic rate measured on the same
+GPU type (profiles/lds_atomic_rates.json).  Beside it: the physical HBM bytes
+per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated by a copy kernel;
+profiles/traffic_k_score_union_<config>.json) as a fraction of 8 TB/s, and the
+reference kernel's stream (4 B doc id + weight bytes per scored posting) as a
+labelled equivalent.  ``selection`` and ``index_build`` give bytes moved over
+time for candidate selection + fp64 rescoring + final sort, and for the device
+index build.  ``cpu_baseline`` times the reference CPU path
+(cpu_sequential_score, restated in C) on a bounded sample of the same batch in
+fresh child processes pinned with taskset and the thread-pool variables.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
-import resource
 import sys
 import time
 
@@ -52,7 +58,9 @@ def parse():
     ap.add_argument("--sample-tiles", type=int, default=0, help="tiles scored with tau = 0 first (0: default)")
     ap.add_argument("--cpu-queries-1", type=int, default=96, help="queries timed on one core")
     ap.add_argument("--cpu-queries-all", type=int, default=512, help="queries timed on all cores")
-    ap.add_argument("--cpu-cores", type=int, default=16, help="cap on the cores of the all-core row")
+    ap.add_argument("--cpu-cores", type=int, default=16,
+                    help="cap on the cores of the all-core row (16: the host-CPU share of one GPU on the "
+                         "GPU boxes; the process's affinity usually lists the whole host)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-queries", type=int, default=4)
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
@@ -61,6 +69,21 @@ def parse():
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run a plain device-to-device copy of this many bytes (PMC counter calibration)")
     return ap.parse_args()
+
+
+def lds_peak():
+    """Measured LDS atomic rate of the MI355X (profiles/lds_atomic_rates.json,
+    written by gpu-sparse_amd/csrc/microbench/lds_atomic_rate.hip): ds_add_u32 on
+    random addresses of a 64 KiB workgroup allocation, in lane-adds/s over the
+    whole GPU.  None when the file is missing."""
+    path = os.path.join(ROOT, "profiles", "lds_atomic_rates.json")
+    try:
+        with open(path) as f:
+            r = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return {"peak": float(r["ds_add_u32_random"]["lane_ops_per_s"]),
+            "source": os.path.relpath(path, ROOT) + ": ds_add_u32, random addresses"}
 
 
 def traffic_file(cfg_name):
@@ -134,38 +157,51 @@ def copy_only(nbytes):
     print(json.dumps({"copy_bytes": n * 4, "launches": 3}), flush=True)
 
 
+THREAD_VARS = ("OMP_NUM_THREADS", "MKL_NUM_THREADS", "OPENBLAS_NUM_THREADS", "NUMEXPR_NUM_THREADS",
+               "RAYON_NUM_THREADS")
+
+
 def cpu_rows(index_h, ti, tw, k, n1, n_all, cap):
-    """Reference CPU path on one core and on `cap` cores: wall, CPU seconds,
-    CPU/wall and queries/s per row.  Pinned with sched_setaffinity (taskset's
-    syscall) and the thread-pool variables."""
-    from oracle import oracle as O
+    """Reference CPU path (cpu_sequential_score restated in C) on one core and on
+    min(cores in this process's affinity, cap) cores.  Each row is a fresh child
+    process, ``taskset -c <cpus> python3 oracle/cpu_baseline.py``, with the
+    thread-pool variables set in its environment before it starts; it never
+    touches the GPU.  The index and queries reach it as .npy files in a
+    temporary directory (/dev/shm when it has room)."""
+    import shutil
+    import subprocess
+    import tempfile
+
+    from oracle.cpu_baseline import save_inputs
     allowed = sorted(os.sched_getaffinity(0))
+    need = sum(index_h[f].nbytes for f in ("doc_ids", "scores", "offsets", "lengths")) + ti.nbytes + tw.nbytes
+    parent = "/dev/shm" if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > 2 * need else None
+    d = tempfile.mkdtemp(prefix="gs_cpu_", dir=parent)
     rows = []
-    for cores, nq in ((1, n1), (min(cap, len(allowed)), n_all)):
-        if nq <= 0:
-            continue
-        nq = min(nq, ti.shape[0])
-        pin = set(allowed[:cores])
-        for v in ("OMP_NUM_THREADS", "MKL_NUM_THREADS", "OPENBLAS_NUM_THREADS", "NUMEXPR_NUM_THREADS",
-                  "RAYON_NUM_THREADS"):
-            os.environ[v] = str(cores)
-        os.sched_setaffinity(0, pin)
-        try:
-            r0 = resource.getrusage(resource.RUSAGE_SELF)
-            t0 = time.perf_counter()
-            O.c_cpu_sequential(index_h, ti[:nq], tw[:nq], k, threads=cores)
-            wall = time.perf_counter() - t0
-            r1 = resource.getrusage(resource.RUSAGE_SELF)
-        finally:
-            os.sched_setaffinity(0, set(allowed))
-        cpu_s = (r1.ru_utime - r0.ru_utime) + (r1.ru_stime - r0.ru_stime)
-        ratio = cpu_s / wall if wall > 0 else 0.0
-        rows.append({"cores": cores, "queries": nq, "wall_s": round(wall, 3), "cpu_s": round(cpu_s, 3),
-                     "cpu_wall_ratio": round(ratio, 3), "qps": round(nq / wall, 3),
-                     "pinning_clean": bool(ratio < 1.35 * cores)})
-        log(f"cpu baseline cores={cores} queries={nq} wall={wall:.2f}s cpu/wall={ratio:.2f} "
-            f"q/s={nq / wall:.2f}")
-    return rows
+    try:
+        save_inputs(d, index_h, ti, tw)
+        for cores, nq in ((1, n1), (min(cap, len(allowed)), n_all)):
+            if nq <= 0:
+                continue
+            cpus = ",".join(str(c) for c in allowed[:cores])
+            env = dict(os.environ)
+            env.update({v: str(cores) for v in THREAD_VARS})
+            cmd = ["taskset", "-c", cpus, sys.executable, os.path.join(ROOT, "oracle", "cpu_baseline.py"),
+                   "--dir", d, "--cores", str(cores), "--k", str(k), "--queries", str(nq)]
+            r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+            if r.returncode != 0:
+                raise RuntimeError(f"CPU baseline child failed ({r.returncode}): {r.stderr[-2000:]}")
+            row = json.loads(r.stdout.strip().splitlines()[-1])
+            row["pinned_cpus"] = row.pop("affinity")
+            row["pinning_clean"] = bool(row["cpu_wall_ratio"] < 1.35 * cores and len(row["pinned_cpus"]) == cores)
+            row["command"] = f"{' '.join(f'{v}={cores}' for v in THREAD_VARS)} taskset -c {cpus} " \
+                             f"python3 oracle/cpu_baseline.py --cores {cores} --k {k} --queries {row['queries']}"
+            rows.append(row)
+            log(f"cpu baseline cores={cores} queries={row['queries']} wall={row['wall_s']:.2f}s "
+                f"cpu/wall={row['cpu_wall_ratio']:.2f} q/s={row['qps']:.2f}")
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return rows, len(allowed)
 
 
 def main():
@@ -210,7 +246,8 @@ def main():
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    index = gs.build_index(docs, dev)
+    build_ev = {}
+    index = gs.build_from_csr(docs, dev, timing=build_ev)
     torch.cuda.synchronize()
     t_build = time.perf_counter() - t0
     t0 = time.perf_counter()
@@ -221,7 +258,7 @@ def main():
     t_bounds = time.perf_counter() - t0
     log(f"index built in {t_build:.2f}s (incl. H2D of the CSR); search state (tile bounds, doc-major copy) "
         f"{t_bounds:.3f}s")
-    qt, qw, T = gs.to_query_tensors(queries, dev)
+    qt, qw, T = gs.to_query_tensors(queries, dev, weight_dtype=None)
     B = qt.shape[0]
     k = min(a.k or cfg.k, docs.shape[0])
     del docs
@@ -246,7 +283,11 @@ def main():
     log(f"{a.steps} steps: {ms_per_step:.2f} ms/step, {qps:.1f} queries/s, "
         f"dense rows {timing.get('dense_rows', 0)}")
 
-    # ---- roofline of the fused tile-scoring kernel
+    # ---- roofline of the fused tile-scoring kernel.  Its unit of work is one
+    # scored posting (a (query, posting) pair of a valid query term), which is one
+    # LDS atomic add into the query's tile slice: the LDS-atomic issue rate bounds
+    # it, not HBM (each posting is fetched once per doc tile and query group and
+    # added to every query of the group holding its term).
     wbytes = index.scores.element_size()
     S = 0
     roof = None
@@ -269,23 +310,79 @@ def main():
         post_launch = int((per_term[tq] * valid).sum())
         post_all = int((all_term[tq] * valid).sum())
         per_post = 4 + wbytes
-        bytes_launch = post_launch * per_post
         avg_ms = float(np.mean(kern_ms))
-        achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4),
-                "traffic": measured_traffic(cfg.name, int(index.num_docs), a.tile_log2),
+        adds_per_s = post_launch / (avg_ms * 1e-3)
+        lds = lds_peak()
+        phys = measured_traffic(cfg.name, int(index.num_docs), a.tile_log2)
+        ref_bytes = post_launch * per_post
+        roof = {"bound": "lds_atomic", "achieved": round(adds_per_s / 1e9, 1),
+                "peak": None if lds is None else round(lds["peak"] / 1e9, 1),
+                "unit": "G LDS atomic adds/s (one per scored posting)",
+                "frac": None if lds is None else round(adds_per_s / lds["peak"], 4),
+                "traffic": phys,
+                "peak_source": None if lds is None else lds["source"],
+                "hbm_physical": None if phys is None else {
+                    "achieved": round(phys / (avg_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(phys / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                    "source": os.path.relpath(traffic_file(cfg.name), ROOT)},
+                "reference_stream_equiv": {
+                    "bytes_per_launch": ref_bytes, "bytes_per_posting": per_post,
+                    "GBs": round(ref_bytes / (avg_ms * 1e-3) / 1e9, 1),
+                    "x_hbm_peak": round(ref_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
+                    "note": "the reference kernel's stream (each posting read once per (query, term): doc id + "
+                            "weight); here each posting is read once per (doc tile, query group), so this is "
+                            "not a fraction of any hardware peak"},
                 "kernel": "k_score_union (fused group-tile LDS scoring + threshold emission)",
                 "kernel_ms_avg": round(avg_ms, 3), "kernel_ms_median": round(float(np.median(kern_ms)), 3),
                 "kernel_ms_min": round(float(np.min(kern_ms)), 3),
-                "scored_postings_per_launch": post_launch, "bytes_per_posting": per_post,
-                "algorithmic_bytes_per_launch": bytes_launch,
+                "scored_postings_per_launch": post_launch,
                 "search_call_ms_avg": round(float(np.mean(call_ms)), 3),
-                "batch_scored_postings": post_all,
-                "batch_gbs_algorithmic": round(post_all * per_post / (ms_per_step * 1e-3) / 1e9, 1)}
-        log(f"scoring kernel {avg_ms:.2f} ms avg: {achieved:.0f} GB/s algorithmic "
-            f"({100 * achieved / PEAK_HBM_GBS:.1f}% of {PEAK_HBM_GBS:.0f} GB/s); "
-            f"batch scored postings {post_all:.3e}")
+                "batch_scored_postings": post_all}
+        log(f"scoring kernel {avg_ms:.2f} ms avg: {adds_per_s / 1e9:.0f} G adds/s"
+            + ("" if lds is None else f" ({100 * adds_per_s / lds['peak']:.1f}% of the measured LDS atomic rate)")
+            + ("" if phys is None else f", HBM {phys / (avg_ms * 1e-3) / 1e9:.0f} GB/s physical"))
+
+    # ---- selection after scoring: candidate selection, fp64 rescoring of the
+    # candidates near the k-th score (doc-major rows), final sort.  Bytes are those
+    # these kernels move: candidate (doc, key) pairs read, rescoring set written,
+    # each rescored doc's row (row pointers + term ids + weights, at the mean row
+    # length) read, fp64 keys written and read back, the [B, k] results written.
+    selection = None
+    if a.path == "fused" and timing.get("phases"):
+        cand, resc = gs.search_counts(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles,
+                                      unroll=a.unroll, tiles_per_wg=a.tiles_per_wg)
+        per = np.array([[ev[i].elapsed_time(ev[i + 1]) for i in range(len(ev) - 1)] for ev in timing["phases"]])
+        sel_ms = float(np.median(per[:, 3:6].sum(axis=1)))
+        n_cand = int(np.minimum(cand.astype(np.int64), 65536).sum())
+        n_resc = int(resc.astype(np.int64).sum())
+        row_bytes = 16 + (int(index.lengths.sum().item()) / max(1, int(index.num_docs))) * (4 + wbytes)
+        sel_bytes = n_cand * 8 + n_resc * 4 + int(n_resc * row_bytes) + n_resc * 8 + n_resc * 12 + B * k * 12
+        selection = {"kernels": "k_select_cands + k_rescore_fwd + k_select_final", "ms": round(sel_ms, 3),
+                     "bytes": sel_bytes, "achieved": round(sel_bytes / (sel_ms * 1e-3) / 1e9, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(sel_bytes / (sel_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "candidates_per_query": round(n_cand / B, 1), "rescored_per_query": round(n_resc / B, 1),
+                     "reference_selection_bytes": B * int(index.num_docs) * 4 + B * k * 8,
+                     "note": "latency-bound (a few thousand candidates per query); the reference's torch.topk "
+                             "reads the whole [B, N] fp32 score matrix instead"}
+        log(f"selection {sel_ms:.3f} ms: {n_cand / B:.0f} candidates, {n_resc / B:.0f} rescored per query")
+
+    # ---- index build on the device (gs_index_count + gs_index_fill; the CSR is in
+    # HBM): algorithmic bytes = CSR term ids + weights + row pointers read, padded
+    # doc ids + weights written, per-term arrays written
+    index_build = None
+    if build_ev:
+        b_ms = build_ev["count"][0].elapsed_time(build_ev["count"][1]) + \
+            build_ev["fill"][0].elapsed_time(build_ev["fill"][1])
+        nnz_b = int(index.lengths.sum().item())
+        n_slots = int(index.doc_ids.numel())
+        b_bytes = nnz_b * (4 + wbytes) + (int(index.num_docs) + 1) * 8 + n_slots * (4 + wbytes) + \
+            int(index.vocab_size) * 24
+        index_build = {"kernels": "gs_index_count + gs_index_fill (stable radix transpose)", "ms": round(b_ms, 3),
+                       "postings": nnz_b, "bytes": b_bytes,
+                       "achieved": round(b_bytes / (b_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                       "frac": round(b_bytes / (b_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        log(f"index build on device {b_ms:.2f} ms for {nnz_b} postings ({index_build['achieved']} GB/s algorithmic)")
 
     # ---- per-phase times of gs_search (HIP events recorded by the library on
     # its launch stream), medians over the timed steps
@@ -316,12 +413,13 @@ def main():
                       "max_abs_diff_vs_fp64": float(np.max(np.abs(got_s.astype(np.float64) - s64)))}
             log(f"parity vs CPU oracle on {nq} queries: {parity} ({time.perf_counter() - t0:.1f}s)")
         if not a.no_cpu:
-            rows = cpu_rows(index_h, ti_h, tw_h, k, a.cpu_queries_1, a.cpu_queries_all, a.cpu_cores)
+            rows, n_aff = cpu_rows(index_h, ti_h, tw_h, k, a.cpu_queries_1, a.cpu_queries_all, a.cpu_cores)
             best = rows[-1]
             cpu = {"value": best["qps"], "unit": "queries/s", "cores": best["cores"], "kind": "port",
                    "sample": f"first {best['queries']} queries of the batch over the full index "
                              f"(reference CPU path cpu_sequential_score restated in C, fp32 accumulator)",
-                   "cpu_wall_ratio": best["cpu_wall_ratio"], "rows": rows}
+                   "cpu_wall_ratio": best["cpu_wall_ratio"], "affinity_cores": n_aff,
+                   "core_cap": a.cpu_cores, "rows": rows}
 
     n_docs = int(index.num_docs)
     res = {
@@ -335,7 +433,8 @@ def main():
                    "path": a.path,
                    "scorer": None if plan is None else {key: plan[key] for key in
                                                         ("group_size", "unroll", "tiles_per_wg", "seed_tiles", "packed")}},
-        "roofline": roof, "cpu_baseline": cpu, "parity": parity, "components_ms": components,
+        "roofline": roof, "selection": selection, "index_build": index_build,
+        "cpu_baseline": cpu, "parity": parity, "components_ms": components,
         "index_build_s": round(t_build, 3), "search_state_s": round(t_bounds, 3), "generate_s": round(t_gen, 1),
         "dense_rows": timing.get("dense_rows", 0),
     }

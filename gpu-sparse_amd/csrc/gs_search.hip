@@ -808,7 +808,7 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
                     md_m = s_e[lo] >> 16;
                     if constexpr (PK) {
                         const int64_t pb = md_p0 & ~int64_t(63);
-                        const uint64_t addr = (uint64_t)(uintptr_t)(pkd + pb);  // < 2^48
+                        const uint64_t addr = (uint64_t)(uintptr_t)(pkd + pb);  // < 2^48 (packed_usable)
                         md_blo = (uint32_t)addr;
                         md_bx = (uint32_t)(addr >> 32) | ((uint32_t)(md_p0 - pb) << 16);
                         md_nm = (uint32_t)md_n | ((uint32_t)md_m << 16);
@@ -1562,6 +1562,16 @@ int check_index(const gs_index *ix) {
     return GS_OK;
 }
 
+// The fused scorer reads the packed copy when it was made for this tile size and
+// lies below 2^48: its per-chunk load windows carry address bits 32..47 in a
+// 16-bit field (k_score_union).  Otherwise it reads the index arrays, with the
+// same results.
+bool packed_usable(const gs_index *ix) {
+    if (!ix->packed_d || ix->packed_tile_log2 != ix->tile_log2) return false;
+    const uint64_t end = (uint64_t)(uintptr_t)ix->packed_d + (uint64_t)ix->n_slots * 4u;
+    return end < (1ull << 48);
+}
+
 // default tiles per scoring workgroup of a launch over `tiles` tiles
 int default_tiles_per_wg(int tiles, int n_groups) {
     return (int64_t)((tiles + 1) / 2) * n_groups >= kPairMinWgs ? 2 : 1;
@@ -1600,7 +1610,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.rcap = kRescoreCap;
     // default postings per lane per chunk: 16 on packed one-word postings (their
     // registers allow it), else 8
-    const bool packed1 = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2;
+    const bool packed1 = packed_usable(ix);
     p.unroll = (o && o->unroll > 0) ? o->unroll : (packed1 ? 16 : 8);
     p.tiles_per_wg = (o && o->tiles_per_wg > 0) ? o->tiles_per_wg : 0;
     p.scale = ar.take<float>(B);
@@ -1675,7 +1685,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         qw = p.qw_p;
     }
     // the fused scorer reads the packed copy when it was made for this tile size
-    const void *pk = ix->packed_d && ix->packed_tile_log2 == ix->tile_log2 ? ix->packed_d : nullptr;
+    const void *pk = packed_usable(ix) ? ix->packed_d : nullptr;
     const int32_t pkf = pk && WT != GS_W_U8 ? 1 : 0;  // integer products of the packed float weights
     k_query_prep<WT><<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d, ix->dup_d,
                                                                      pkf, ix->packed_shift, p.scale, p.mfix, p.tau,
@@ -1854,7 +1864,22 @@ extern "C" int gs_search_plan(const gs_index *index, int32_t B, int32_t T, int32
     out->unroll = p.unroll;
     const int rest = index->n_tiles - p.S;
     out->tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : (rest > 0 ? default_tiles_per_wg(rest, p.n_groups) : 1);
-    out->packed = index->packed_d && index->packed_tile_log2 == index->tile_log2;
+    out->packed = packed_usable(index);
+    return GS_OK;
+}
+
+extern "C" int gs_search_counts(const gs_index *index, int32_t B, int32_t T, int32_t k, const gs_search_opts *opts,
+                                const void *workspace_d, size_t workspace_bytes, uint32_t *cand_d, uint32_t *resc_d,
+                                void *stream) {
+    if (int rc = check_index(index)) return rc;
+    GS_REQUIRE(B > 0 && T > 0 && k > 0 && (int64_t)T <= kGroupSortCap, "bad search sizes");
+    GS_REQUIRE(workspace_d && cand_d && resc_d, "null pointer");
+    gs_arena ar{reinterpret_cast<char *>(const_cast<void *>(workspace_d)), 0, workspace_bytes};
+    const SearchPlan p = plan_search(index, B, T, k, opts, ar);
+    GS_REQUIRE(ar.ok(), "workspace smaller than the search's (%zu < %zu bytes)", workspace_bytes, ar.used);
+    hipStream_t s = gs_stream(stream);
+    GS_CHECK_HIP(hipMemcpyAsync(cand_d, p.cnt, sizeof(uint32_t) * (size_t)B, hipMemcpyDeviceToDevice, s));
+    GS_CHECK_HIP(hipMemcpyAsync(resc_d, p.resc_cnt, sizeof(uint32_t) * (size_t)B, hipMemcpyDeviceToDevice, s));
     return GS_OK;
 }
 

@@ -1,5 +1,7 @@
 // LDS atomic throughput on gfx950: ds_add_f32 vs ds_add_u32 vs ds_add_u64 vs a
-// plain read-add-write, on random and conflict-free addresses.  Each lane keeps
+// plain read-add-write, on random and conflict-free addresses.  Prints a table and
+// one line "JSON {...}" with the rates in lane-ops/s over the whole GPU (and
+// 32-bit slot adds/s: two per ds_add_u64).  Each lane keeps
 // 16 fixed random word indices and xors them with a wave-uniform value per
 // round, so one VALU op precedes each LDS op and the LDS pipe is the limit.
 // Every address stays inside the workgroup's own 64 KiB allocation.
@@ -47,6 +49,9 @@ int main() {
   (void)hipEventCreate(&e1);
   const int blocks = 2048, iters = 256;
   const char *names[] = {"ds_add_f32 (atomic)", "ds_add_u32 (atomic)", "ds_read+add+ds_write", "ds_add_u64 (atomic)"};
+  const char *keys[] = {"ds_add_f32", "ds_add_u32", "ds_read_add_write", "ds_add_u64"};
+  char json[2048];
+  int jn = snprintf(json, sizeof json, "{");
   for (int cf = 0; cf < 2; ++cf)
     for (int mode = 0; mode < 4; ++mode) {
       for (int rep = 0; rep < 2; ++rep) {
@@ -60,12 +65,25 @@ int main() {
         float ms = 0;
         (void)hipEventElapsedTime(&ms, e0, e1);
         const double ops = (double)blocks * 1024 * iters * U;
-        if (rep)
-          printf("%-22s %s: %8.3f ms  %.2f lane-ops/clk/CU (2.4 GHz, 256 CU)\n", names[mode],
-                 cf ? "conflict-free" : "random       ", ms, ops / (ms * 1e-3) / 2.4e9 / 256);
+        if (rep) {
+          const double rate = ops / (ms * 1e-3);  // lane-ops per second over the whole GPU
+          printf("%-22s %s: %8.3f ms  %.3e lane-ops/s  %.2f lane-ops/clk/CU (2.4 GHz, 256 CU)\n", names[mode],
+                 cf ? "conflict-free" : "random       ", ms, rate, rate / 2.4e9 / 256);
+          // 32-bit slots added per second: a ds_add_u64 adds two
+          jn += snprintf(json + jn, sizeof json - jn,
+                         "%s\"%s_%s\": {\"ms\": %.4f, \"lane_ops_per_s\": %.4e, \"slot_adds_per_s\": %.4e}",
+                         jn > 1 ? ", " : "", keys[mode], cf ? "conflict_free" : "random", ms, rate,
+                         rate * (mode == 3 ? 2.0 : 1.0));
+        }
       }
     }
   hipError_t e = hipDeviceSynchronize();
   printf("status %s\n", hipGetErrorString(e));
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, 0) == hipSuccess)
+    jn += snprintf(json + jn, sizeof json - jn, ", \"device\": \"%s\", \"cus\": %d, \"clock_khz\": %d",
+                   prop.gcnArchName, prop.multiProcessorCount, prop.clockRate);
+  snprintf(json + jn, sizeof json - jn, ", \"ops_per_lane\": %d, \"blocks\": %d, \"threads\": 1024}", iters * U, blocks);
+  printf("JSON %s\n", json);
   return 0;
 }

@@ -127,6 +127,8 @@ SIGNATURES = {
                                  C.POINTER(GsSearchPlanInfo)]),
     "gs_search": (C.c_int, [C.POINTER(GsIndex), _P, _P, _I32, _I32, _I32, C.POINTER(GsSearchOpts), _P, _P,
                             _P, _P, _SZ, _P]),
+    "gs_search_counts": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts), _P, _SZ, _P, _P,
+                                   _P]),
     "gs_search_dense_workspace": (C.c_int, [C.POINTER(GsIndex), _I32, C.POINTER(_SZ)]),
     "gs_search_dense": (C.c_int, [C.POINTER(GsIndex), _P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _SZ,
                                   _P]),

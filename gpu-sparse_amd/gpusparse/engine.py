@@ -49,17 +49,21 @@ def determine_dimension(*embedding_sets):
     return d + VOCAB_PAD
 
 
-def to_query_tensors(q_csr, device):
+def to_query_tensors(q_csr, device, *, weight_dtype=torch.float32):
     """Dense [nq, max_nnz] term-id / weight tensors, -1 / 0 padded, no truncation
-    (gpusparse_retrieval.py:118-132).  uint8 query weights stay uint8."""
+    (gpusparse_retrieval.py:118-132).  Weights are float32 as in the reference
+    (:124); ``weight_dtype=None`` keeps uint8 query weights as uint8 (the native
+    form a uint8 index takes, which then needs no conversion per search)."""
     if not isinstance(q_csr, CSR):
         q_csr = CSR(np.asarray(q_csr.indptr), np.asarray(q_csr.indices), np.asarray(q_csr.data),
                     tuple(q_csr.shape))
+    if weight_dtype not in (None, torch.float32):
+        raise ValueError(f"weight_dtype must be torch.float32 or None, got {weight_dtype}")
     indptr = np.asarray(q_csr.indptr, dtype=np.int64)
     nq = indptr.shape[0] - 1
     nnz = np.diff(indptr)
     max_nnz = int(nnz.max()) if nq else 1
-    wdt = np.uint8 if q_csr.data.dtype == np.uint8 else np.float32
+    wdt = np.uint8 if (weight_dtype is None and q_csr.data.dtype == np.uint8) else np.float32
     ti = np.full((nq, max_nnz), -1, dtype=np.int32)
     ts = np.zeros((nq, max_nnz), dtype=wdt)
     if nq and indptr[-1]:

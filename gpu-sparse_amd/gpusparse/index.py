@@ -114,12 +114,16 @@ def _as_csr(m) -> CSR:
 
 
 def _weights_of(data: np.ndarray, weight_dtype) -> np.ndarray:
-    """Weights as stored: float16 / uint8 data is kept, anything else becomes
-    float32 as in the reference builders (run_correctness_verification.py:41)."""
+    """Posting weights in the storage type.  ``weight_dtype=None`` keeps float16 /
+    uint8 data as it is and makes anything else float32; torch.float32 converts
+    every type to float32, as the reference builders do
+    (gpusparse_retrieval.py:98, run_correctness_verification.py:41)."""
     if weight_dtype is None:
         if data.dtype in (np.float16, np.uint8):
             return np.ascontiguousarray(data)
         return np.ascontiguousarray(data, dtype=np.float32)
+    if weight_dtype not in (torch.float32, torch.float16, torch.uint8):
+        raise ValueError(f"weight_dtype must be torch.float32, torch.float16 or torch.uint8, got {weight_dtype}")
     want = {torch.float32: np.float32, torch.float16: np.float16, torch.uint8: np.uint8}[weight_dtype]
     if data.dtype == want:
         return np.ascontiguousarray(data)
@@ -129,12 +133,17 @@ def _weights_of(data: np.ndarray, weight_dtype) -> np.ndarray:
 
 
 def build_from_csr(csr, device=None, *, vocab_size: int | None = None, weight_dtype=None,
-                   index_error: bool = False) -> GPUInvertedIndex:
+                   index_error: bool = False, timing: dict | None = None) -> GPUInvertedIndex:
     """GPU index build from a doc-major CSR (rows = documents, columns = terms).
 
-    ``vocab_size`` defaults to the number of columns.  Term ids outside
-    ``[0, vocab_size)`` raise (IndexError when ``index_error``, as numpy does in
-    run_correctness_verification.py:54, else ValueError)."""
+    The native builder: float16 and uint8 CSR data are stored as they are unless
+    ``weight_dtype`` names another type (the reference-named builders below store
+    float32 by default).  ``vocab_size`` defaults to the number of columns.  Term
+    ids outside ``[0, vocab_size)`` raise (IndexError when ``index_error``, as
+    numpy does in run_correctness_verification.py:54, else ValueError).
+    ``timing``: optional dict; receives ("count", "fill") pairs of events on the
+    launch stream around gs_index_count and gs_index_fill (the device-side build,
+    the CSR already in HBM)."""
     dev = _lib.require_gpu(device)
     c = _as_csr(csr)
     n_docs = int(c.shape[0])
@@ -158,8 +167,13 @@ def build_from_csr(csr, device=None, *, vocab_size: int | None = None, weight_dt
     padded = torch.empty(V, dtype=torch.int32, device=dev)
     offsets = torch.empty(V, dtype=torch.int64, device=dev)
     info = torch.zeros(2, dtype=torch.int64, device=dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if timing is not None else None
+    if ev:
+        ev[0].record()
     _lib.check(L.gs_index_count(_lib.ptr(indices_d) if nnz else None, nnz, V, _lib.ptr(lengths),
                                 _lib.ptr(padded), _lib.ptr(offsets), _lib.ptr(info), s), "gs_index_count")
+    if ev:
+        ev[1].record()
     n_slots, n_bad = (int(x) for x in info.cpu())
     if n_bad:
         msg = f"{n_bad} postings have term ids outside [0, {V})"
@@ -170,12 +184,18 @@ def build_from_csr(csr, device=None, *, vocab_size: int | None = None, weight_dt
     max_scores = torch.empty(V, dtype=torch.float32, device=dev)
     max_abs = torch.empty(V, dtype=torch.float32, device=dev)
     ws = torch.empty(L.gs_index_fill_workspace(nnz, V), dtype=torch.uint8, device=dev)
+    if ev:
+        ev[2].record()
     _lib.check(L.gs_index_fill(_lib.ptr(indptr_d), _lib.ptr(indices_d) if nnz else None,
                                _lib.ptr(data_d) if nnz else None, _lib.WTYPE_OF_DTYPE[wdt], n_docs, nnz, V,
                                _lib.ptr(offsets), _lib.ptr(lengths), _lib.ptr(padded), n_slots,
                                _lib.ptr(doc_ids) if n_slots else None, _lib.ptr(weights) if n_slots else None,
                                _lib.ptr(max_scores), _lib.ptr(max_abs), _lib.ptr(ws), ws.numel(), s),
                "gs_index_fill")
+    if ev:
+        ev[3].record()
+        timing["count"] = (ev[0], ev[1])
+        timing["fill"] = (ev[2], ev[3])
     del ws
     idx = GPUInvertedIndex(doc_ids=doc_ids, scores=weights, offsets=offsets, lengths=lengths,
                            padded_lengths=padded, max_scores=max_scores, num_docs=n_docs, vocab_size=V,
@@ -189,15 +209,18 @@ def build_from_csr(csr, device=None, *, vocab_size: int | None = None, weight_dt
 # ------------------------------------------------------------------ reference builders
 
 
-def build_index(doc_csr, device, *, weight_dtype=None) -> GPUInvertedIndex:
+def build_index(doc_csr, device, *, weight_dtype=torch.float32) -> GPUInvertedIndex:
     """Drop-in for build_index (lsr_benchmark_engine/gpusparse_retrieval.py:81-115):
-    vocabulary = number of CSR columns."""
+    vocabulary = number of CSR columns; weights stored as float32 like the
+    reference (:98) unless ``weight_dtype`` opts into torch.float16 or torch.uint8
+    (uint8 data must already hold the quantized impacts)."""
     return build_from_csr(doc_csr, device, weight_dtype=weight_dtype)
 
 
-def build_gpu_index_from_csr(csr_mat, device, *, weight_dtype=None) -> GPUInvertedIndex:
+def build_gpu_index_from_csr(csr_mat, device, *, weight_dtype=torch.float32) -> GPUInvertedIndex:
     """Drop-in for build_gpu_index_from_csr (src/run_correctness_verification.py:32-84):
-    the vocabulary is fixed at 30522 and larger term ids raise IndexError."""
+    the vocabulary is fixed at 30522, larger term ids raise IndexError, weights
+    are stored as float32 (:41) unless ``weight_dtype`` says otherwise."""
     return build_from_csr(csr_mat, device, vocab_size=VOCAB_SIZE, weight_dtype=weight_dtype, index_error=True)
 
 

@@ -47,7 +47,14 @@ def query_tensors(index, query_batch):
     want = torch.uint8 if index.scores.dtype == torch.uint8 else torch.float32
     if qw.dtype != want:
         if want == torch.uint8:
-            raise ValueError("a uint8 index takes uint8 query weights")
+            # float query weights (the reference's query tensors are float32,
+            # gpusparse_retrieval.py:124) are taken when every one is an integer
+            # in [0, 255]: the uint8 impacts they carry
+            if not (qw.dtype.is_floating_point or qw.dtype in (torch.int16, torch.int32, torch.int64)):
+                raise ValueError(f"a uint8 index takes uint8 query weights, got {qw.dtype}")
+            ok = bool(((qw >= 0) & (qw <= 255) & (qw == torch.round(qw.double()))).all()) if qw.numel() else True
+            if not ok:
+                raise ValueError("a uint8 index takes uint8 query weights: float weights must be integers in [0, 255]")
         qw = qw.to(want)
     return qt.contiguous(), qw.contiguous()
 
@@ -176,6 +183,27 @@ def search_plan(index, B: int, T: int, k: int, *, tile_log2: int | None = None, 
                                          _lib.C.byref(opts), _lib.C.byref(info)), "gs_search_plan")
     return {"tile_log2": tile_log2, "seed_tiles": info.seed_tiles, "group_size": info.group_size,
             "unroll": info.unroll, "tiles_per_wg": info.tiles_per_wg, "packed": bool(info.packed)}
+
+
+def search_counts(index, B: int, T: int, k: int, *, tile_log2: int | None = None, sample_tiles: int = 0,
+                  cand_cap: int = 0, unroll: int = 0, tiles_per_wg: int = 0):
+    """Per scoring slot of the fused search that last ran with these arguments:
+    (docs the scorer emitted as candidates, candidates rescored in fp64), two
+    numpy uint32 [B] arrays (gs_search_counts on the index's cached workspace)."""
+    if tile_log2 is None:
+        tile_log2 = default_tile_log2(index)
+    ws = index.aux().get("workspace")
+    if ws is None:
+        raise ValueError("no fused search has run on this index")
+    dev = _device_of(index)
+    gidx = gs_index_struct(index, tile_log2)
+    opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, 0, None, None, tiles_per_wg)
+    cand = torch.empty(B, dtype=torch.int32, device=dev)
+    resc = torch.empty(B, dtype=torch.int32, device=dev)
+    _lib.check(_lib.lib().gs_search_counts(_lib.C.byref(gidx), int(B), int(T), min(int(k), int(index.num_docs)),
+                                           _lib.C.byref(opts), _lib.ptr(ws), ws.numel(), _lib.ptr(cand),
+                                           _lib.ptr(resc), _lib.stream_ptr(dev)), "gs_search_counts")
+    return cand.cpu().numpy().view(np.uint32), resc.cpu().numpy().view(np.uint32)
 
 
 def triton_fused_score(index, query_term_ids: torch.Tensor, query_term_scores: torch.Tensor, top_k: int = 10,

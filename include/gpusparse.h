@@ -219,6 +219,16 @@ int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_wei
               int64_t *out_ids_d, int32_t *status_d, void *workspace_d, size_t workspace_bytes,
               void *stream);
 
+/* Candidate counts of the gs_search that last ran on `workspace_d` with the same
+ * (index, B, T, k, opts) (no counterpart in the reference: an introspection call
+ * for benchmarks), per scoring slot: cand_d[s] <- docs the fused scorer emitted
+ * (before the cand_cap cut), resc_d[s] <- candidates rescored in fp64 (0 for
+ * uint8 indexes and for rows flagged GS_ROW_DENSE).  uint32 [B] each; copied on
+ * `stream` after the search's kernels. */
+int gs_search_counts(const gs_index *index, int32_t B, int32_t T, int32_t k, const gs_search_opts *opts,
+                     const void *workspace_d, size_t workspace_bytes, uint32_t *cand_d, uint32_t *resc_d,
+                     void *stream);
+
 /* Monolithic exact path (the reference's [B, N] accumulator, triton_kernel.py:182-199):
  * rows listed in rows_d (int32 [R], or NULL for rows 0..B-1) are scored densely
  * over all documents (fp64 or uint32 tiles written to a dense row buffer) and

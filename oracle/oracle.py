@@ -24,6 +24,8 @@ products, exhaustive sorting, closed forms):
   compacted_topk         pinned: topk of the thresholded row
   to_query_tensors       pinned: explicit per-row loop
   fp16 / u8 codes        pinned: numpy float16 cast / closed-form values
+  checksum_csr / _index  pinned: equal on an index and its CSR, different after
+                         any single planted change (moved, altered, lost posting)
 """
 from __future__ import annotations
 
@@ -359,6 +361,10 @@ def clib():
         P, I32, I64 = C.c_void_p, C.c_int32, C.c_int64
         L.orc_search.restype = C.c_int
         L.orc_search.argtypes = [P, P, C.c_int, P, P, I32, I64, P, P, I32, I32, I32, P, P, P, C.c_int]
+        L.orc_checksum_csr.restype = C.c_uint64
+        L.orc_checksum_csr.argtypes = [P, P, P, C.c_int, I64, C.c_int]
+        L.orc_checksum_index.restype = C.c_uint64
+        L.orc_checksum_index.argtypes = [P, P, C.c_int, P, P, P, I32, C.c_int, P]
         L.orc_cpu_sequential.restype = C.c_int
         L.orc_cpu_sequential.argtypes = [P, P, C.c_int, P, P, I32, I64, P, P, I32, I32, I32, P, P, C.c_int]
         _clib = L
@@ -409,3 +415,27 @@ def c_cpu_sequential(index: dict, q_terms, q_weights, k: int, threads: int = 1):
     if rc:
         raise RuntimeError(f"orc_cpu_sequential failed ({rc})")
     return vals, ids
+
+
+def checksum_csr(indptr, indices, data, threads: int = 8) -> int:
+    """Order-independent checksum of the (doc, term, weight bits) triples of a
+    doc-major CSR (orc_checksum_csr); equal to checksum_index of an index built
+    from it when the index holds exactly its postings."""
+    ip = np.ascontiguousarray(indptr, dtype=np.int64)
+    ix = np.ascontiguousarray(indices, dtype=np.int32)
+    d = np.ascontiguousarray(data)
+    return int(clib().orc_checksum_csr(ip.ctypes.data, ix.ctypes.data, d.ctypes.data, _WT[d.dtype],
+                                       ip.shape[0] - 1, int(threads)))
+
+
+def checksum_index(index: dict, threads: int = 8) -> tuple[int, int]:
+    """(checksum of the index's postings, padding / list slots out of layout)."""
+    doc = np.ascontiguousarray(index["doc_ids"], dtype=np.int32)
+    w = np.ascontiguousarray(index["scores"])
+    off = np.ascontiguousarray(index["offsets"], dtype=np.int64)
+    ln = np.ascontiguousarray(index["lengths"], dtype=np.int32)
+    pd = np.ascontiguousarray(index["padded_lengths"], dtype=np.int32)
+    bad = C.c_int64(0)
+    s = clib().orc_checksum_index(doc.ctypes.data, w.ctypes.data, _WT[w.dtype], off.ctypes.data, ln.ctypes.data,
+                                  pd.ctypes.data, int(index["vocab_size"]), int(threads), C.byref(bad))
+    return int(s), int(bad.value)

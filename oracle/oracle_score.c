@@ -234,3 +234,58 @@ int orc_cpu_sequential(const int32_t *doc, const void *w, int wtype, const int64
     }
     return bad;
 }
+
+/*
+ * Order-independent checksum of a posting multiset: the sum (mod 2^64) over
+ * postings of mix(doc, term, weight bits), with mix a SplitMix64-style finaliser.
+ * Two collections of (doc, term, weight) triples agree on it when they hold the
+ * same triples; any lost, duplicated, moved or altered posting changes it with
+ * probability 1 - 2^-64.  Used to check a full-size GPU index against the CSR it
+ * was built from without a host rebuild.
+ */
+static uint64_t mix3(uint64_t d, uint64_t t, uint64_t w) {
+    uint64_t h = d * 0x9E3779B97F4A7C15ull ^ (t + 0x632BE59BD9B4E019ull) * 0xC2B2AE3D27D4EB4Full ^
+                 (w + 0x8CB92BA72F3D8DD7ull) * 0x165667B19E3779F9ull;
+    h ^= h >> 31;
+    h *= 0xBF58476D1CE4E5B9ull;
+    h ^= h >> 29;
+    h *= 0x94D049BB133111EBull;
+    return h ^ (h >> 32);
+}
+
+static uint64_t wbits(const void *w, int wtype, int64_t i) {
+    if (wtype == 0) return ((const uint32_t *)w)[i];
+    if (wtype == 1) return ((const uint16_t *)w)[i];
+    return ((const uint8_t *)w)[i];
+}
+
+/* CSR rows = docs, columns = terms. */
+uint64_t orc_checksum_csr(const int64_t *indptr, const int32_t *indices, const void *data, int wtype, int64_t n_rows,
+                          int threads) {
+    uint64_t sum = 0;
+#pragma omp parallel for schedule(dynamic, 4096) reduction(+ : sum) num_threads(threads > 0 ? threads : 1)
+    for (int64_t d = 0; d < n_rows; ++d)
+        for (int64_t i = indptr[d]; i < indptr[d + 1]; ++i)
+            sum += mix3((uint64_t)d, (uint64_t)(uint32_t)indices[i], wbits(data, wtype, i));
+    return sum;
+}
+
+/* Term-major index: list t = slots [off[t], off[t] + len[t]).  *bad_pad <- number
+ * of slots in [off[t] + len[t], off[t] + padded[t]) that are not (-1, 0), plus
+ * list slots holding a negative doc id. */
+uint64_t orc_checksum_index(const int32_t *doc, const void *w, int wtype, const int64_t *off, const int32_t *len,
+                            const int32_t *padded, int32_t V, int threads, int64_t *bad_pad) {
+    uint64_t sum = 0;
+    int64_t bad = 0;
+#pragma omp parallel for schedule(dynamic, 16) reduction(+ : sum, bad) num_threads(threads > 0 ? threads : 1)
+    for (int32_t t = 0; t < V; ++t) {
+        for (int64_t i = off[t]; i < off[t] + len[t]; ++i) {
+            if (doc[i] < 0) ++bad;
+            sum += mix3((uint64_t)(uint32_t)doc[i], (uint64_t)t, wbits(w, wtype, i));
+        }
+        for (int64_t i = off[t] + len[t]; i < off[t] + padded[t]; ++i)
+            if (doc[i] != -1 || wbits(w, wtype, i) != 0) ++bad;
+    }
+    *bad_pad = bad;
+    return sum;
+}

@@ -1,10 +1,18 @@
-"""Writes tests/golden/golden.npz: small seeded inputs and the expected outputs of
-the scoring path (index arrays, chunk bounds, exact top-k) for fp32, fp16 and
-uint8 weights.
+"""Writes the committed fixtures under tests/golden/.
 
+golden.npz: small seeded inputs and the expected outputs of the scoring path
+(index arrays, chunk bounds, exact top-k) for fp32, fp16 and uint8 weights.
 Expected outputs come from the CPU oracle and are cross-checked here against
 brute force (dict-of-lists index, dense products, full sorts) before they are
-written.  Run from the repository root:  python tests/golden/make_golden.py
+written.
+
+engine_embeddings.npz + engine_run.txt: sparse doc and query embeddings for the
+plug-in's entry point (lsr_benchmark_engine/gpusparse_retrieval.py:175-222) and
+the TREC run it must write at k = 10.  The run comes from a brute-force ranking
+written here independently of the oracle and the library: per (query, doc) a
+Python float (fp64) sum of products in query-term order, docs ordered by (score
+descending, doc index ascending), scores printed as float32, only scores > 0
+kept (:169-170).  Run from the repository root:  python tests/golden/make_golden.py
 """
 import os
 import sys
@@ -62,7 +70,80 @@ def build(weights):
     return out
 
 
+ENGINE_K = 10
+
+
+def engine_embeddings(seed=77, n_docs=400, n_queries=20, vocab=600):
+    """(doc, query) embeddings as lists of (id, tokens, values) with float32
+    values.  Includes two identical docs that tie at the top of one query, a
+    query whose tokens no doc holds (empty ranking), a query with fewer than k
+    matching docs and a query that repeats a token."""
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, vocab - 10 + 1) ** 1.05
+    p /= p.sum()
+
+    def row(n):
+        toks = rng.choice(vocab - 10, size=n, replace=False, p=p)
+        vals = rng.lognormal(-0.5, 0.8, size=n).astype(np.float32)
+        return [int(t) for t in toks], [float(v) for v in vals]
+
+    docs = [(f"D{i:04d}",) + row(int(rng.integers(3, 41))) for i in range(n_docs)]
+    docs[17] = ("D0017", docs[17][1] + [vocab - 8], docs[17][2] + [2.5])
+    docs[240] = ("D0240", list(docs[17][1]), list(docs[17][2]))
+    rare = [t for t in range(vocab - 10) if sum(t in d[1] for d in docs) == 3][0]
+    queries = [(f"Q{i:03d}",) + row(int(rng.integers(2, 13))) for i in range(n_queries)]
+    queries[5] = ("Q005", [vocab - 5, vocab - 3], [0.5, 1.25])
+    queries[7] = ("Q007", [rare], [0.75])
+    t9, v9 = queries[9][1], queries[9][2]
+    queries[9] = ("Q009", t9 + [t9[0]], v9 + [0.3125])
+    queries[11] = ("Q011", [vocab - 8, docs[17][1][0]], [1.0, 0.5])  # D0017 and D0240 tie on top
+    return docs, queries
+
+
+def brute_run(docs, queries, k, tag="gpusparse"):
+    """TREC lines of the exact top-k by brute force over the embeddings."""
+    lines = []
+    for qid, qt, qv in queries:
+        scored = []
+        for di, (_, dt, dv) in enumerate(docs):
+            s = 0.0
+            for t, w in zip(qt, qv):
+                for t2, w2 in zip(dt, dv):
+                    if t2 == t:
+                        s += w * w2
+            scored.append((s, di))
+        scored.sort(key=lambda x: (-x[0], x[1]))
+        rank = 0
+        for s, di in scored[:k]:
+            if np.float32(s) > 0:
+                rank += 1
+                lines.append(f"{qid} Q0 {docs[di][0]} {rank} {float(np.float32(s))} {tag}")
+    return lines
+
+
+def pack_embeddings(emb):
+    indptr = np.zeros(len(emb) + 1, np.int64)
+    indptr[1:] = np.cumsum([len(e[1]) for e in emb])
+    return (np.array([e[0] for e in emb]), indptr, np.array([t for e in emb for t in e[1]], np.int64),
+            np.array([v for e in emb for v in e[2]], np.float32))
+
+
+def write_engine_fixture(here):
+    docs, queries = engine_embeddings()
+    arrays = {}
+    for kind, emb in (("doc", docs), ("query", queries)):
+        ids, indptr, toks, vals = pack_embeddings(emb)
+        arrays.update({f"{kind}_ids": ids, f"{kind}_indptr": indptr, f"{kind}_tokens": toks,
+                       f"{kind}_values": vals})
+    np.savez_compressed(os.path.join(here, "engine_embeddings.npz"), **arrays)
+    lines = brute_run(docs, queries, ENGINE_K)
+    with open(os.path.join(here, "engine_run.txt"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(f"wrote engine fixture: {len(docs)} docs, {len(queries)} queries, {len(lines)} run lines")
+
+
 def main():
+    write_engine_fixture(os.path.dirname(os.path.abspath(__file__)))
     arrays = {}
     for w in ("f32", "f16", "u8"):
         for name, arr in build(w).items():

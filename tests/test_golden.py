@@ -53,7 +53,7 @@ def test_oracle_reproduces_outputs(v):
 def test_gpu_reproduces_outputs(device, v, path):
     import gpusparse as gs
     csr = CSR(arr(v, "doc_indptr"), arr(v, "doc_indices"), arr(v, "doc_data"), (400, 1500))
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     for f in FIELDS:
         assert same(getattr(ix, f).cpu().numpy(), arr(v, "ix_" + f)), f
     assert same(gs.build_chunk_boundaries(ix, 128).cpu().numpy(), arr(v, "chunk_bounds"))

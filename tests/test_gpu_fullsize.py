@@ -1,0 +1,124 @@
+"""GPU parity at the configurations' full sizes (C2: 1M docs, B=1024; C3 and C5:
+8.8M docs, ~1.06e9 postings, B=512), after src/remeasure_2026_09.py:155-235.
+
+At these sizes the oracle does not rebuild the index on the host.  Instead:
+- the GPU-built index is checked against its CSR by size-independent
+  properties: lengths equal the CSR's column counts, padding to 32, exclusive
+  offsets, every list ascending (gs_check_lists), and the same multiset of
+  (doc, term, weight) postings (the oracle's order-independent checksum);
+- the oracle then scores the host copy of that index (as bench.py does), and
+  the GPU answers must equal its exact top-k bit for bit: ids, and scores equal
+  to the fp64 scatter-add rounded to fp32 (|diff| <= 1e-5 follows) or the
+  exact uint32 sums.
+One configuration is held at a time (the previous one is freed first)."""
+import gc
+
+import numpy as np
+import pytest
+import torch
+
+import gpusparse as gs
+from gpusparse import synth
+from gpusparse.index import to_host
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+_held = {}
+
+
+def full(name, device):
+    """(config, index, host index, query terms, query weights, CSR checksum) of
+    one configuration at full size, built once."""
+    if name not in _held:
+        _held.clear()
+        gc.collect()
+        torch.cuda.empty_cache()
+        cfg = synth.CONFIGS[name]
+        print(f"generating {name} at full size ({cfg.docs.n_rows} docs)", flush=True)
+        docs, queries = synth.generate(cfg)
+        want = O.checksum_csr(docs.indptr, docs.indices, docs.data, threads=16)
+        counts = np.bincount(docs.indices, minlength=docs.shape[1]).astype(np.int32)
+        ix = gs.build_from_csr(docs, device)
+        nnz = docs.nnz
+        del docs
+        qt, qw, _ = gs.to_query_tensors(queries, device, weight_dtype=None)
+        _held[name] = (cfg, ix, to_host(ix), qt, qw, want, counts, nnz)
+    return _held[name]
+
+
+def check_index(name, device):
+    cfg, ix, h, qt, qw, want, counts, nnz = full(name, device)
+    print(f"{name}: index invariants over {nnz} postings", flush=True)
+    assert np.array_equal(h["lengths"], counts)
+    assert int(h["lengths"].astype(np.int64).sum()) == nnz
+    assert np.array_equal(h["padded_lengths"], (counts + 31) // 32 * 32)
+    off = np.zeros_like(h["offsets"])
+    np.cumsum(h["padded_lengths"][:-1].astype(np.int64), out=off[1:])
+    assert np.array_equal(h["offsets"], off)
+    assert ix.doc_ids.numel() == int(off[-1]) + int(h["padded_lengths"][-1])
+    n_bad, n_nonempty = gs.check_lists(ix)
+    assert n_bad == 0 and n_nonempty == int(np.count_nonzero(counts))
+    assert O.checksum_index(h, threads=16) == (want, 0)
+
+
+def check_search(name, device, k, rows):
+    cfg, ix, h, qt, qw, *_ = full(name, device)
+    print(f"{name}: search B={qt.shape[0]} k={k}, {len(rows)} rows checked", flush=True)
+    timing = {}
+    s, i = gs.search(ix, (qt, qw), k, timing=timing)
+    assert s.shape == (qt.shape[0], k)
+    ti, tw = qt.cpu().numpy()[rows], qw.cpu().numpy()[rows]
+    vs, s64, vi = O.c_search(h, ti, tw, k, threads=16)
+    got_s, got_i = s.cpu().numpy()[rows], i.cpu().numpy()[rows]
+    assert np.array_equal(got_i, vi)
+    assert got_s.dtype == vs.dtype and np.array_equal(got_s, vs)
+    if got_s.dtype == np.float32:
+        assert np.max(np.abs(got_s.astype(np.float64) - s64)) <= 1e-5
+    return timing
+
+
+def sample_rows(B, n, seed):
+    """n rows of a B-query batch: the first n/2 and n/2 more spread at random."""
+    rng = np.random.default_rng(seed)
+    head = np.arange(n // 2)
+    rest = rng.choice(np.arange(n // 2, B), size=n - n // 2, replace=False)
+    return np.sort(np.concatenate([head, rest]))
+
+
+def test_c2_full_index(device):
+    check_index("C2", device)
+
+
+def test_c2_full_search_whole_batch(device):
+    """1M docs, B=1024 (the groups of a whole 1024-query ordering block), fp32,
+    k=1000: every query of the batch checked."""
+    check_search("C2", device, 1000, np.arange(1024))
+
+
+def test_c3_full_index(device):
+    check_index("C3", device)
+
+
+@pytest.mark.parametrize("k", [1000, 10])
+def test_c3_full_search(device, k):
+    rows = sample_rows(512, 48, seed=k)
+    timing = check_search("C3", device, k, rows)
+    assert timing["dense_rows"] == 0
+
+
+def test_c5_full_index(device):
+    check_index("C5", device)
+
+
+def test_c5_full_search_bit_exact(device):
+    """The integer configuration: uint8 x uint8 products summed in uint32,
+    bit-exact with the CPU integer reference, ties by ascending doc id."""
+    rows = sample_rows(512, 48, seed=5)
+    check_search("C5", device, 1000, rows)
+
+
+def test_zz_release_full_size(device):
+    _held.clear()
+    gc.collect()
+    torch.cuda.empty_cache()

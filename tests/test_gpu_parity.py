@@ -52,7 +52,7 @@ def assert_search_equal(ix, ref, ti, tw, k, **opts):
 def test_build_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
     print(f"build case seed={seed} n_docs={n_docs} vocab={vocab} dtype={dtype.__name__}", flush=True)
     csr = random_csr(np.random.default_rng(seed), n_docs, vocab, dtype=dtype, dup_rate=dup)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     assert_index_equal(ix, oracle_index(csr))
 
 
@@ -63,7 +63,7 @@ def test_forward_index_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
     from gpusparse.index import build_forward
     print(f"forward case seed={seed} n_docs={n_docs} vocab={vocab} dtype={dtype.__name__}", flush=True)
     csr = random_csr(np.random.default_rng(seed), n_docs, vocab, dtype=dtype, dup_rate=dup)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     row_ptr, terms, w = build_forward(ix)
     want = O.forward_index(oracle_index(csr))
     nnz = int(want[0][-1])
@@ -81,7 +81,7 @@ def test_packed_copy_matches_oracle(device, seed, dtype, tile_log2):
     if dtype != np.uint8:  # signed weights and ties at half units of the scale
         csr.data[::5] *= -1
         csr.data[3::13] = ((np.arange(len(csr.data[3::13])) % 7) + 0.5).astype(dtype) / 2
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     pk = build_packed(ix, tile_log2)
     want_shift = 0 if dtype == np.uint8 else O.pack_shift(float(np.abs(csr.data.astype(np.float64)).max()))
@@ -97,7 +97,7 @@ def test_search_without_packed_copy(device, dtype):
     from gpusparse.index import default_tile_log2, ensure_search_state
     rng = np.random.default_rng(5)
     csr = random_csr(rng, 30000, 60, max_len=12, dtype=dtype, dup_rate=0.02)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti, tw = random_queries(rng, 24, 60, max_len=9, dtype=np.uint8 if dtype == np.uint8 else np.float32)
     print(f"packed vs plain scorer {dtype.__name__}", flush=True)
@@ -125,7 +125,7 @@ def test_rescoring_without_forward_copy(c1):
 
 def test_build_generated_c1(device):
     docs, _ = synth.generate("C1")
-    ix = gs.build_index(docs, device)
+    ix = gs.build_from_csr(docs, device)
     assert_index_equal(ix, oracle_index(docs))
 
 
@@ -159,7 +159,7 @@ def test_build_from_lists_and_torch_sparse(device):
 
 def test_chunk_bounds_and_ascending_check(device):
     csr = random_csr(np.random.default_rng(10), 3000, 120, dup_rate=0.02)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     for chunk in (1, 100, 1024, 2999, 5000):
         b = gs.build_chunk_boundaries(ix, chunk).cpu().numpy()
@@ -186,7 +186,7 @@ def test_chunk_bounds_and_ascending_check(device):
 @pytest.fixture(scope="module")
 def c1(device):
     docs, queries = synth.generate("C1")
-    ix = gs.build_index(docs, device)
+    ix = gs.build_from_csr(docs, device)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
     return ix, oracle_index(docs), ti, tw
 
@@ -237,7 +237,7 @@ def test_search_few_tiles_with_dirty_workspace(device, n_docs, tile_log2):
     oracle's answer whatever the workspace held before the call."""
     rng = np.random.default_rng(n_docs)
     csr = random_csr(rng, n_docs, 90, dup_rate=0.05)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti, tw = random_queries(rng, 20, 90, max_len=8)
     assert_search_equal(ix, ref, ti, tw, 7, path="fused", tile_log2=tile_log2)
@@ -253,7 +253,7 @@ def test_search_edge_cases(device, dtype):
     documents fill the list by ascending id) and k > N (clamped)."""
     rng = np.random.default_rng(21)
     csr = random_csr(rng, 700, 50, dtype=dtype, dup_rate=0.05, empty_rate=0.3, max_len=4)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     qdt = np.uint8 if dtype == np.uint8 else np.float32
     ti, tw = random_queries(rng, 12, 50, dtype=qdt, invalid_rate=0.3, max_len=5)
@@ -269,7 +269,7 @@ def test_search_edge_cases(device, dtype):
 def test_search_f16_config_reduced(device):
     cfg = synth.scaled(synth.CONFIGS["C3"], n_docs=300_000, n_queries=64)
     docs, queries = synth.generate(cfg)
-    ix = gs.build_index(docs, device)
+    ix = gs.build_from_csr(docs, device)
     assert ix.scores.dtype == torch.float16
     ref = oracle_index(docs)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
@@ -282,7 +282,7 @@ def test_search_f16_config_reduced(device):
 def c3_small(device):
     cfg = synth.scaled(synth.CONFIGS["C3"], n_docs=120_000, n_queries=24)
     docs, queries = synth.generate(cfg)
-    ix = gs.build_index(docs, device)
+    ix = gs.build_from_csr(docs, device)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
     return ix, oracle_index(docs), ti, tw
 
@@ -320,7 +320,7 @@ def test_heavy_terms_matches_oracle(device, vocab, seed):
     rng = np.random.default_rng(seed)
     print(f"heavy terms vocab={vocab}", flush=True)
     csr = random_csr(rng, 4000, vocab, max_len=12, dtype=np.float32)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     assert np.array_equal(heavy_terms(ix).cpu().numpy(), O.heavy_terms(ix.lengths.cpu().numpy()))
 
 
@@ -341,7 +341,7 @@ def test_grouped_queries_many_blocks(device):
     multiple of the group size), and queries repeating terms."""
     rng = np.random.default_rng(7)
     csr = random_csr(rng, 6000, 200, max_len=20, dtype=np.float16, dup_rate=0.02)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti, tw = random_queries(rng, 1503, 200, max_len=10)
     ti[::11, 1] = ti[::11, 0]
@@ -376,7 +376,7 @@ def test_packed_scores_exact_under_near_ties(device, dtype, pattern):
     indptr = np.cumsum([0] + [len(t) for t, _ in rows]).astype(np.int64)
     csr = CSR(indptr, np.concatenate([t for t, _ in rows]).astype(np.int32),
               np.concatenate([w for _, w in rows]).astype(dtype), (n_docs, vocab))
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti = np.array([[0, 1, 2, 3, 4, 5], [2, 3, 5, -1, -1, -1], [0, 0, 1, 4, -1, -1], [5, 4, 3, 2, 1, 0]], np.int32)
     tw = np.array([[0.7, 1.3, 0.9, 2.1, 0.4, 1.0], [1.0, 1.0, 1.0, 0, 0, 0], [0.5, 0.25, 3.0, 1.0, 0, 0],
@@ -390,7 +390,7 @@ def test_packed_scores_exact_under_near_ties(device, dtype, pattern):
 def test_search_u8_config_reduced(device):
     cfg = synth.scaled(synth.CONFIGS["C5"], n_docs=300_000, n_queries=64)
     docs, queries = synth.generate(cfg)
-    ix = gs.build_index(docs, device)
+    ix = gs.build_from_csr(docs, device)
     assert ix.scores.dtype == torch.uint8
     ref = oracle_index(docs)
     assert_index_equal(ix, ref)
@@ -406,7 +406,7 @@ def test_search_queries_repeating_terms(device, tile_log2):
     than its query group has queries (groups of 16, 4 and 2 queries here)."""
     rng = np.random.default_rng(31)
     csr = random_csr(rng, 30000, 40, max_len=12)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti, tw = random_queries(rng, 24, 40, max_len=6)
     # column 0 three times, columns 1 and 2 twice, with other weights
@@ -417,12 +417,37 @@ def test_search_queries_repeating_terms(device, tile_log2):
         assert_search_equal(ix, ref, ti, tw, k, path="fused", tile_log2=tile_log2)
 
 
+@pytest.mark.parametrize("packed", [True, False])
+@pytest.mark.parametrize("unroll", [1, 4, 16])
+def test_search_terms_held_by_more_than_64_slots(device, packed, unroll):
+    """256-doc tiles put 32 queries in a group; every query holds one term three
+    times, so that term has more than 64 (slot, weight) entries in each group (the
+    scorer's per-entry loop for such terms).  Lists repeat docs, so with one
+    posting per lane a chunk can be full; otherwise chunks end inside the tile."""
+    from gpusparse.index import ensure_search_state
+    rng = np.random.default_rng(47)
+    csr = random_csr(rng, 20000, 30, max_len=10, dup_rate=0.05)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = random_queries(rng, 40, 30, max_len=5)
+    ti = np.ascontiguousarray(np.concatenate([ti, np.full((40, 3), 3, np.int32)], axis=1))
+    tw = np.ascontiguousarray(np.concatenate([tw, np.tile(np.float32([0.5, 1.25, 2.0]), (40, 1))], axis=1))
+    a = ensure_search_state(ix, 8)
+    if not packed:
+        a[("packed", 8)] = None
+    plan = gs.search_plan(ix, 40, ti.shape[1], 200, tile_log2=8, unroll=unroll)
+    assert plan["group_size"] == 32 and plan["packed"] == packed
+    print(f"term in >64 slots packed={packed} unroll={unroll}", flush=True)
+    for k in (10, 200):
+        assert_search_equal(ix, ref, ti, tw, k, path="fused", tile_log2=8, unroll=unroll)
+
+
 @pytest.mark.parametrize("tile_log2,tiles_per_wg", [(8, 0), (10, 0), (12, 0), (13, 0), (10, 4), (13, 2)])
 def test_search_head_heavy_reduced(device, tile_log2, tiles_per_wg):
     """Wide head-heavy queries: group unions above one LDS batch of terms."""
     cfg = synth.scaled(synth.CONFIGS["C4"], n_docs=200_000, n_queries=32)
     docs, queries = synth.generate(cfg)
-    ix = gs.build_index(docs, device)
+    ix = gs.build_from_csr(docs, device)
     ref = oracle_index(docs)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
     print(f"C4 reduced tile_log2={tile_log2} tiles_per_wg={tiles_per_wg} T={ti.shape[1]}", flush=True)
@@ -455,7 +480,7 @@ def test_compacted_topk_matches_oracle(device):
 def test_scatter_add_matches_oracle(device, dtype):
     rng = np.random.default_rng(32)
     csr = random_csr(rng, 4000, 200, dtype=dtype)
-    ix = gs.build_index(csr, device)
+    ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     qdt = np.uint8 if dtype == np.uint8 else np.float32
     ti, tw = random_queries(rng, 10, 200, dtype=qdt, invalid_rate=0.1)
@@ -499,6 +524,74 @@ def test_reference_entry_points(c1):
         assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
     with pytest.raises(AssertionError, match="power of 2"):
         gs.triton_fused_score(ix, qt, qw, block_pl=100)
+
+
+def test_chunked_entry_points_ignore_bound_contents_and_block_pl(c1):
+    """Contract of this build: triton_chunked_score(_fused) check chunk_bounds for
+    shape (and the lists for ascending order) but schedule by their own tile
+    bounds, so the contents of a well-shaped table do not change the answer;
+    block_pl is validated (power of two) and has no effect."""
+    ix, ref, ti, tw = c1
+    qt, qw = torch.from_numpy(ti[:24]).cuda(), torch.from_numpy(tw[:24]).cuda()
+    vs, _, vi = O.c_search(ref, ti[:24], tw[:24], 50, threads=8)
+    good = gs.build_chunk_boundaries(ix, 30000)
+    junk = torch.zeros_like(good)
+    for bounds in (good, junk):
+        for block_pl in (32, 128, 1024):
+            for fn in (gs.triton_chunked_score, gs.triton_chunked_score_fused):
+                s, i = fn(ix, qt, qw, top_k=50, doc_chunk=30000, block_pl=block_pl, chunk_bounds=bounds)
+                assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+    with pytest.raises(ValueError, match="shape"):
+        gs.triton_chunked_score_fused(ix, qt, qw, top_k=50, doc_chunk=30000, chunk_bounds=good[:-1])
+
+
+def test_k_and_width_limits_raise_value_error(c1):
+    """Documented limits: k above 8192 (the LDS selection's capacity) and query
+    widths above 8192 terms raise ValueError instead of answering."""
+    ix, ref, ti, tw = c1
+    assert gs.MAX_K == 8192
+    q = (torch.from_numpy(ti[:2]), torch.from_numpy(tw[:2]))
+    with pytest.raises(ValueError, match="8192"):
+        gs.search(ix, q, 8193)
+    with pytest.raises(ValueError, match="8192"):
+        gs.triton_fused_score(ix, q[0], q[1], top_k=9000)
+    wide_t = torch.full((1, 8193), 5, dtype=torch.int32)
+    with pytest.raises(ValueError, match="8192"):
+        gs.search(ix, (wide_t, torch.ones((1, 8193))), 10, path="fused")
+    s, i = gs.search(ix, q, 8192)
+    vs, _, vi = O.c_search(ref, ti[:2], tw[:2], 8192, threads=8)
+    assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.uint8])
+def test_reference_builders_store_float32(device, dtype):
+    """build_index / build_gpu_index_from_csr store float32 weights whatever the
+    CSR holds, as the reference does (gpusparse_retrieval.py:98), and answer
+    float32 queries; weight_dtype opts into the native types."""
+    rng = np.random.default_rng(3)
+    csr = random_csr(rng, 3000, 200, dtype=dtype, max_len=10)
+    ti, tw = random_queries(rng, 16, 200, max_len=6, dtype=np.float32)
+    if dtype == np.uint8:
+        tw = np.rint(tw * 40).clip(1, 255).astype(np.float32)
+    f32 = CSR(csr.indptr, csr.indices, csr.data.astype(np.float32), csr.shape)
+    ref = oracle_index(f32)
+    for build in (gs.build_index, gs.build_gpu_index_from_csr):
+        ix = build(csr, device)
+        assert ix.scores.dtype == torch.float32
+        assert np.array_equal(ix.scores.cpu().numpy(), ref["scores"])
+        s, i = gs.triton_fused_score(ix, torch.from_numpy(ti).cuda(), torch.from_numpy(tw).cuda(), top_k=20)
+        vs, _, vi = O.c_search(ref, ti, tw, 20, threads=8)
+        assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+    native = gs.build_index(csr, device, weight_dtype=torch.float16 if dtype == np.float16 else torch.uint8)
+    assert native.scores.dtype == (torch.float16 if dtype == np.float16 else torch.uint8)
+    if dtype == np.uint8:
+        # float query weights that are integers in [0, 255] are the uint8 impacts
+        nref = oracle_index(csr)
+        s, i = gs.search(native, (torch.from_numpy(ti), torch.from_numpy(tw)), 20)
+        vs, _, vi = O.c_search(nref, ti, tw.astype(np.uint8), 20, threads=8)
+        assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+        with pytest.raises(ValueError, match="integers"):
+            gs.search(native, (torch.from_numpy(ti), torch.from_numpy(tw + 0.5)), 20)
 
 
 def test_retrieve_and_run_engine(device, tmp_path):

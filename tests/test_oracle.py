@@ -317,3 +317,47 @@ def test_to_query_tensors_oracle():
     assert T == 3
     assert ti.tolist() == [[4, 1, 9], [-1, -1, -1], [2, 2, -1]]
     assert ts.tolist() == [[.5, .25, 1.], [0, 0, 0], [2., 3., 0]]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.uint8])
+def test_posting_checksum_detects_planted_changes(dtype):
+    """The full-size index check: CSR and index checksums agree on an index and
+    its CSR, and each planted mistake (in the oracle's index, on the CPU) changes
+    the checksum or the layout count."""
+    rng = np.random.default_rng(5)
+    csr = random_csr(rng, 400, 60, dtype=dtype, max_len=15)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 400, 60)
+    want = O.checksum_csr(csr.indptr, csr.indices, csr.data)
+    assert O.checksum_index(ix) == (want, 0)
+    t = int(np.argmax(ix["lengths"]))
+    o, n = int(ix["offsets"][t]), int(ix["lengths"][t])
+
+    def planted(fn):
+        j = {k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in ix.items()}
+        fn(j)
+        return O.checksum_index(j)
+
+    def move(j):   # a posting filed under the wrong doc
+        j["doc_ids"][o] = (j["doc_ids"][o] + 1) % 400
+
+    def alter(j):  # one weight bit flipped
+        j["scores"].view(np.uint8)[o * j["scores"].itemsize] ^= 1
+
+    def drop(j):   # last posting lost (list shortened, slot padded)
+        j["lengths"][t] -= 1
+        j["doc_ids"][o + n - 1] = -1
+        j["scores"][o + n - 1] = 0
+
+    def swap_terms(j):  # two postings exchanged between lists
+        t2 = int(np.argsort(j["lengths"])[-2])
+        o2 = int(j["offsets"][t2])
+        j["doc_ids"][o], j["doc_ids"][o2] = j["doc_ids"][o2], j["doc_ids"][o]
+
+    for fn in (move, alter, drop, swap_terms):
+        assert planted(fn)[0] != want, fn.__name__
+
+    def dirty_pad(j):
+        j["doc_ids"][o + n] = 3 if j["padded_lengths"][t] > n else j["doc_ids"][o + n]
+
+    if ix["padded_lengths"][t] > n:
+        assert planted(dirty_pad)[1] == 1

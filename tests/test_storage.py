@@ -71,7 +71,7 @@ def test_gpu_round_trip_searches_identically(device, tmp_path):
     from gpusparse import synth
     cfg = synth.scaled(synth.CONFIGS["C1"], n_docs=60_000, n_queries=16)
     docs, queries = synth.generate(cfg)
-    ix = gs.build_index(docs, device)
+    ix = gs.build_from_csr(docs, device)
     p = str(tmp_path / "c1.gsp")
     gs.save_index(ix, p, forward=True)
     back = gs.load_index(p, device, verify=True)

@@ -90,3 +90,22 @@ def test_u8_code_closed_form():
 def test_config_manifest(name):
     m = synth.manifest(name)
     assert m["name"] == name and m["docs"]["vocab"] == 30522
+
+
+def test_c4_is_head_heavy():
+    """C4's defining property at its full size (1M docs): each of the 50 most
+    frequent terms holds more than 200K postings, and every query holds at least
+    8 of those 50 terms (its forced head terms) within at most 256 terms."""
+    cfg = synth.CONFIGS["C4"]
+    docs = synth.generate_rows(cfg.docs, cfg.seed, synth.STREAM_DOCS)
+    assert docs.shape[0] == 1_000_000
+    df = np.bincount(docs.indices, minlength=synth.VOCAB)
+    top50 = np.argsort(-df, kind="stable")[:50]
+    assert df[top50].min() > 200_000
+    assert set(top50.tolist()) == set(range(50))  # term id = Zipf rank - 1
+    queries = synth.generate_rows(cfg.queries, cfg.seed, synth.STREAM_QUERIES)
+    lens = np.diff(queries.indptr)
+    assert lens.max() <= 256 and lens.min() >= 16
+    rows = np.repeat(np.arange(queries.shape[0]), lens)
+    held = np.bincount(rows[queries.indices < 50], minlength=queries.shape[0])
+    assert held.min() >= 8
