@@ -34,6 +34,7 @@
 //    tiles written to a full row, then an exact radix select).
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "gs_topk.h"
@@ -1883,17 +1884,23 @@ extern "C" int gs_search_counts(const gs_index *index, int32_t B, int32_t T, int
     return GS_OK;
 }
 
-extern "C" int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d, int32_t B,
-                         int32_t T, int32_t k, const gs_search_opts *opts, void *out_scores_d, int64_t *out_ids_d,
-                         int32_t *status_d, void *workspace_d, size_t workspace_bytes, void *stream) {
+namespace {
+int check_search_args(const gs_index *index, int32_t B, int32_t T, int32_t k, const gs_search_opts *opts,
+                      const int32_t *q_terms_d, const void *q_weights_d, void *out_scores_d, int64_t *out_ids_d,
+                      int32_t *status_d) {
     if (int rc = check_index(index)) return rc;
     GS_REQUIRE(B > 0 && T > 0, "empty query batch (B=%d, T=%d)", B, T);
     GS_REQUIRE(k >= 1 && k <= kMaxK && (int64_t)k <= index->n_docs, "k=%d outside [1, min(n_docs, %d)]", k, kMaxK);
     GS_REQUIRE(T <= kGroupSortCap, "query width T=%d exceeds %d terms", T, kGroupSortCap);
-    GS_REQUIRE(q_terms_d && q_weights_d && out_scores_d && out_ids_d && status_d && workspace_d, "null pointer");
+    GS_REQUIRE(q_terms_d && q_weights_d && out_scores_d && out_ids_d && status_d, "null pointer");
     GS_REQUIRE(!opts || (opts->tiles_per_wg >= 0 && opts->tiles_per_wg <= 64), "tiles_per_wg=%d outside [0, 64]",
                opts->tiles_per_wg);
-    hipStream_t s = gs_stream(stream);
+    return GS_OK;
+}
+
+int search_dispatch(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d, int32_t B, int32_t T,
+                    int32_t k, const gs_search_opts *opts, void *out_scores_d, int64_t *out_ids_d, int32_t *status_d,
+                    void *workspace_d, size_t workspace_bytes, hipStream_t s) {
     switch (index->wtype) {
         case GS_W_F32:
             return search_impl<GS_W_F32>(index, q_terms_d, q_weights_d, B, T, k, opts, out_scores_d, out_ids_d,
@@ -1905,6 +1912,69 @@ extern "C" int gs_search(const gs_index *index, const int32_t *q_terms_d, const 
             return search_impl<GS_W_U8>(index, q_terms_d, q_weights_d, B, T, k, opts, out_scores_d, out_ids_d,
                                         status_d, workspace_d, workspace_bytes, s);
     }
+}
+}  // namespace
+
+extern "C" int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d, int32_t B,
+                         int32_t T, int32_t k, const gs_search_opts *opts, void *out_scores_d, int64_t *out_ids_d,
+                         int32_t *status_d, void *workspace_d, size_t workspace_bytes, void *stream) {
+    if (int rc = check_search_args(index, B, T, k, opts, q_terms_d, q_weights_d, out_scores_d, out_ids_d, status_d))
+        return rc;
+    GS_REQUIRE(workspace_d, "null workspace");
+    return search_dispatch(index, q_terms_d, q_weights_d, B, T, k, opts, out_scores_d, out_ids_d, status_d,
+                           workspace_d, workspace_bytes, gs_stream(stream));
+}
+
+// ---------------------------------------------------------------------- allocation-free search
+
+// The workspace of gs_search_noalloc: a device array of the library itself, one
+// per GPU the library runs on, held until the process ends.  In host code
+// `scratch` is a host-side stand-in for the array, not a device address; host
+// code only ever uses the address hipGetSymbolAddress reports for the current
+// device (scratch_address below).
+static __device__ __align__(256) unsigned char scratch[GS_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices];  // device address of `scratch` per device, set on the first call there
+
+// Address of the current device's scratch array, looked up once per device
+// with that device current.
+int scratch_address(void **out) {
+    int dev = -1;
+    GS_CHECK_HIP(hipGetDevice(&dev));
+    GS_REQUIRE(dev >= 0 && dev < kScratchDevices, "device %d outside the %d the allocation-free search serves", dev,
+               kScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        GS_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        GS_REQUIRE(p != nullptr, "no device address for the scratch array on device %d", dev);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GS_OK;
+}
+}  // namespace
+
+extern "C" int gs_search_noalloc(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d, int32_t B,
+                                 int32_t T, int32_t k, const gs_search_opts *opts, void *out_scores_d,
+                                 int64_t *out_ids_d, int32_t *status_d, void *stream) {
+    if (int rc = check_search_args(index, B, T, k, opts, q_terms_d, q_weights_d, out_scores_d, out_ids_d, status_d))
+        return rc;
+    gs_arena need{nullptr, 0, 0};
+    plan_search(index, B, T, k, opts, need);
+    if (need.used > GS_NOALLOC_SCRATCH_BYTES) {
+        gs_set_error("this search needs %zu bytes of scratch; the allocation-free search holds %zu (use fewer "
+                     "queries, a smaller cand_cap, or gs_search with a workspace)",
+                     need.used, (size_t)GS_NOALLOC_SCRATCH_BYTES);
+        return GS_ENOSPC;
+    }
+    void *ws = nullptr;
+    if (int rc = scratch_address(&ws)) return rc;
+    return search_dispatch(index, q_terms_d, q_weights_d, B, T, k, opts, out_scores_d, out_ids_d, status_d, ws,
+                           GS_NOALLOC_SCRATCH_BYTES, gs_stream(stream));
 }
 
 extern "C" int gs_search_dense_workspace(const gs_index *index, int32_t rows_per_pass, size_t *bytes) {

@@ -21,6 +21,7 @@ GS_OK, GS_EINVAL, GS_EHIP, GS_ENOSPC = 0, 1, 2, 3
 GS_W_F32, GS_W_F16, GS_W_U8 = 0, 1, 2
 GS_ROW_DONE, GS_ROW_DENSE = 0, 1
 GS_SEARCH_PHASES = 7
+NOALLOC_SCRATCH_BYTES = 256 << 20   # GS_NOALLOC_SCRATCH_BYTES
 PHASE_NAMES = ("query_prep", "threshold_seed", "scoring", "candidate_select", "fp64_rescore", "final_sort")
 ABI_VERSION = 6
 
@@ -127,6 +128,8 @@ SIGNATURES = {
                                  C.POINTER(GsSearchPlanInfo)]),
     "gs_search": (C.c_int, [C.POINTER(GsIndex), _P, _P, _I32, _I32, _I32, C.POINTER(GsSearchOpts), _P, _P,
                             _P, _P, _SZ, _P]),
+    "gs_search_noalloc": (C.c_int, [C.POINTER(GsIndex), _P, _P, _I32, _I32, _I32, C.POINTER(GsSearchOpts), _P, _P,
+                                    _P, _P]),
     "gs_search_counts": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts), _P, _SZ, _P, _P,
                                    _P]),
     "gs_search_dense_workspace": (C.c_int, [C.POINTER(GsIndex), _I32, C.POINTER(_SZ)]),

@@ -219,6 +219,24 @@ int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_wei
               int64_t *out_ids_d, int32_t *status_d, void *workspace_d, size_t workspace_bytes,
               void *stream);
 
+/* ------------------------------------------------------------ allocation-free search
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): gs_search with its workspace in a scratch array of the
+ * library itself, GS_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load
+ * on a GPU until the process ends.  Same arguments (minus the workspace),
+ * results and status as gs_search; the caller still passes inputs and outputs.
+ * GS_ENOSPC, with a message, when the search needs more scratch than that
+ * (gs_search_workspace reports the need): e.g. B = 512, T = 107, k = 1000 fits
+ * with cand_cap <= 32768, and B <= 256 fits at the default caps.  The scratch
+ * keeps the last call's contents; every call clears what it needs cleared.
+ * Calls that overlap on one GPU (other threads, other streams) share that GPU's
+ * array and race: serialise them.  Allocates nothing and does not synchronise. */
+#define GS_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+int gs_search_noalloc(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d, int32_t B,
+                      int32_t T, int32_t k, const gs_search_opts *opts, void *out_scores_d, int64_t *out_ids_d,
+                      int32_t *status_d, void *stream);
+
 /* Candidate counts of the gs_search that last ran on `workspace_d` with the same
  * (index, B, T, k, opts) (no counterpart in the reference: an introspection call
  * for benchmarks), per scoring slot: cand_d[s] <- docs the fused scorer emitted
