@@ -14,6 +14,7 @@
 #include <stdarg.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "gs_common.h"
 
@@ -157,18 +158,30 @@ __device__ __forceinline__ uint32_t load_code(const void *p, int64_t i, int src_
     return reinterpret_cast<const uint8_t *>(p)[i];
 }
 
+// Radix tile of this workgroup.  Workgroup i runs on XCD i % 8; XCD x takes the
+// tiles [x*q + min(x, r), ...) in order (q, r = nblocks / 8, nblocks % 8), so the
+// workgroups resident on one XCD hold neighbouring tiles, and their writes into
+// one digit's region (or one digit's row of the histogram) fall next to each
+// other in that XCD's L2 and leave it as whole lines.
+__device__ __forceinline__ int64_t rs_tile(int64_t nblocks) {
+    const int64_t p = blockIdx.x, x = p & 7;
+    const int64_t q = nblocks >> 3, r = nblocks & 7;
+    return x * q + (x < r ? x : r) + (p >> 3);
+}
+
 __global__ void __launch_bounds__(kRsThreads) k_rs_hist(const uint32_t *__restrict__ key, int64_t n, int shift,
                                                         uint32_t *__restrict__ hist, int64_t nblocks) {
     __shared__ uint32_t h[256];
     h[threadIdx.x] = 0;
     __syncthreads();
-    const int64_t base = blockIdx.x * (int64_t)kRsTile;
+    const int64_t tile = rs_tile(nblocks);
+    const int64_t base = tile * kRsTile;
     for (int r = 0; r < kRsRounds; ++r) {
         int64_t i = base + r * kRsThreads + threadIdx.x;
         if (i < n) atomicAdd(&h[(key[i] >> shift) & 255u], 1u);
     }
     __syncthreads();
-    hist[(int64_t)threadIdx.x * nblocks + blockIdx.x] = h[threadIdx.x];
+    hist[(int64_t)threadIdx.x * nblocks + tile] = h[threadIdx.x];
 }
 
 // Device-wide exclusive scan of uint32 (three launches).
@@ -215,38 +228,67 @@ __global__ void __launch_bounds__(1024) k_scan_down(uint32_t *__restrict__ data,
     }
 }
 
-// Stable scatter of one 8-bit digit.  Entries of a block are taken in rounds of
-// 256 (wave w of round r owns entries r*256 + w*64 + lane), so the rank of an
-// entry among equal digits is: digits of earlier rounds + earlier waves of this
-// round + earlier lanes of this wave (from a 64-lane ballot match).
+// Stable scatter of one 8-bit digit.  A block owns tile b = rs_tile(): kRsTile
+// consecutive entries, wave w the kRsTile/4 of them from w*kRsTile/4 on:
+//  1. every lane loads its kRsRounds entries (entry r*64 + lane of its wave's
+//     range), all loads in flight together;
+//  2. each wave ranks its entries among equal digits on its own, in order
+//     (earlier rounds: the wave's running digit counts in LDS; earlier lanes of
+//     the round: a 64-lane ballot match), with no block barrier;
+//  3. the waves' digit counts give each entry its place in the block's staged
+//     (digit-major, stable) order: the block's run of the digit starts at
+//     l_off[digit], wave w's part of it after the parts of waves 0..w-1;
+//  4. keys, then doc ids, then codes pass through one LDS buffer in staged
+//     order and are written out from it: consecutive threads write consecutive
+//     positions of a digit's run, so a wave's stores land in a few contiguous
+//     runs instead of one scattered word per lane.  One 16 KiB buffer (not
+//     three) keeps several blocks resident per CU.
+// The block's run of digit t starts at global position scanned[t*nblocks + b]
+// (the scanned digit-major histogram).  FINAL (the last pass of the index
+// build): the entry of term k at sorted position pos goes to padded slot
+// pos + delta[k], as its doc id and weight.
 template <bool FINAL, int WT>
-__global__ void __launch_bounds__(kRsThreads)
+__global__ void __launch_bounds__(kRsThreads, 4)
     k_rs_scatter(const uint32_t *__restrict__ key_in, const uint32_t *__restrict__ doc_in,
                  const void *__restrict__ code_in, int src_code_bytes, int64_t n, int shift, int bits,
                  const uint32_t *__restrict__ scanned, int64_t nblocks, uint32_t *__restrict__ key_out,
                  uint32_t *__restrict__ doc_out, uint32_t *__restrict__ code_out,
                  const int64_t *__restrict__ delta, int32_t *__restrict__ final_doc,
                  void *__restrict__ final_w) {
-    __shared__ uint32_t run[256];
-    __shared__ uint32_t wcnt[4][256];
-    const int tid = threadIdx.x, lane = gs_lane(), wave = tid >> 6;
-    run[tid] = scanned[(int64_t)tid * nblocks + blockIdx.x];
-    const int64_t base = blockIdx.x * (int64_t)kRsTile;
+    constexpr int kWaves = kRsThreads / 64, kPerWave = kRsTile / kWaves;
+    __shared__ uint32_t s_buf[kRsTile];
+    __shared__ uint32_t g_run[256];          // global position of this block's run of each digit
+    __shared__ uint32_t l_off[256];          // start of each digit's run in the staged order
+    __shared__ uint32_t wcnt[kWaves][256];   // per wave: digits seen, then the wave's offset in the run
+    __shared__ uint32_t sh[17];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = gs_lane();
+    const int64_t tile = rs_tile(nblocks);
+    const int64_t base = tile * kRsTile;
+    const int cnt = (int)(n - base < kRsTile ? n - base : kRsTile);
+    const int wbase = wave * kPerWave;
+
+    uint32_t k[kRsRounds], d[kRsRounds], c[kRsRounds], lp[kRsRounds];
+#pragma unroll
     for (int r = 0; r < kRsRounds; ++r) {
-        wcnt[0][tid] = 0;
-        wcnt[1][tid] = 0;
-        wcnt[2][tid] = 0;
-        wcnt[3][tid] = 0;
-        __syncthreads();
-        const int64_t i = base + r * kRsThreads + tid;
-        const bool valid = i < n;
-        uint32_t k = 0, d = 0, c = 0, dig = 0;
-        if (valid) {
-            k = key_in[i];
-            d = doc_in[i];
-            c = load_code(code_in, i, src_code_bytes);
-            dig = (k >> shift) & 255u;
+        const int j = wbase + r * 64 + lane;
+        k[r] = d[r] = 0;
+        if (j < cnt) {
+            k[r] = key_in[base + j];
+            d[r] = doc_in[base + j];
         }
+    }
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) wcnt[w][tid] = 0;
+    {
+        const int64_t idx = (int64_t)tid * nblocks + tile;
+        g_run[tid] = scanned[idx];
+    }
+    __syncthreads();
+    // 2. wave-local stable ranks (lp = rank among the wave's entries of that digit)
+#pragma unroll
+    for (int r = 0; r < kRsRounds; ++r) {
+        const bool valid = wbase + r * 64 + lane < cnt;
+        const uint32_t dig = (k[r] >> shift) & 255u;
         uint64_t peers = __ballot(valid);
         for (int b = 0; b < bits; ++b) {
             const bool bit = (dig >> b) & 1u;
@@ -254,31 +296,96 @@ __global__ void __launch_bounds__(kRsThreads)
             peers &= bit ? m : ~m;
         }
         const uint32_t rank = __popcll(peers & gs_lanemask_lt());
-        if (valid && rank == 0) wcnt[wave][dig] = __popcll(peers);
-        __syncthreads();
-        if (valid) {
-            uint32_t pos = run[dig] + rank;
-            for (int w = 0; w < wave; ++w) pos += wcnt[w][dig];
+        uint32_t seen = 0;
+        if (valid) seen = wcnt[wave][dig];
+        __builtin_amdgcn_wave_barrier();
+        lp[r] = seen + rank;
+        if (valid && rank == 0) wcnt[wave][dig] = seen + (uint32_t)__popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    // 3. the block's digit counts, their exclusive scan, and each wave's offset in a run
+    {
+        uint32_t tot_d = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const uint32_t x = wcnt[w][tid];
+            wcnt[w][tid] = tot_d;
+            tot_d += x;
+        }
+        uint32_t tot;
+        l_off[tid] = block_excl_scan<uint32_t>(tot_d, sh, &tot);
+    }
+    __syncthreads();  // every digit's l_off is read by other waves below
+#pragma unroll
+    for (int r = 0; r < kRsRounds; ++r) {
+        const uint32_t dig = (k[r] >> shift) & 255u;
+        lp[r] += l_off[dig] + wcnt[wave][dig];
+    }
+    // 4. keys, then doc ids, then codes through the staging buffer
+#pragma unroll
+    for (int r = 0; r < kRsRounds; ++r)
+        if (wbase + r * 64 + lane < cnt) s_buf[lp[r]] = k[r];
+    // the codes are loaded only now, into the registers the keys held
+#pragma unroll
+    for (int r = 0; r < kRsRounds; ++r) {
+        const int j = wbase + r * 64 + lane;
+        c[r] = j < cnt ? load_code(code_in, base + j, src_code_bytes) : 0u;
+    }
+    __syncthreads();
+    // destination of staged entry i*256 + tid: sorted position, or padded slot (FINAL)
+    using Dst = typename std::conditional<FINAL, int64_t, uint32_t>::type;
+    Dst dst[kRsRounds];
+#pragma unroll
+    for (int i = 0; i < kRsRounds; ++i) {
+        const int j = i * kRsThreads + tid;
+        dst[i] = 0;
+        if (j < cnt) {
+            const uint32_t kk = s_buf[j];
+            const uint32_t dig = (kk >> shift) & 255u;
+            const uint32_t pos = g_run[dig] + ((uint32_t)j - l_off[dig]);
             if (FINAL) {
-                const int64_t slot = (int64_t)pos + delta[k];
-                final_doc[slot] = (int32_t)d;
-                if (WT == GS_W_F32)
-                    reinterpret_cast<uint32_t *>(final_w)[slot] = c;
-                else if (WT == GS_W_F16)
-                    reinterpret_cast<uint16_t *>(final_w)[slot] = (uint16_t)c;
-                else
-                    reinterpret_cast<uint8_t *>(final_w)[slot] = (uint8_t)c;
+                dst[i] = (int64_t)pos + delta[kk];
             } else {
-                key_out[pos] = k;
-                doc_out[pos] = d;
-                code_out[pos] = c;
+                dst[i] = pos;
+                key_out[pos] = kk;
             }
         }
-        __syncthreads();
-        run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
-        __syncthreads();
     }
-    (void)lane;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRsRounds; ++r)
+        if (wbase + r * 64 + lane < cnt) s_buf[lp[r]] = d[r];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kRsRounds; ++i) {
+        const uint32_t v = s_buf[i * kRsThreads + tid];
+        if (i * kRsThreads + tid < cnt) {
+            if (FINAL)
+                final_doc[dst[i]] = (int32_t)v;
+            else
+                doc_out[dst[i]] = v;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRsRounds; ++r)
+        if (wbase + r * 64 + lane < cnt) s_buf[lp[r]] = c[r];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kRsRounds; ++i) {
+        const uint32_t v = s_buf[i * kRsThreads + tid];
+        if (i * kRsThreads + tid < cnt) {
+            if (!FINAL)
+                code_out[dst[i]] = v;
+            else if (WT == GS_W_F32)
+                reinterpret_cast<uint32_t *>(final_w)[dst[i]] = v;
+            else if (WT == GS_W_F16)
+                reinterpret_cast<uint16_t *>(final_w)[dst[i]] = (uint16_t)v;
+            else
+                reinterpret_cast<uint8_t *>(final_w)[dst[i]] = (uint8_t)v;
+        }
+    }
 }
 
 // ------------------------------------------------------------------ forward (doc-major) copy
