@@ -124,14 +124,30 @@ def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
             raise SystemExit(f"no {name} dispatch under {os.path.join(d, sub)}")
         return rows[max(rows)]
 
+    def dispatches(sub, names):
+        rows = {}
+        for path in glob.glob(os.path.join(d, sub, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                if any(n in r["Kernel_Name"] for n in names):
+                    did = int(r["Dispatch_Id"])
+                    name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+                    rows.setdefault(did, [name, 0.0])[1] += float(r["Counter_Value"])
+        return [rows[k] for k in sorted(rows)]
+
     f, w = last("f", "k_score_union"), last("w", "k_score_union")
     cf, cw = last("cf", "copyBuffer"), last("cw", "copyBuffer")
     fs, ws = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+    # the radix passes of the index build (term keys) and of the doc-major copy
+    # (doc-id keys), in launch order: a histogram, then a scatter, per pass
+    rf, rw = dispatches("f", ("k_rs_hist", "k_rs_scatter")), dispatches("w", ("k_rs_hist", "k_rs_scatter"))
+    radix = [{"kernel": a[0], "fetch_bytes": round(a[1] * 1024 * fs), "write_bytes": round(b[1] * 1024 * ws)}
+             for a, b in zip(rf, rw) if a[0] == b[0]]
     out = {"config": cfg_name, "n_docs": n_docs, "tile_log2": tile_log2, "kernel": "k_score_union",
            "fetch_kib_per_launch": f, "write_kib_per_launch": w, "copy_bytes": copy_bytes,
            "copy_fetch_kib": cf, "copy_write_kib": cw, "fetch_scale": fs, "write_scale": ws,
            "fetch_bytes_per_launch": f * 1024 * fs, "write_bytes_per_launch": w * 1024 * ws,
            "traffic_bytes_per_launch": f * 1024 * fs + w * 1024 * ws,
+           "radix_dispatches": radix,
            "commands": [
                f"rocprofv3 --pmc FETCH_SIZE -d <out>/f -o f --output-format csv -- python3 bench.py --config {cfg_name} "
                "--no-cpu --parity-queries 0 --steps 1 --warmup 1",
