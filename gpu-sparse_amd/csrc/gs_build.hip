@@ -621,26 +621,122 @@ __global__ void k_tile_bounds(const int32_t *__restrict__ doc, const int64_t *__
 // float weights the int16 rint(w * 2^shift) (w * 2^shift is exact in fp64 and
 // rounded once, half to even; clamped to +-32767).  Padding slots (doc < 0) hold 0.
 template <int WT>
+__device__ __forceinline__ uint32_t pack_word(int32_t d, const void *__restrict__ w, int64_t i, uint32_t mask,
+                                              int32_t shift) {
+    if (d < 0) return 0u;
+    const uint32_t off = ((uint32_t)d & mask) << 2;
+    uint32_t wq;
+    if (WT == GS_W_U8) {
+        wq = reinterpret_cast<const uint8_t *>(w)[i];
+    } else {
+        const double x = gs_weight<WT>::decode(reinterpret_cast<const typename gs_weight<WT>::store_t *>(w)[i]);
+        const double r = rint(ldexp(x, shift));
+        const int32_t q = (int32_t)fmin(fmax(r, -32767.0), 32767.0);
+        wq = (uint32_t)(uint16_t)(int16_t)q;
+    }
+    return off | (wq << 16);
+}
+
+template <int WT>
 __global__ void k_pack_postings(const int32_t *__restrict__ doc, const void *__restrict__ w, int64_t n,
                                 int32_t tile_log2, int32_t shift, uint32_t *__restrict__ out) {
     const uint32_t mask = (1u << tile_log2) - 1u;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const int32_t d = doc[i];
-        if (d < 0) {
-            out[i] = 0u;
-            continue;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = pack_word<WT>(doc[i], w, i, mask, shift);
+}
+
+// Bank-aware order of the packed copy inside each (term, tile) sub-range.  The
+// scorer adds a sub-range's postings 64 at a time -- one ds_add_u32 per lane,
+// groups aligned to the sub-range's start -- into the words of their docs, and
+// postings whose docs agree mod 64 fall in one LDS bank.  Any order inside a
+// sub-range gives the same sums, so a sub-range of n > 64 postings (G groups,
+// the last one holding n_last = n - 64 (G - 1)) is rewritten "column-major by
+// residue": its postings sorted by (doc mod 64, doc) are dealt to the groups
+// in turn -- the k-th of them to group k mod G, position k / G, while every
+// group has room at that position (k < n_last * G), then to the first G - 1
+// groups only.  The postings of one residue land in different groups while
+// they last, so a group holds a residue ceil(count / G) times at most (2 for
+// random docs), where docs in ascending order pile 3-5 lanes onto one bank.
+// One thread per (term, tile); its wave rewrites the wave's sub-ranges of more
+// than 64 postings one after the other: a pass counting residues, then a pass
+// that ranks each posting among its residue (64-lane ballot match plus the
+// wave's running counts) and writes its word to its place.
+template <int WT>
+__global__ void __launch_bounds__(256)
+    k_pack_arrange(const int32_t *__restrict__ doc, const void *__restrict__ w, const int64_t *__restrict__ offsets,
+                   const int32_t *__restrict__ tb, int32_t V, int64_t n_tiles, int32_t tile_log2, int32_t shift,
+                   uint32_t *__restrict__ out) {
+    __shared__ uint32_t s_cnt[4][64], s_run[4][64], s_below[4][64];
+    const int lane = gs_lane(), wave = threadIdx.x >> 6;
+    const uint32_t mask = (1u << tile_log2) - 1u;
+    const int64_t g = blockIdx.x * 256ll + threadIdx.x;
+    int64_t s = 0;
+    int n = 0;
+    if (g < (int64_t)V * n_tiles) {
+        const int64_t t = g / n_tiles, j = g - t * n_tiles;
+        const int32_t *b = tb + t * (n_tiles + 1) + j;
+        n = b[1] - b[0];
+        s = offsets[t] + b[0];
+    }
+    uint64_t todo = __ballot(n > 64);
+    while (todo) {
+        const int src = __ffsll((long long)todo) - 1;
+        todo &= todo - 1;
+        const int64_t ss = ((int64_t)__builtin_amdgcn_readlane((int)(s >> 32), src) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)s, src);
+        const int nn = __builtin_amdgcn_readlane(n, src);
+        const int G = (nn + 63) >> 6, nl = nn - 64 * (G - 1);
+        s_cnt[wave][lane] = 0;
+        __builtin_amdgcn_wave_barrier();
+        for (int c = 0; c < nn; c += 64)
+            if (c + lane < nn) atomicAdd(&s_cnt[wave][doc[ss + c + lane] & 63], 1u);
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t cnt = s_cnt[wave][lane];
+        uint32_t x = cnt;  // inclusive scan of the residue counts over the lanes
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = __shfl_up(x, d, 64);
+            if (lane >= d) x += o;
         }
-        const uint32_t off = ((uint32_t)d & mask) << 2;
-        uint32_t wq;
-        if (WT == GS_W_U8) {
-            wq = reinterpret_cast<const uint8_t *>(w)[i];
-        } else {
-            const double x = gs_weight<WT>::decode(reinterpret_cast<const typename gs_weight<WT>::store_t *>(w)[i]);
-            const double r = rint(ldexp(x, shift));
-            const int32_t q = (int32_t)fmin(fmax(r, -32767.0), 32767.0);
-            wq = (uint32_t)(uint16_t)(int16_t)q;
+        s_below[wave][lane] = x - cnt;
+        s_run[wave][lane] = 0;
+        __builtin_amdgcn_wave_barrier();
+        for (int c = 0; c < nn; c += 64) {
+            const int i = c + lane;
+            const bool valid = i < nn;
+            const int32_t d = valid ? doc[ss + i] : 0;
+            const uint32_t r = (uint32_t)d & 63u;
+            uint64_t peers = __ballot(valid);
+#pragma unroll
+            for (int bit = 0; bit < 6; ++bit) {
+                const bool on = (r >> bit) & 1u;
+                const uint64_t m = __ballot(on);
+                peers &= on ? m : ~m;
+            }
+            const uint32_t rank = __popcll(peers & gs_lanemask_lt());
+            uint32_t seen = 0, below = 0;
+            if (valid) {
+                seen = s_run[wave][r];
+                below = s_below[wave][r];
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (valid && rank == 0) s_run[wave][r] = seen + (uint32_t)__popcll(peers);
+            __builtin_amdgcn_wave_barrier();
+            if (valid) {
+                const uint32_t k = below + seen + rank;  // place in (residue, doc) order
+                uint32_t grp, pos;
+                if (k < (uint32_t)(nl * G)) {
+                    pos = k / (uint32_t)G;
+                    grp = k - pos * (uint32_t)G;
+                } else {
+                    const uint32_t k2 = k - (uint32_t)(nl * G);
+                    const uint32_t q = k2 / (uint32_t)(G - 1);
+                    grp = k2 - q * (uint32_t)(G - 1);
+                    pos = (uint32_t)nl + q;
+                }
+                out[ss + (int64_t)grp * 64 + pos] = pack_word<WT>(d, w, ss + i, mask, shift);
+            }
         }
-        out[i] = off | (wq << 16);
     }
 }
 
@@ -1093,24 +1189,41 @@ extern "C" int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, 
 }
 
 extern "C" int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, int64_t n_slots,
+                                const int64_t *offsets_d, const int32_t *tile_bounds_d, int32_t vocab, int64_t n_docs,
                                 int32_t tile_log2, int32_t w_shift, void *out_d, void *stream) {
     GS_REQUIRE(n_slots >= 0, "n_slots %lld is negative", (long long)n_slots);
     GS_REQUIRE(tile_log2 >= 6 && tile_log2 <= 14, "tile_log2 %d outside [6, 14]", tile_log2);
     GS_REQUIRE(wtype >= GS_W_F32 && wtype <= GS_W_U8, "unknown weight type %d", wtype);
     GS_REQUIRE(wtype == GS_W_U8 || (w_shift >= -200 && w_shift <= 200), "w_shift %d outside [-200, 200]", w_shift);
     GS_REQUIRE(n_slots == 0 || (doc_ids_d && weights_d && out_d), "null pointer");
+    GS_REQUIRE(!tile_bounds_d || (offsets_d && vocab > 0 && n_docs >= 0), "tile bounds need offsets, vocab, n_docs");
     if (n_slots == 0) return GS_OK;
     hipStream_t s = gs_stream(stream);
     const unsigned g = gs_blocks(n_slots, 256, 1 << 16);
     uint32_t *out = reinterpret_cast<uint32_t *>(out_d);
+    const int64_t n_tiles = (n_docs + (1ll << tile_log2) - 1) >> tile_log2;
+    const int64_t pairs = (int64_t)vocab * n_tiles;
+    GS_REQUIRE(!tile_bounds_d || pairs <= (int64_t)256 * 0x7FFFFFFF, "too many (term, tile) pairs");
+    const unsigned ga = (unsigned)((pairs + 255) / 256);
     switch (wtype) {
         case GS_W_F32:
             k_pack_postings<GS_W_F32><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, w_shift, out);
+            if (tile_bounds_d && pairs > 0)
+                k_pack_arrange<GS_W_F32><<<ga, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, tile_bounds_d, vocab,
+                                                            n_tiles, tile_log2, w_shift, out);
             break;
         case GS_W_F16:
             k_pack_postings<GS_W_F16><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, w_shift, out);
+            if (tile_bounds_d && pairs > 0)
+                k_pack_arrange<GS_W_F16><<<ga, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, tile_bounds_d, vocab,
+                                                            n_tiles, tile_log2, w_shift, out);
             break;
-        default: k_pack_postings<GS_W_U8><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, 0, out); break;
+        default:
+            k_pack_postings<GS_W_U8><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, 0, out);
+            if (tile_bounds_d && pairs > 0)
+                k_pack_arrange<GS_W_U8><<<ga, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, tile_bounds_d, vocab,
+                                                           n_tiles, tile_log2, 0, out);
+            break;
     }
     GS_CHECK_LAUNCH();
     return GS_OK;

@@ -420,19 +420,33 @@ class Packed(NamedTuple):
     shift: int
 
 
-def build_packed(index, tile_log2: int) -> Packed | None:
+def build_packed(index, tile_log2: int, arrange: bool = True) -> Packed | None:
     """Packed scoring copy of the postings for one tile size (gs_pack_postings):
     per slot the byte offset of its doc in a tile slice (bits 0-15) and the weight
     (bits 16-31): the uint8 weight, or int16 rint(w * 2^shift) for float weights.
-    None when a weight is not finite."""
+    With `arrange` each (term, tile) sub-range of more than 64 postings is
+    reordered so that every 64-posting group spreads its docs over the residues
+    mod 64 (the LDS banks the scorer adds into); the sums do not depend on the
+    order.  None when a weight is not finite."""
     shift = pack_shift(index)
     if shift is None:
         return None
     dev = _device_of(index)
     n = int(index.doc_ids.numel())
+    N, V = int(index.num_docs), int(index.vocab_size)
+    tb = None
+    if arrange:
+        tb = index.aux().get(("tile_bounds", tile_log2))
+        if tb is None:
+            n_tiles = (N + (1 << tile_log2) - 1) >> tile_log2
+            tb = torch.empty((V, n_tiles + 1), dtype=torch.int32, device=dev)
+            _lib.check(_lib.lib().gs_tile_bounds(_lib.ptr(index.doc_ids), _lib.ptr(index.offsets),
+                                                 _lib.ptr(index.lengths), V, N, tile_log2, _lib.ptr(tb),
+                                                 _lib.stream_ptr(dev)), "gs_tile_bounds")
     out = torch.empty(n, dtype=torch.int32, device=dev)
-    _lib.check(_lib.lib().gs_pack_postings(_lib.ptr(index.doc_ids), _lib.ptr(index.scores), index.wtype, n, tile_log2,
-                                           shift, _lib.ptr(out), _lib.stream_ptr(dev)), "gs_pack_postings")
+    _lib.check(_lib.lib().gs_pack_postings(_lib.ptr(index.doc_ids), _lib.ptr(index.scores), index.wtype, n,
+                                           _lib.ptr(index.offsets), _lib.ptr(tb), V, N,
+                                           tile_log2, shift, _lib.ptr(out), _lib.stream_ptr(dev)), "gs_pack_postings")
     return Packed(out, shift)
 
 

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 6
+#define GS_ABI_VERSION 7
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -172,8 +172,16 @@ int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wty
  * the weight in bits 16..31 -- for GS_W_U8 the uint8 weight, for float weights
  * the int16 rint(w * 2^w_shift) (clamped to +-32767; w_shift from gs_pack_shift
  * keeps every |value| <= 8191).  Padding slots (doc id < 0) hold 0.
+ * With tile_bounds_d (gs_tile_bounds for this tile_log2; offsets_d, vocab and
+ * n_docs of the index) the words of each (term, tile) sub-range of more than 64
+ * postings are reordered so that each 64-posting group aligned to the sub-range's
+ * start spreads its docs over the 64 residues mod 64 (the LDS banks of their
+ * score words): sorted by (doc mod 64, doc), the k-th goes to group k mod G at
+ * position k / G while all G groups have room there, then to the first G - 1.
+ * With tile_bounds_d NULL the words stay in slot order.
  * tile_log2 <= 14; w_shift in [-200, 200] (ignored for GS_W_U8). */
 int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, int64_t n_slots,
+                     const int64_t *offsets_d, const int32_t *tile_bounds_d, int32_t vocab, int64_t n_docs,
                      int32_t tile_log2, int32_t w_shift, void *out_d, void *stream);
 /* The GS_HEAVY_TERMS non-empty posting lists with the most postings (no
  * counterpart in the reference: gs_search's query grouping reads them), as term

@@ -141,12 +141,14 @@ def pack_shift(max_abs: float) -> int:
     return s
 
 
-def pack_postings(index: dict, tile_log2: int, shift: int | None = None) -> np.ndarray:
+def pack_postings(index: dict, tile_log2: int, shift: int | None = None, arrange: bool = True) -> np.ndarray:
     """Packed scoring copy (gs_pack_postings; no reference counterpart: a layout of
     its posting arrays), int32 [n]: per slot (doc mod 2^tile_log2) * 4 in bits 0-15
     and the weight in bits 16-31 -- the uint8 weight, or for float weights the
     int16 rint(w * 2^shift) (half to even, clamped to +-32767), shift defaulting to
-    pack_shift of the largest |w|; padding slots (doc < 0) are 0."""
+    pack_shift of the largest |w|; padding slots (doc < 0) are 0.
+    arrange: each (term, tile) sub-range of n > 64 postings is rewritten in the
+    order arrange_order gives (the sums over a sub-range do not depend on it)."""
     doc = index["doc_ids"].astype(np.int64)
     w = index["scores"]
     ok = doc >= 0
@@ -159,7 +161,45 @@ def pack_postings(index: dict, tile_log2: int, shift: int | None = None) -> np.n
             shift = pack_shift(np.max(np.abs(wf[ok])) if ok.any() else 0.0)
         q = np.clip(np.rint(np.ldexp(wf, shift)), -32767, 32767).astype(np.int16)
         bits = q.view(np.uint16).astype(np.uint32)
-    return (off | (np.where(ok, bits, 0).astype(np.uint32) << 16)).view(np.int32)
+    words = (off | (np.where(ok, bits, 0).astype(np.uint32) << 16)).view(np.int32)
+    if not arrange:
+        return words
+    out = words.copy()
+    n_docs = int(index["num_docs"])
+    edges = np.arange(((n_docs + (1 << tile_log2) - 1) >> tile_log2) + 1, dtype=np.int64) << tile_log2
+    for t in np.nonzero(index["lengths"] > 64)[0]:
+        o, L = int(index["offsets"][t]), int(index["lengths"][t])
+        lst = doc[o:o + L]
+        b = np.searchsorted(lst, edges, side="left")
+        for lo, hi in zip(b[:-1], b[1:]):
+            if hi - lo > 64:
+                src = o + lo + arrange_order(lst[lo:hi])
+                out[o + lo: o + hi] = words[src]
+    return out
+
+
+def arrange_order(docs: np.ndarray) -> np.ndarray:
+    """Bank-aware order of one (term, tile) sub-range of n > 64 postings (docs
+    ascending): element i of the result is the sub-range index of the posting
+    placed at position i.  G = ceil(n / 64) groups of 64 positions, the last one
+    n_last = n - 64 (G - 1) long.  The postings sorted by (doc mod 64, doc) are
+    dealt out in turn: the k-th to group k mod G, position k // G while
+    k < n_last * G, after that to group k' mod (G - 1), position n_last +
+    k' // (G - 1) (k' = k - n_last * G).  Checked in tests against the invariants
+    that fix it: a permutation of the sub-range, every residue in ceil(count / G)
+    groups' worth at most per group, and the deal order itself on small cases."""
+    n = len(docs)
+    G = (n + 63) // 64
+    nl = n - 64 * (G - 1)
+    by_res = np.argsort(docs & 63, kind="stable")  # (residue, doc) order
+    k = np.arange(n)
+    first = k < nl * G
+    k2 = k - nl * G
+    grp = np.where(first, k % G, k2 % max(G - 1, 1))
+    pos = np.where(first, k // G, nl + k2 // max(G - 1, 1))
+    order = np.empty(n, dtype=np.int64)
+    order[grp * 64 + pos] = by_res
+    return order
 
 
 def chunk_bounds(doc_ids, offsets, lengths, vocab: int, n_docs: int, doc_chunk: int) -> np.ndarray:

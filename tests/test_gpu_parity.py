@@ -72,12 +72,17 @@ def test_forward_index_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
     assert w.cpu().numpy()[:nnz].tobytes() == want[2].tobytes()
 
 
-@pytest.mark.parametrize("seed,dtype,tile_log2", [(0, np.float32, 12), (1, np.float16, 13), (2, np.uint8, 8),
-                                                 (3, np.float16, 10), (4, np.float32, 14)])
-def test_packed_copy_matches_oracle(device, seed, dtype, tile_log2):
+@pytest.mark.parametrize("seed,dtype,tile_log2,vocab", [(0, np.float32, 12, 300), (1, np.float16, 13, 300),
+                                                       (2, np.uint8, 8, 300), (3, np.float16, 10, 300),
+                                                       (4, np.float32, 14, 300), (5, np.float16, 13, 9),
+                                                       (6, np.uint8, 12, 20), (7, np.float32, 6, 3)])
+def test_packed_copy_matches_oracle(device, seed, dtype, tile_log2, vocab):
+    """Bit for bit, including the bank-aware order inside (term, tile) sub-ranges
+    of more than 64 postings (vocab 9 / 20 / 3: sub-ranges of up to a whole tile,
+    with repeated doc ids)."""
     from gpusparse.index import build_packed
-    print(f"packed copy seed={seed} {dtype.__name__} tile_log2={tile_log2}", flush=True)
-    csr = random_csr(np.random.default_rng(seed), 20000, 300, dtype=dtype, dup_rate=0.05)
+    print(f"packed copy seed={seed} {dtype.__name__} tile_log2={tile_log2} vocab={vocab}", flush=True)
+    csr = random_csr(np.random.default_rng(seed), 20000, vocab, dtype=dtype, dup_rate=0.05)
     if dtype != np.uint8:  # signed weights and ties at half units of the scale
         csr.data[::5] *= -1
         csr.data[3::13] = ((np.arange(len(csr.data[3::13])) % 7) + 0.5).astype(dtype) / 2

@@ -141,7 +141,7 @@ def test_pack_postings_decodes_and_matches_scalar_loop(tile_log2, dtype):
         csr.data[::7] *= -1
         csr.data[5::11] = (np.arange(len(csr.data[5::11])) % 9 + 0.5).astype(dtype) / 4
     ix = O.build_index(csr.indptr, csr.indices, csr.data, 40000, 50)
-    pk = O.pack_postings(ix, tile_log2)
+    pk = O.pack_postings(ix, tile_log2, arrange=False)
     doc, w = ix["doc_ids"], ix["scores"]
     mask = (1 << tile_log2) - 1
     u = pk.view(np.uint32)
@@ -169,6 +169,72 @@ def test_pack_postings_decodes_and_matches_scalar_loop(tile_log2, dtype):
         else:
             b = round(Fraction(float(w[i])) * Fraction(2) ** shift) & 0xFFFF
         assert int(pk[i]) & 0xFFFFFFFF == o + (b << 16)
+
+
+def deal_by_enumeration(docs):
+    """arrange_order restated as a literal deal: the cells (group, position) are
+    listed position by position, groups in order, skipping positions the last
+    (partial) group does not have; the postings sorted by (doc mod 64, doc) fill
+    them in that order."""
+    n = len(docs)
+    G = (n + 63) // 64
+    cap = [64] * (G - 1) + [n - 64 * (G - 1)]
+    cells = [(g, p) for p in range(64) for g in range(G) if p < cap[g]]
+    srt = sorted(range(n), key=lambda i: (int(docs[i]) % 64, int(docs[i]), i))
+    order = [None] * n
+    for (g, p), i in zip(cells, srt):
+        order[g * 64 + p] = i
+    return np.array(order)
+
+
+@pytest.mark.parametrize("n,seed", [(65, 0), (128, 1), (130, 2), (191, 3), (1000, 4), (4096, 5), (8191, 6)])
+def test_arrange_order_is_the_deal(n, seed):
+    rng = np.random.default_rng(seed)
+    docs = np.sort(rng.choice(8192 if n < 8000 else 16384, size=n, replace=False)).astype(np.int64)
+    if seed % 2:  # repeated doc ids (a term twice in one doc) keep their order
+        docs = np.sort(np.concatenate([docs[: n - n // 8], docs[: n // 8]]))
+    order = O.arrange_order(docs)
+    assert np.array_equal(order, deal_by_enumeration(docs))
+    assert np.array_equal(np.sort(order), np.arange(n))
+    G = (n + 63) // 64
+    res = docs[order] & 63
+    counts = np.bincount(docs & 63, minlength=64)
+    for g in range(G):
+        per = np.bincount(res[g * 64:(g + 1) * 64], minlength=64)
+        assert np.all(per <= -(-counts // max(G - 1, 1)))
+
+
+def test_arrange_order_known_answers():
+    # consecutive docs: every group already holds 64 distinct residues -> identity
+    for n in (65, 130, 1000):
+        d = np.arange(n, dtype=np.int64) + 4096
+        assert np.array_equal(O.arrange_order(d), np.arange(n))
+    # docs 0, 2, 4, ...: 32 even residues, each 4 times among 128 postings (G = 2):
+    # residue r's docs r, r + 64, r + 128, r + 192 go to groups 0, 1, 0, 1
+    d = np.arange(0, 256, 2, dtype=np.int64)
+    got = d[O.arrange_order(d)]
+    assert list(got[:4]) == [0, 128, 2, 130] and list(got[64:68]) == [64, 192, 66, 194]
+
+
+def test_pack_arrangement_permutes_sub_ranges_only():
+    rng = np.random.default_rng(11)
+    csr = random_csr(rng, 30000, 12, dtype=np.float16, dup_rate=0.05)
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 30000, 12)
+    tl = 12
+    plain, arr = O.pack_postings(ix, tl, arrange=False), O.pack_postings(ix, tl)
+    moved = 0
+    edges = np.arange(((30000 + (1 << tl) - 1) >> tl) + 1, dtype=np.int64) << tl
+    covered = np.zeros(len(plain), dtype=bool)
+    for t in range(12):
+        o, L = int(ix["offsets"][t]), int(ix["lengths"][t])
+        b = np.searchsorted(ix["doc_ids"][o:o + L], edges)
+        for lo, hi in zip(b[:-1], b[1:]):
+            a, z = o + lo, o + hi
+            assert np.array_equal(np.sort(arr[a:z]), np.sort(plain[a:z]))
+            if hi - lo > 64:
+                covered[a:z] = True
+                moved += int(np.count_nonzero(arr[a:z] != plain[a:z]))
+    assert np.array_equal(arr[~covered], plain[~covered]) and moved > 0
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 17, 64, 1000])
