@@ -924,6 +924,14 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
                 }
             };
             auto apply = [&](Chunk &k, int j) {
+                // One wait for the whole chunk: its loads are all but the newest
+                // vm ones (the next chunk's, issued by the fetch before this call),
+                // so the adds below need no per-group waits.
+                {
+                    constexpr int vm = (PK ? UNROLL : 2 * UNROLL) + (SE ? 0 : 1);
+                    static_assert(vm < 64, "vmcnt is 6 bits");
+                    __builtin_amdgcn_s_waitcnt((vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+                }
                 if (k.m > 64) {  // a term held by more than 64 query slots (queries repeating terms)
                     if (k.n < CH)
 #pragma unroll
