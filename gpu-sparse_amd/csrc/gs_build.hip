@@ -621,20 +621,26 @@ __global__ void k_tile_bounds(const int32_t *__restrict__ doc, const int64_t *__
 // float weights the int16 rint(w * 2^shift) (w * 2^shift is exact in fp64 and
 // rounded once, half to even; clamped to +-32767).  Padding slots (doc < 0) hold 0.
 template <int WT>
-__device__ __forceinline__ uint32_t pack_word(int32_t d, const void *__restrict__ w, int64_t i, uint32_t mask,
-                                              int32_t shift) {
+__device__ __forceinline__ uint32_t pack_word_of(int32_t d, typename gs_weight<WT>::store_t wv, uint32_t mask,
+                                                 int32_t shift) {
     if (d < 0) return 0u;
     const uint32_t off = ((uint32_t)d & mask) << 2;
     uint32_t wq;
     if (WT == GS_W_U8) {
-        wq = reinterpret_cast<const uint8_t *>(w)[i];
+        wq = (uint32_t)wv;
     } else {
-        const double x = gs_weight<WT>::decode(reinterpret_cast<const typename gs_weight<WT>::store_t *>(w)[i]);
-        const double r = rint(ldexp(x, shift));
+        const double r = rint(ldexp((double)gs_weight<WT>::decode(wv), shift));
         const int32_t q = (int32_t)fmin(fmax(r, -32767.0), 32767.0);
         wq = (uint32_t)(uint16_t)(int16_t)q;
     }
     return off | (wq << 16);
+}
+
+template <int WT>
+__device__ __forceinline__ uint32_t pack_word(int32_t d, const void *__restrict__ w, int64_t i, uint32_t mask,
+                                              int32_t shift) {
+    if (d < 0) return 0u;
+    return pack_word_of<WT>(d, reinterpret_cast<const typename gs_weight<WT>::store_t *>(w)[i], mask, shift);
 }
 
 template <int WT>
@@ -661,6 +667,8 @@ __global__ void k_pack_postings(const int32_t *__restrict__ doc, const void *__r
 // than 64 postings one after the other: a pass counting residues, then a pass
 // that ranks each posting among its residue (64-lane ballot match plus the
 // wave's running counts) and writes its word to its place.
+constexpr int kArrangeUnroll = 4;  // 64-posting groups loaded together per lane
+
 template <int WT>
 __global__ void __launch_bounds__(256)
     k_pack_arrange(const int32_t *__restrict__ doc, const void *__restrict__ w, const int64_t *__restrict__ offsets,
@@ -688,8 +696,17 @@ __global__ void __launch_bounds__(256)
         const int G = (nn + 63) >> 6, nl = nn - 64 * (G - 1);
         s_cnt[wave][lane] = 0;
         __builtin_amdgcn_wave_barrier();
-        for (int c = 0; c < nn; c += 64)
-            if (c + lane < nn) atomicAdd(&s_cnt[wave][doc[ss + c + lane] & 63], 1u);
+        for (int c = 0; c < nn; c += 64 * kArrangeUnroll) {  // kArrangeUnroll loads in flight per lane
+            int32_t dv[kArrangeUnroll];
+#pragma unroll
+            for (int u = 0; u < kArrangeUnroll; ++u) {
+                const int i = c + u * 64 + lane;
+                dv[u] = i < nn ? doc[ss + i] : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < kArrangeUnroll; ++u)
+                if (dv[u] >= 0) atomicAdd(&s_cnt[wave][dv[u] & 63], 1u);
+        }
         __builtin_amdgcn_wave_barrier();
         const uint32_t cnt = s_cnt[wave][lane];
         uint32_t x = cnt;  // inclusive scan of the residue counts over the lanes
@@ -701,10 +718,26 @@ __global__ void __launch_bounds__(256)
         s_below[wave][lane] = x - cnt;
         s_run[wave][lane] = 0;
         __builtin_amdgcn_wave_barrier();
-        for (int c = 0; c < nn; c += 64) {
-            const int i = c + lane;
+        using store_t = typename gs_weight<WT>::store_t;
+        const store_t *wall = reinterpret_cast<const store_t *>(w);
+        for (int c = 0; c < nn; c += 64 * kArrangeUnroll) {
+            int32_t dv[kArrangeUnroll];
+            store_t wv[kArrangeUnroll];
+#pragma unroll
+            for (int u = 0; u < kArrangeUnroll; ++u) {
+                const int i = c + u * 64 + lane;
+                dv[u] = 0;
+                wv[u] = store_t(0);
+                if (i < nn) {
+                    dv[u] = doc[ss + i];
+                    wv[u] = wall[ss + i];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kArrangeUnroll; ++u) {
+            const int i = c + u * 64 + lane;
             const bool valid = i < nn;
-            const int32_t d = valid ? doc[ss + i] : 0;
+            const int32_t d = dv[u];
             const uint32_t r = (uint32_t)d & 63u;
             uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -734,7 +767,8 @@ __global__ void __launch_bounds__(256)
                     grp = k2 - q * (uint32_t)(G - 1);
                     pos = (uint32_t)nl + q;
                 }
-                out[ss + (int64_t)grp * 64 + pos] = pack_word<WT>(d, w, ss + i, mask, shift);
+                out[ss + (int64_t)grp * 64 + pos] = pack_word_of<WT>(d, wv[u], mask, shift);
+            }
             }
         }
     }
