@@ -59,8 +59,9 @@ def parse():
     ap.add_argument("--cpu-queries-1", type=int, default=96, help="queries timed on one core")
     ap.add_argument("--cpu-queries-all", type=int, default=512, help="queries timed on all cores")
     ap.add_argument("--cpu-cores", type=int, default=16,
-                    help="cap on the cores of the all-core row (16: the host-CPU share of one GPU on the "
-                         "GPU boxes; the process's affinity usually lists the whole host)")
+                    help="cap on the cores of the all-core row, which takes every core of the process's "
+                         "affinity up to this cap (the GPU boxes give a process 16 CPUs, one GPU's share of "
+                         "the host; the JSON records the affinity beside the cores used)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-queries", type=int, default=4)
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
