@@ -169,19 +169,44 @@ __device__ __forceinline__ int64_t rs_tile(int64_t nblocks) {
     return x * q + (x < r ? x : r) + (p >> 3);
 }
 
+// Digit counts of one tile, per wave in LDS (waves do not contend on hot digits)
+// and summed at the end.  A whole, 16-byte aligned tile is read as four uint4
+// per thread, all in flight together (the order of the keys does not matter).
 __global__ void __launch_bounds__(kRsThreads) k_rs_hist(const uint32_t *__restrict__ key, int64_t n, int shift,
                                                         uint32_t *__restrict__ hist, int64_t nblocks) {
-    __shared__ uint32_t h[256];
-    h[threadIdx.x] = 0;
+    constexpr int kWaves = kRsThreads / 64;
+    __shared__ uint32_t h[kWaves][256];
+    const int tid = threadIdx.x, wave = tid >> 6;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) h[w][tid] = 0;
     __syncthreads();
     const int64_t tile = rs_tile(nblocks);
     const int64_t base = tile * kRsTile;
-    for (int r = 0; r < kRsRounds; ++r) {
-        int64_t i = base + r * kRsThreads + threadIdx.x;
-        if (i < n) atomicAdd(&h[(key[i] >> shift) & 255u], 1u);
+    uint32_t *hw = h[wave];
+    if (n - base >= kRsTile && ((uintptr_t)(key + base) & 15u) == 0) {
+        static_assert(kRsTile == kRsThreads * 16, "four uint4 per thread");
+        const uint4 *k4 = reinterpret_cast<const uint4 *>(key + base);
+        uint4 v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = k4[r * kRsThreads + tid];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            atomicAdd(&hw[(v[r].x >> shift) & 255u], 1u);
+            atomicAdd(&hw[(v[r].y >> shift) & 255u], 1u);
+            atomicAdd(&hw[(v[r].z >> shift) & 255u], 1u);
+            atomicAdd(&hw[(v[r].w >> shift) & 255u], 1u);
+        }
+    } else {
+        for (int r = 0; r < kRsRounds; ++r) {
+            const int64_t i = base + r * kRsThreads + tid;
+            if (i < n) atomicAdd(&hw[(key[i] >> shift) & 255u], 1u);
+        }
     }
     __syncthreads();
-    hist[(int64_t)threadIdx.x * nblocks + tile] = h[threadIdx.x];
+    uint32_t c = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) c += h[w][tid];
+    hist[(int64_t)tid * nblocks + tile] = c;
 }
 
 // Device-wide exclusive scan of uint32 (three launches).
