@@ -128,6 +128,46 @@ def test_rescoring_without_forward_copy(c1):
         a["fwd"] = saved
 
 
+def test_search_with_packed_copy_in_slot_order(c1):
+    """A packed copy left in slot order (gs_pack_postings without tile bounds)
+    scores the same as the bank-aware one: the order inside a (term, tile)
+    sub-range does not change the integer sums."""
+    from gpusparse.index import build_packed, default_tile_log2, ensure_search_state
+    ix, ref, ti, tw = c1
+    tl = default_tile_log2(ix)
+    a = ensure_search_state(ix, tl)
+    saved = a[("packed", tl)]
+    a[("packed", tl)] = build_packed(ix, tl, arrange=False)
+    try:
+        assert not torch.equal(a[("packed", tl)].words, saved.words)
+        assert torch.equal(torch.sort(a[("packed", tl)].words).values, torch.sort(saved.words).values)
+        assert_search_equal(ix, ref, ti[:64], tw[:64], 100, path="fused")
+    finally:
+        a[("packed", tl)] = saved
+
+
+def test_search_counts_cover_the_answers(c1):
+    """gs_search_counts after a search: per scoring slot, the candidates emitted
+    and the candidates rescored in fp64.  Slots hold the queries in group order,
+    so the checks hold for every slot: each query's positive answers were all
+    emitted (at least min(k, positives) candidates) and rescored, and the rescored
+    set lies inside the candidates."""
+    ix, ref, ti, tw = c1
+    k, B = 100, 64
+    timing = {}
+    s, i = gs.search(ix, (torch.from_numpy(ti[:B]), torch.from_numpy(tw[:B])), k, timing=timing, path="fused")
+    assert timing["dense_rows"] == 0  # a row finished by the dense path reports 0 rescored
+    cand, resc = gs.search_counts(ix, B, ti.shape[1], k)
+    pos = (s.cpu().numpy() > 0).sum(axis=1)
+    assert cand.shape == (B,) and resc.shape == (B,)
+    assert np.all(np.sort(cand) >= np.sort(pos))
+    assert np.all(np.sort(resc) >= np.sort(pos))
+    assert np.all(resc <= cand)
+    with pytest.raises(ValueError):
+        gs.search_counts(gs.build_from_csr(random_csr(np.random.default_rng(1), 50, 20), ix.doc_ids.device),
+                         B, ti.shape[1], k)
+
+
 def test_build_generated_c1(device):
     docs, _ = synth.generate("C1")
     ix = gs.build_from_csr(docs, device)
