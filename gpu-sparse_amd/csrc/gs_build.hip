@@ -323,10 +323,10 @@ __global__ void __launch_bounds__(kRsThreads, 4)
         const uint32_t rank = __popcll(peers & gs_lanemask_lt());
         uint32_t seen = 0;
         if (valid) seen = wcnt[wave][dig];
-        __builtin_amdgcn_wave_barrier();
+        gs_wave_sync();
         lp[r] = seen + rank;
         if (valid && rank == 0) wcnt[wave][dig] = seen + (uint32_t)__popcll(peers);
-        __builtin_amdgcn_wave_barrier();
+        gs_wave_sync();
     }
     __syncthreads();
     // 3. the block's digit counts, their exclusive scan, and each wave's offset in a run
@@ -720,7 +720,7 @@ __global__ void __launch_bounds__(256)
         const int nn = __builtin_amdgcn_readlane(n, src);
         const int G = (nn + 63) >> 6, nl = nn - 64 * (G - 1);
         s_cnt[wave][lane] = 0;
-        __builtin_amdgcn_wave_barrier();
+        gs_wave_sync();
         for (int c = 0; c < nn; c += 64 * kArrangeUnroll) {  // kArrangeUnroll loads in flight per lane
             int32_t dv[kArrangeUnroll];
 #pragma unroll
@@ -732,7 +732,7 @@ __global__ void __launch_bounds__(256)
             for (int u = 0; u < kArrangeUnroll; ++u)
                 if (dv[u] >= 0) atomicAdd(&s_cnt[wave][dv[u] & 63], 1u);
         }
-        __builtin_amdgcn_wave_barrier();
+        gs_wave_sync();
         const uint32_t cnt = s_cnt[wave][lane];
         uint32_t x = cnt;  // inclusive scan of the residue counts over the lanes
 #pragma unroll
@@ -742,7 +742,7 @@ __global__ void __launch_bounds__(256)
         }
         s_below[wave][lane] = x - cnt;
         s_run[wave][lane] = 0;
-        __builtin_amdgcn_wave_barrier();
+        gs_wave_sync();
         using store_t = typename gs_weight<WT>::store_t;
         const store_t *wall = reinterpret_cast<const store_t *>(w);
         for (int c = 0; c < nn; c += 64 * kArrangeUnroll) {
@@ -777,9 +777,9 @@ __global__ void __launch_bounds__(256)
                 seen = s_run[wave][r];
                 below = s_below[wave][r];
             }
-            __builtin_amdgcn_wave_barrier();
+            gs_wave_sync();
             if (valid && rank == 0) s_run[wave][r] = seen + (uint32_t)__popcll(peers);
-            __builtin_amdgcn_wave_barrier();
+            gs_wave_sync();
             if (valid) {
                 const uint32_t k = below + seen + rank;  // place in (residue, doc) order
                 uint32_t grp, pos;
