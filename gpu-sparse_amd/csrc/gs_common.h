@@ -160,11 +160,19 @@ __device__ __forceinline__ uint2 gs_bload64(__amdgpu_buffer_rsrc_t r, int off) {
     return make_uint2(v[0], v[1]);
 }
 
-// Histogram bin of a positive score: bits of its fp32 value >> 20 (exponent and
-// three mantissa bits, ~9% wide bins), 2048 bins cover every positive float.
+// Histogram bin of a score (a positive integer sum, as fp32): 64 bins per binade
+// of [1, 2^32) -- the exponent above 2^0 and six mantissa bits of its fp32 value,
+// bins at most 1/64 of their value wide -- which fills the 2048 bins exactly;
+// values below 1 fall in bin 0, 2^32 (the fp32 image of the largest uint32) in
+// the last.  Monotone in v, so a bin's lower edge bounds every value in it and
+// above from below.
 constexpr int GS_HIST_BINS = 2048;
-__device__ __forceinline__ uint32_t gs_bin_of(float v) { return __float_as_uint(v) >> 20; }
-__device__ __forceinline__ float gs_bin_edge(uint32_t b) { return __uint_as_float(b << 20); }
+__device__ __forceinline__ uint32_t gs_bin_of(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t b = u < 0x3F800000u ? 0u : (u - 0x3F800000u) >> 17;
+    return b < (uint32_t)(GS_HIST_BINS - 1) ? b : (uint32_t)(GS_HIST_BINS - 1);
+}
+__device__ __forceinline__ float gs_bin_edge(uint32_t b) { return __uint_as_float(0x3F800000u + (b << 17)); }
 
 // Orders LDS accesses among the lanes of one wave.  The LDS executes a wave's
 // instructions in order, but without a fence the compiler may move or forward
