@@ -1176,12 +1176,41 @@ size_t fwd_layout(int64_t nnz, int32_t vocab, gs_arena &a, FwdLayout &l) {
     l.parts = a.take<uint32_t>(p.nparts);
     return a.used;
 }
+// One wave per CSR row: sets *unsorted when a column index is smaller than the
+// one before it in the same row (equal neighbours, a repeated term, are sorted).
+__global__ void __launch_bounds__(256) k_rows_sorted(const int64_t *__restrict__ indptr,
+                                                     const int32_t *__restrict__ indices, int64_t n_rows,
+                                                     int32_t *__restrict__ unsorted) {
+    const int lane = gs_lane();
+    const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
+    bool bad = false;
+    for (int64_t r = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6; r < n_rows; r += waves) {
+        const int64_t b = indptr[r], e = indptr[r + 1];
+        for (int64_t i = b + 1 + lane; i < e; i += 64) bad |= indices[i] < indices[i - 1];
+    }
+    if (__ballot(bad) && lane == 0) atomicOr(reinterpret_cast<unsigned int *>(unsorted), 1u);
+}
+
 }  // namespace
 
 extern "C" size_t gs_forward_fill_workspace(int64_t nnz, int32_t vocab) {
     gs_arena a{nullptr, 0, 0};
     FwdLayout l;
     return fwd_layout(nnz, vocab, a, l) + 256;
+}
+
+// ------------------------------------------------------------------ CSR row order
+
+extern "C" int gs_rows_sorted(const int64_t *indptr_d, const int32_t *indices_d, int64_t n_rows,
+                              int32_t *unsorted_d, void *stream) {
+    GS_REQUIRE(n_rows >= 0, "n_rows %lld is negative", (long long)n_rows);
+    GS_REQUIRE(unsorted_d && (n_rows == 0 || (indptr_d && indices_d)), "null pointer");
+    hipStream_t s = gs_stream(stream);
+    k_fill<int32_t><<<1, 64, 0, s>>>(unsorted_d, 1, 0);
+    if (n_rows > 0)
+        k_rows_sorted<<<gs_blocks(n_rows * 64, 256, 1 << 16), 256, 0, s>>>(indptr_d, indices_d, n_rows, unsorted_d);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
 }
 
 extern "C" int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype,

@@ -23,7 +23,7 @@ GS_ROW_DONE, GS_ROW_DENSE = 0, 1
 GS_SEARCH_PHASES = 7
 NOALLOC_SCRATCH_BYTES = 256 << 20   # GS_NOALLOC_SCRATCH_BYTES
 PHASE_NAMES = ("query_prep", "threshold_seed", "scoring", "candidate_select", "fp64_rescore", "final_sort")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 WTYPE_OF_DTYPE = {torch.float32: GS_W_F32, torch.float16: GS_W_F16, torch.uint8: GS_W_U8}
 
@@ -120,6 +120,7 @@ SIGNATURES = {
     "gs_forward_fill_workspace": (_SZ, [_I64, _I32]),
     "gs_forward_fill": (C.c_int, [_P, _P, _I32, _P, _P, _I32, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
     "gs_pack_postings": (C.c_int, [_P, _P, _I32, _I64, _P, _P, _I32, _I64, _I32, _I32, _P, _P]),
+    "gs_rows_sorted": (C.c_int, [_P, _P, _I64, _P, _P]),
     "gs_pack_shift": (C.c_int, [C.c_float, C.POINTER(C.c_int32)]),
     "gs_heavy_terms": (C.c_int, [_P, _I32, _P, _P]),
     "gs_search_workspace": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts),

@@ -203,6 +203,15 @@ def build_from_csr(csr, device=None, *, vocab_size: int | None = None, weight_dt
     idx.aux()["max_abs"] = max_abs
     idx.aux()["csr_nnz"] = nnz
     check_lists(idx)
+    if wdt != torch.uint8 and nnz > 0 and n_docs > 0:
+        # Float indexes are rescored from a doc-major copy.  When every CSR row is
+        # sorted by term, the uploaded CSR is that copy (the same rows, a repeated
+        # term's entries in CSR order, weights already in the storage type).
+        unsorted = torch.empty(1, dtype=torch.int32, device=dev)
+        _lib.check(L.gs_rows_sorted(_lib.ptr(indptr_d), _lib.ptr(indices_d), n_docs, _lib.ptr(unsorted), s),
+                   "gs_rows_sorted")
+        if int(unsorted.item()) == 0:
+            idx.aux()["fwd"] = (indptr_d, indices_d, data_d)
     return idx
 
 

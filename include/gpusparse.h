@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 7
+#define GS_ABI_VERSION 8
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -152,6 +152,14 @@ int gs_chunk_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d, const in
  * The reference's per-(term, chunk) sub-ranges at LDS-tile granularity. */
 int gs_tile_bounds(const int32_t *doc_ids_d, const int64_t *offsets_d, const int32_t *lengths_d,
                    int32_t vocab, int64_t n_docs, int32_t tile_log2, int32_t *bounds_d, void *stream);
+
+/* Whether every row of a doc-major CSR has non-decreasing column indices (no
+ * counterpart in the reference): *unsorted_d = 0 if so, 1 if not.  A CSR whose
+ * rows are sorted already is the doc-major copy below (the same rows, term ids
+ * ascending, a repeated term's entries in CSR order), so the index build keeps
+ * it instead of transposing the index back. */
+int gs_rows_sorted(const int64_t *indptr_d, const int32_t *indices_d, int64_t n_rows, int32_t *unsorted_d,
+                   void *stream);
 
 /* Doc-major copy of a term-major index, for exact candidate rescoring (the
  * forward-index layout of src/triton_kernel_v4.py:92-158, built on the GPU from

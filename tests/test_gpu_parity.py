@@ -72,6 +72,36 @@ def test_forward_index_matches_oracle(device, seed, n_docs, vocab, dtype, dup):
     assert w.cpu().numpy()[:nnz].tobytes() == want[2].tobytes()
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_forward_copy_taken_from_sorted_csr(device, dtype):
+    """A CSR whose rows are sorted by term (a repeated term's entries in CSR order)
+    is kept as the doc-major copy at build time; it equals the copy gs_forward_fill
+    builds from the index and the oracle's.  Unsorted rows leave the copy to the
+    first search."""
+    from gpusparse.index import build_forward
+    rng = np.random.default_rng(21)
+    csr = random_csr(rng, 3000, 400, dtype=dtype, dup_rate=0.1)
+    idx, dat = csr.indices.copy(), csr.data.copy()
+    for r in range(csr.shape[0]):
+        a, b = csr.indptr[r], csr.indptr[r + 1]
+        o = np.argsort(idx[a:b], kind="stable")
+        idx[a:b], dat[a:b] = idx[a:b][o], dat[a:b][o]
+    srt = CSR(csr.indptr, idx, dat, csr.shape)
+    ix = gs.build_from_csr(srt, device)
+    fwd = ix.aux().get("fwd")
+    assert fwd is not None
+    built = build_forward(ix)
+    want = O.forward_index(oracle_index(srt))
+    nnz = int(want[0][-1])
+    assert np.array_equal(fwd[0].cpu().numpy(), want[0]) and np.array_equal(built[0].cpu().numpy(), want[0])
+    for got, b, w in ((fwd[1], built[1], want[1]), (fwd[2], built[2], want[2])):
+        assert got.cpu().numpy()[:nnz].tobytes() == w.tobytes() == b.cpu().numpy()[:nnz].tobytes()
+    ti, tw = random_queries(rng, 16, 400, max_len=12)
+    assert_search_equal(ix, oracle_index(srt), ti, tw, 50, path="fused")
+    unsorted = gs.build_from_csr(csr, device)
+    assert "fwd" not in unsorted.aux()
+
+
 @pytest.mark.parametrize("seed,dtype,tile_log2,vocab", [(0, np.float32, 12, 300), (1, np.float16, 13, 300),
                                                        (2, np.uint8, 8, 300), (3, np.float16, 10, 300),
                                                        (4, np.float32, 14, 300), (5, np.float16, 13, 9),
