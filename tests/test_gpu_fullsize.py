@@ -1,5 +1,6 @@
-"""GPU parity at the configurations' full sizes (C2: 1M docs, B=1024; C3 and C5:
-8.8M docs, ~1.06e9 postings, B=512), after src/remeasure_2026_09.py:155-235.
+"""GPU parity at the configurations' full sizes (C2: 1M docs, B=1024; C4: 1M docs
+with Zipf(1.3) terms, B=512; C3 and C5: 8.8M docs, ~1.06e9 postings, B=512),
+after src/remeasure_2026_09.py:155-235.
 
 At these sizes the oracle does not rebuild the index on the host.  Instead:
 - the GPU-built index is checked against its CSR by size-independent
@@ -94,6 +95,17 @@ def test_c2_full_search_whole_batch(device):
     """1M docs, B=1024 (the groups of a whole 1024-query ordering block), fp32,
     k=1000: every query of the batch checked."""
     check_search("C2", device, 1000, np.arange(1024))
+
+
+def test_c4_full_index(device):
+    check_index("C4", device)
+
+
+def test_c4_full_search(device):
+    """1M docs whose top-50 terms each hold > 200K postings (dense in every tile):
+    the head-heavy case of the scorer, 96 rows of the 512-query batch."""
+    rows = sample_rows(512, 96, seed=4)
+    check_search("C4", device, 1000, rows)
 
 
 def test_c3_full_index(device):
