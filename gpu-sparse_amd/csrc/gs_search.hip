@@ -598,6 +598,7 @@ constexpr int kUnionBatch = 220;    // union terms described in LDS at a time
 constexpr int kEmitChunks = (int)(kUnionTileLds / 4 / 256);  // 256-doc emission chunks of one workgroup
 constexpr int kLocalBins = 256;  // bins of the per-slot score histogram of the seed launch
 constexpr int kLocalSlots = 4;   // slots per workgroup that get a local threshold
+constexpr int kEmitReads = 4;    // emission chunks a wave reads at once in the counting pass
 
 // LDS bytes of k_score_union besides the G score slices
 constexpr size_t kUnionMetaLds =
@@ -1061,19 +1062,32 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
         }
         return tot;
     };
-    for (int ch = wave; ch < nce; ch += NW) {
-        const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
-        const int mx = max(max((int32_t)v4.x, (int32_t)v4.y), max((int32_t)v4.z, (int32_t)v4.w));
-        uint32_t cnt = 0;
-        if (__ballot(mx >= (int)s_thr[ch >> cps_log2])) {
-            uint32_t vv[4];
-            bool keep[4];
-            uint64_t mk[4];
-            cnt = scan4(ch, vv, keep, mk);
-        }
-        if (lane == 0) {
-            s_off[ch] = cnt;
-            s_ccnt[ch] = cnt;
+    // Pass 1 reads a wave's chunks kEmitReads at a time, so that many LDS reads
+    // are in flight instead of one read-wait-count round trip per chunk; lane g
+    // holds slot g's threshold (nq <= 64).
+    {
+        const int thr_l = lane < nq ? (int)s_thr[lane] : 0;
+        for (int c0 = wave; c0 < nce; c0 += NW * kEmitReads) {
+            uint4 v4[kEmitReads];
+#pragma unroll
+            for (int u = 0; u < kEmitReads; ++u) {  // past the end: the last chunk again, not counted
+                const int ch = min(c0 + u * NW, nce - 1);
+                v4[u] = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
+            }
+#pragma unroll
+            for (int u = 0; u < kEmitReads; ++u) {
+                const int ch = c0 + u * NW;
+                if (ch >= nce) break;
+                const int thr = __builtin_amdgcn_readlane(thr_l, ch >> cps_log2);
+                const uint32_t cnt = (uint32_t)__popcll(__ballot((int32_t)v4[u].x >= thr)) +
+                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].y >= thr)) +
+                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].z >= thr)) +
+                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].w >= thr));
+                if (lane == 0) {
+                    s_off[ch] = cnt;
+                    s_ccnt[ch] = cnt;
+                }
+            }
         }
     }
     __syncthreads();
