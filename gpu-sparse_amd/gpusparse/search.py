@@ -99,7 +99,8 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     fused scoring kernel ("score_kernel") and the whole gs_search call ("search"),
     the GS_SEARCH_PHASES events of each call ("phases": start, query prep,
     threshold seed, scoring, candidate selection, fp64 rescoring, final sort) and
-    the number of rows finished by the dense path ("dense_rows").
+    the number of rows finished by the dense path ("dense_rows").  Events come
+    from timing["event_pool"] while it lasts (see `timing_dict`).
     batch_order: score queries in groups of consecutive queries instead of groups of
     queries sharing frequent terms (same results; for comparisons)."""
     dev = _lib.require_gpu(_device_of(index))
@@ -143,13 +144,10 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     if timing is not None:
         # events recorded by gs_search itself around the fused scoring kernel and at
         # its phase boundaries, and around the whole gs_search call, on the launch stream
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-        ph = [torch.cuda.Event(enable_timing=True) for _ in range(_lib.GS_SEARCH_PHASES)]
-        for e in evs + ph:
-            e.record()
+        pool = timing.get("event_pool")
+        evs, ph, ph_ptr = pool.pop() if pool else _call_events()
         opts.ev_score_begin, opts.ev_score_end = evs[0].cuda_event, evs[1].cuda_event
-        ph_arr = (_lib.C.c_void_p * len(ph))(*[e.cuda_event for e in ph])
-        opts.ev_phases = _lib.C.cast(ph_arr, _lib.C.POINTER(_lib.C.c_void_p))
+        opts.ev_phases = ph_ptr
         evs[2].record()
     _lib.check(L.gs_search(_lib.C.byref(gidx), _lib.ptr(qt), _lib.ptr(qw), B, T, kk, _lib.C.byref(opts),
                            _lib.ptr(out_s), _lib.ptr(out_i), _lib.ptr(status), _lib.ptr(ws), ws.numel(), s),
@@ -158,7 +156,8 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
         evs[3].record()
         timing.setdefault("score_kernel", []).append((evs[0], evs[1]))
         timing.setdefault("search", []).append((evs[2], evs[3]))
-        timing.setdefault("phases", []).append(ph)
+        if ph:
+            timing.setdefault("phases", []).append(ph)
     st = status.cpu().numpy()
     bad = np.nonzero(st != _lib.GS_ROW_DONE)[0]
     if timing is not None:
@@ -167,6 +166,30 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
         rows = torch.from_numpy(bad.astype(np.int32)).to(dev)
         _dense_rows(index, gidx, qt, qw, kk, rows, out_s, out_i, max(dense_budget, 1))
     return out_s, out_i
+
+
+def _call_events(phases: bool = True):
+    """The events of one timed `search` call: 4 bracketing ones, one per phase
+    (unless `phases` is false) and the C array of the phase events.  Each is
+    recorded once here, which creates its HIP event."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ph = [torch.cuda.Event(enable_timing=True) for _ in range(_lib.GS_SEARCH_PHASES)] if phases else []
+    for e in evs + ph:
+        e.record()
+    ph_ptr = None
+    if ph:
+        arr = (_lib.C.c_void_p * len(ph))(*[e.cuda_event for e in ph])
+        ph_ptr = _lib.C.cast(arr, _lib.C.POINTER(_lib.C.c_void_p))
+        ph_ptr._keep = arr
+    return evs, ph, ph_ptr
+
+
+def timing_dict(n_calls: int, phases: bool = True) -> dict:
+    """A `timing` dict for `search` holding the events of `n_calls` calls, created
+    up front: the timed calls then only record them (creating them inside a call
+    costs ~0.1 ms of host time, which the GPU waits out after the call's status
+    read).  phases=False leaves out the per-phase events (and "phases")."""
+    return {"event_pool": [_call_events(phases) for _ in range(int(n_calls))]}
 
 
 def search_plan(index, B: int, T: int, k: int, *, tile_log2: int | None = None, sample_tiles: int = 0,

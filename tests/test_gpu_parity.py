@@ -198,6 +198,38 @@ def test_search_counts_cover_the_answers(c1):
                          B, ti.shape[1], k)
 
 
+def test_timing_dict_events(c1):
+    """Searches timed with a pre-built `timing_dict` use its events (one call's
+    set each), time every phase and return what an untimed search returns."""
+    ix, ref, ti, tw = c1
+    q = (torch.from_numpy(ti[:32]), torch.from_numpy(tw[:32]))
+    s0, i0 = gs.search(ix, q, 50, path="fused")
+    timing = gs.timing_dict(2)
+    pool = [ev for pair in timing["event_pool"] for ev in pair[0] + pair[1]]
+    for _ in range(2):
+        s, i = gs.search(ix, q, 50, path="fused", timing=timing)
+        assert torch.equal(s, s0) and torch.equal(i, i0)
+    torch.cuda.synchronize()
+    assert timing["event_pool"] == [] and len(timing["search"]) == 2 and len(timing["phases"]) == 2
+    used = [e for pair in timing["search"] + timing["score_kernel"] for e in pair] + \
+        [e for ph in timing["phases"] for e in ph]
+    assert {id(e) for e in used} == {id(e) for e in pool}
+    for e0, e1 in timing["search"]:
+        assert e0.elapsed_time(e1) > 0
+    for ph in timing["phases"]:
+        assert all(ph[j].elapsed_time(ph[j + 1]) >= 0 for j in range(len(ph) - 1))
+    # the pool exhausted, further calls create their own events
+    gs.search(ix, q, 50, path="fused", timing=timing)
+    assert len(timing["search"]) == 3
+    # without phase events: the bracketing ones only
+    t2 = gs.timing_dict(1, phases=False)
+    s, i = gs.search(ix, q, 50, path="fused", timing=t2)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s0) and torch.equal(i, i0)
+    assert "phases" not in t2 and len(t2["score_kernel"]) == 1
+    assert t2["score_kernel"][0][0].elapsed_time(t2["score_kernel"][0][1]) > 0
+
+
 def test_build_generated_c1(device):
     docs, _ = synth.generate("C1")
     ix = gs.build_from_csr(docs, device)
