@@ -1803,8 +1803,12 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     if ((rc = phase(4))) return rc;
     if (FP) {
         dim3 g(64u, (unsigned)B);
+        // doc-major rescoring: about 16K waves over the batch (16 to 64 workgroups
+        // per query), so that each wave's start-up is spread over more candidates
+        // (C2: 0.51 -> 0.48 ms at 16 per query); small batches keep 64 per query
+        const dim3 gf((unsigned)std::min(64, std::max(16, (16384 / kRescoreWaves) / std::max(B, 1))), (unsigned)B);
         if (ix->fwd_ptr_d)
-            k_rescore_fwd<WT><<<g, 64 * kRescoreWaves, 0, s>>>(
+            k_rescore_fwd<WT><<<gf, 64 * kRescoreWaves, 0, s>>>(
                 ix->fwd_ptr_d, ix->fwd_terms_d, ix->fwd_weights_d, ix->vocab, qt,
                 reinterpret_cast<const float *>(qw), T, p.resc_doc, p.resc_cnt, p.rcap, p.resc_key);
         else
