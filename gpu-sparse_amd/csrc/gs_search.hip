@@ -1064,7 +1064,7 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
     };
     // Pass 1 reads a wave's chunks kEmitReads at a time, so that many LDS reads
     // are in flight instead of one read-wait-count round trip per chunk; lane g
-    // holds slot g's threshold (nq <= 64).
+    // holds slot g's threshold (a group holds at most 32 queries).
     {
         const int thr_l = lane < nq ? (int)s_thr[lane] : 0;
         for (int c0 = wave; c0 < nce; c0 += NW * kEmitReads) {
