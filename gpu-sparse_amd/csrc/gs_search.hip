@@ -1242,6 +1242,19 @@ __global__ void __launch_bounds__(kSelThreads)
 // finds query term j's posting(s) of the doc (binary search inside the doc's
 // tile), then the products are summed in query-term order, which makes the sum
 // bit-identical to the fp64 scatter-add.
+// 1 + the index of a query's last valid term (0 when it has none): the
+// rescoring loops over query terms stop there, since a batch is padded to its
+// widest query (one wave, all lanes, reads the row)
+__device__ __forceinline__ int valid_terms_end(const int32_t *__restrict__ qrow, int T, int V) {
+    int end = 0;
+    for (int j0 = 0; j0 < T; j0 += 64) {
+        const int j = j0 + gs_lane();
+        const uint64_t b = __ballot(j < T && (uint32_t)qrow[j] < (uint32_t)V);
+        if (b) end = j0 + 64 - __clzll((long long)b);
+    }
+    return end;
+}
+
 template <int WT>
 __global__ void __launch_bounds__(256)
     k_rescore(const int32_t *__restrict__ doc_ids, const void *__restrict__ w, const int64_t *__restrict__ offsets,
@@ -1256,11 +1269,12 @@ __global__ void __launch_bounds__(256)
     const int wpb = blockDim.x >> 6;
     const int64_t row = (int64_t)n_tiles + 1;
     const store_t *wall = reinterpret_cast<const store_t *>(w);
+    const int t_end = valid_terms_end(qt + (int64_t)q * T, T, V);
     for (uint32_t i = blockIdx.x * wpb + (threadIdx.x >> 6); i < m; i += gridDim.x * wpb) {
         const int32_t d = (int32_t)resc_doc[(int64_t)q * resc_cap + i];
         const int tile = d >> tile_log2;
         double s = 0.0;
-        for (int j0 = 0; j0 < T; j0 += 64) {
+        for (int j0 = 0; j0 < t_end; j0 += 64) {
             const int j = j0 + lane;
             int cnt_p = 0;       // postings of doc d in term j's list (> 1 only for duplicates)
             int64_t pos = 0;     // slot of the first of them
@@ -1341,6 +1355,7 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
     store_t *roww = s_rw[w];
     const store_t *wall = reinterpret_cast<const store_t *>(fw);
     const uint32_t stride = gridDim.x * kRescoreWaves;
+    const int t_end = valid_terms_end(qt + (int64_t)q * T, T, V);
     // the query's first 128 terms and weights stay in registers (lane j: terms j
     // and j + 64) for all of the wave's candidates
     int32_t qt_r[2];
@@ -1393,7 +1408,7 @@ __global__ void __launch_bounds__(64 * kRescoreWaves)
             auto term_at = [&](int64_t e) { return staged ? row[e] : fterm[r0 + e]; };
             auto weight_at = [&](int64_t e) { return staged ? roww[e] : wall[r0 + e]; };
             double s = 0.0;
-            for (int j0 = 0; j0 < T; j0 += 64) {
+            for (int j0 = 0; j0 < t_end; j0 += 64) {
                 const int j = j0 + lane;
                 int cnt_p = 0;  // entries of term j in the row (> 1 only for duplicates)
                 int lo = 0;     // the first of them, within the row
