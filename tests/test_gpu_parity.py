@@ -373,6 +373,28 @@ def test_search_edge_cases(device, dtype):
     assert s.shape == (12, 700)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_rescoring_stops_at_last_valid_term(device, dtype):
+    """Padded query rows whose valid terms start past the first 64 columns or sit
+    only in the last column: the fp64 rescoring reads each row up to its last
+    valid term (in query order) and returns the oracle's scores bit for bit."""
+    rng = np.random.default_rng(33)
+    csr = random_csr(rng, 20000, 300, max_len=20, dtype=dtype)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    B, T = 24, 150
+    ti = np.full((B, T), -1, np.int32)
+    tw = np.zeros((B, T), np.float32)
+    for q in range(B):
+        cols = {0: [T - 1], 1: [70, 149], 2: [64, 65, 127, 128]}.get(q % 6, sorted(rng.choice(np.arange(64, T), 12,
+                                                                                           replace=False)))
+        ti[q, cols] = rng.choice(300, len(cols), replace=False)
+        tw[q, cols] = rng.uniform(0.1, 3.0, len(cols)).astype(np.float32)
+        if q % 6 == 4:
+            ti[q, rng.choice(cols, 2, replace=False)] = 300 + q  # invalid ids among the valid ones
+    assert_search_equal(ix, ref, ti, tw, 120, path="fused")
+
+
 def test_search_f16_config_reduced(device):
     cfg = synth.scaled(synth.CONFIGS["C3"], n_docs=300_000, n_queries=64)
     docs, queries = synth.generate(cfg)
