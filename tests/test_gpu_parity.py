@@ -692,6 +692,21 @@ def test_k_and_width_limits_raise_value_error(c1):
     assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
 
 
+@pytest.mark.parametrize("width,n_q", [(3000, 6), (8192, 2)])
+def test_search_very_wide_queries(c1, width, n_q):
+    """Queries of thousands of terms (up to the 8192-term limit, some repeated):
+    a group's union then spans many batches of union terms and the group size
+    shrinks to fit the LDS sort of its entries; answers equal the oracle's."""
+    ix, ref, _, _ = c1
+    rng = np.random.default_rng(width)
+    V = int(ref["vocab_size"])
+    ti = np.stack([rng.choice(V, width, replace=False) for _ in range(n_q)]).astype(np.int32)
+    ti[:, -5:] = ti[:, :5]  # repeated terms
+    tw = rng.uniform(0.01, 1.0, ti.shape).astype(np.float32)
+    print(f"wide queries T={width}", flush=True)
+    assert_search_equal(ix, ref, ti, tw, 100, path="fused")
+
+
 @pytest.mark.parametrize("dtype", [np.float16, np.uint8])
 def test_reference_builders_store_float32(device, dtype):
     """build_index / build_gpu_index_from_csr store float32 weights whatever the
