@@ -1512,6 +1512,40 @@ __global__ void __launch_bounds__(kSelThreads)
     }
 }
 
+// k above kMaxK: rounds of up to kMaxK entries, each the top of the entries
+// after the previous round's last one (SrcRowAfter), written one after the other.
+template <int WT>
+__global__ void __launch_bounds__(kSelThreads)
+    k_select_dense_large(const void *__restrict__ dense, int64_t ld, int64_t n_docs, int32_t k,
+                         const int32_t *__restrict__ rows, int32_t r0, void *__restrict__ out_scores,
+                         int64_t *__restrict__ out_ids) {
+    constexpr bool F64 = WT != GS_W_U8;
+    __shared__ SelStatic sst;
+    SelShared sh = sel_view(sst, kMaxK);
+    const int r = blockIdx.x;
+    const int q = rows ? rows[r0 + r] : r0 + r;
+    const size_t esz = F64 ? sizeof(double) : sizeof(uint32_t);
+    SrcRowAfter<F64> src{reinterpret_cast<const unsigned char *>(dense) + (size_t)r * (size_t)ld * esz, n_docs, 0, 0,
+                         false};
+    for (int done = 0; done < k;) {
+        const int kr = min(kMaxK, k - done);
+        const int got = block_topk<64>(src, kr, sh, true);  // == kr: k <= n_docs
+        for (int i = threadIdx.x; i < got; i += blockDim.x) {
+            const uint64_t key = sh.key[i] - 1;
+            const int64_t o = (int64_t)q * k + done + i;
+            if (F64) reinterpret_cast<float *>(out_scores)[o] = (float)gs_unkey_f64(key);
+            else reinterpret_cast<int32_t *>(out_scores)[o] = (int32_t)(uint32_t)key;
+            out_ids[o] = (int64_t)sh.doc[i];
+        }
+        if (got <= 0) break;
+        src.ck = sh.key[got - 1] - 1;
+        src.cd = sh.doc[got - 1];
+        src.cut = true;
+        done += got;
+        __syncthreads();  // the next round rewrites the sort buffer
+    }
+}
+
 // ---------------------------------------------------------------------- host plumbing
 
 int dense_waves(int tile_log2, size_t acc_bytes) {
@@ -1874,9 +1908,15 @@ int search_dense_impl(const gs_index *ix, const int32_t *qt, const void *qw, int
         }
         int rc = launch_dense<WT>(a, waves, s);
         if (rc) return rc;
-        GS_CHECK_HIP(sel_attr((const void *)k_select_dense<WT>, sel_lds_bytes(k)));
-        k_select_dense<WT><<<n, kSelThreads, sel_lds_bytes(k), s>>>(ws, ld, ix->n_docs, k, rows, r0, out_scores,
-                                                                     out_ids);
+        if (k <= kMaxK) {
+            GS_CHECK_HIP(sel_attr((const void *)k_select_dense<WT>, sel_lds_bytes(k)));
+            k_select_dense<WT><<<n, kSelThreads, sel_lds_bytes(k), s>>>(ws, ld, ix->n_docs, k, rows, r0,
+                                                                         out_scores, out_ids);
+        } else {
+            GS_CHECK_HIP(sel_attr((const void *)k_select_dense_large<WT>, sel_lds_bytes(kMaxK)));
+            k_select_dense_large<WT><<<n, kSelThreads, sel_lds_bytes(kMaxK), s>>>(ws, ld, ix->n_docs, k, rows, r0,
+                                                                                   out_scores, out_ids);
+        }
         GS_CHECK_LAUNCH();
     }
     return GS_OK;
@@ -2034,7 +2074,8 @@ extern "C" int gs_search_dense(const gs_index *index, const int32_t *q_terms_d, 
                                int64_t *out_ids_d, void *workspace_d, size_t workspace_bytes, void *stream) {
     if (int rc = check_index(index)) return rc;
     GS_REQUIRE(B > 0 && T > 0 && R >= 0 && R <= B, "bad sizes (B=%d, T=%d, R=%d)", B, T, R);
-    GS_REQUIRE(k >= 1 && k <= kMaxK && (int64_t)k <= index->n_docs, "k=%d outside [1, min(n_docs, %d)]", k, kMaxK);
+    GS_REQUIRE(k >= 1 && (int64_t)k <= index->n_docs, "k=%d outside [1, n_docs=%lld]", k,
+               (long long)index->n_docs);
     GS_REQUIRE(q_terms_d && q_weights_d && out_scores_d && out_ids_d && workspace_d, "null pointer");
     if (R == 0) return GS_OK;
     hipStream_t s = gs_stream(stream);

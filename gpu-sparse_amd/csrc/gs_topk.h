@@ -136,6 +136,27 @@ struct SrcRowF32 {  // dense fp32 row, optionally only entries >= tau
     __device__ uint32_t d(int64_t i) const { return (uint32_t)i; }
 };
 
+// Dense row (fp64 or uint32 values, doc = column) past a cutoff: only the
+// entries after (ck, cd) in (key desc, doc asc) order take part, as key + 1 (a
+// finite score's key is below 2^64 - 1); the others read 0, filtered out.  With
+// `cut` false every entry takes part.  Successive selections of up to kMaxK
+// entries, each after the previous one's last entry, give a top-k of any k.
+template <bool F64>
+struct SrcRowAfter {
+    const void *v;
+    int64_t n;
+    uint64_t ck;
+    uint32_t cd;
+    bool cut;
+    __device__ uint64_t k(int64_t i) const {
+        const uint64_t kk = F64 ? gs_key_f64(reinterpret_cast<const double *>(v)[i])
+                                : (uint64_t)reinterpret_cast<const uint32_t *>(v)[i];
+        const bool after = !cut || kk < ck || (kk == ck && (uint32_t)i > cd);
+        return after ? kk + 1 : 0;
+    }
+    __device__ uint32_t d(int64_t i) const { return (uint32_t)i; }
+};
+
 __device__ __forceinline__ bool sel_before(uint64_t ka, uint32_t da, uint64_t kb, uint32_t db) {
     return ka > kb || (ka == kb && da < db);
 }

@@ -19,7 +19,7 @@ import torch
 from . import _lib
 from .index import default_tile_log2, gs_index_struct, _device_of
 
-MAX_K = 8192
+MAX_K = 8192  # largest k of the fused path and of compacted_topk; search answers larger k densely
 DEFAULT_DENSE_BUDGET = 1 << 30   # bytes of [B, N] score rows below which the dense path is used
 
 
@@ -94,7 +94,8 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
 
     tile_log2: doc-tile size of the scorer (default: index.default_tile_log2).
-    path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense".
+    path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense";
+    k above MAX_K (8192) always takes the dense path (any k up to the doc count).
     timing: optional dict; receives event pairs on the launch stream bracketing the
     fused scoring kernel ("score_kernel") and the whole gs_search call ("search"),
     the GS_SEARCH_PHASES events of each call ("phases": start, query prep,
@@ -108,8 +109,6 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     kk = min(int(k), N)
     if kk < 1:
         raise ValueError(f"k must be >= 1, got {k}")
-    if kk > MAX_K:
-        raise ValueError(f"k={kk} exceeds the supported maximum {MAX_K}")
     qt, qw = query_tensors(index, query_batch)
     B, T = qt.shape
     out_dtype = torch.int32 if index.scores.dtype == torch.uint8 else torch.float32
@@ -129,7 +128,8 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     dense_bytes = B * gidx.n_tiles * (1 << tile_log2) * acc_bytes
     if path not in ("auto", "fused", "dense"):
         raise ValueError(f"unknown path {path!r}")
-    use_dense = path == "dense" or (path == "auto" and dense_bytes <= dense_budget)
+    # k above MAX_K: the dense path, whose selection takes any k (rounds of MAX_K)
+    use_dense = path == "dense" or kk > MAX_K or (path == "auto" and dense_bytes <= dense_budget)
     if use_dense:
         _dense_rows(index, gidx, qt, qw, kk, None, out_s, out_i, max(dense_budget, 1))
         return out_s, out_i

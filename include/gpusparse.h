@@ -267,7 +267,9 @@ int gs_search_counts(const gs_index *index, int32_t B, int32_t T, int32_t k, con
  * rows listed in rows_d (int32 [R], or NULL for rows 0..B-1) are scored densely
  * over all documents (fp64 or uint32 tiles written to a dense row buffer) and
  * selected exactly; results go to the same rows of out_*.  The workspace bounds
- * how many rows are processed per pass (at least one row must fit). */
+ * how many rows are processed per pass (at least one row must fit).
+ * 1 <= k <= n_docs: above 8192 the selection runs in rounds of 8192, each the
+ * top of the entries after the previous round's last one. */
 int gs_search_dense_workspace(const gs_index *index, int32_t rows_per_pass, size_t *bytes);
 int gs_search_dense(const gs_index *index, const int32_t *q_terms_d, const void *q_weights_d,
                     int32_t B, int32_t T, int32_t k, const int32_t *rows_d, int32_t R,

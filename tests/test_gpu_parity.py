@@ -674,22 +674,44 @@ def test_chunked_entry_points_ignore_bound_contents_and_block_pl(c1):
         gs.triton_chunked_score_fused(ix, qt, qw, top_k=50, doc_chunk=30000, chunk_bounds=good[:-1])
 
 
-def test_k_and_width_limits_raise_value_error(c1):
-    """Documented limits: k above 8192 (the LDS selection's capacity) and query
-    widths above 8192 terms raise ValueError instead of answering."""
+def test_k_above_8192_and_width_limit(c1):
+    """k above 8192 (the LDS selection's capacity) is answered by the dense path
+    in rounds of 8192 and equals the oracle bit for bit, up to k = num_docs, for
+    any path argument; query widths above 8192 terms on the fused path raise
+    ValueError, as does compacted_topk above its capacity."""
     ix, ref, ti, tw = c1
     assert gs.MAX_K == 8192
-    q = (torch.from_numpy(ti[:2]), torch.from_numpy(tw[:2]))
-    with pytest.raises(ValueError, match="8192"):
-        gs.search(ix, q, 8193)
-    with pytest.raises(ValueError, match="8192"):
-        gs.triton_fused_score(ix, q[0], q[1], top_k=9000)
+    q = (torch.from_numpy(ti[:3]), torch.from_numpy(tw[:3]))
+    for k, path in ((8192, "fused"), (8193, "fused"), (20000, "auto"), (24577, "dense")):
+        print(f"large k={k} path={path}", flush=True)
+        s, i = gs.search(ix, q, k, path=path)
+        vs, _, vi = O.c_search(ref, ti[:3], tw[:3], k, threads=8)
+        assert s.shape == (3, k)
+        assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+    s, i = gs.triton_fused_score(ix, q[0], q[1], top_k=9000)
+    vs, _, vi = O.c_search(ref, ti[:3], tw[:3], 9000, threads=8)
+    assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
     wide_t = torch.full((1, 8193), 5, dtype=torch.int32)
     with pytest.raises(ValueError, match="8192"):
         gs.search(ix, (wide_t, torch.ones((1, 8193))), 10, path="fused")
-    s, i = gs.search(ix, q, 8192)
-    vs, _, vi = O.c_search(ref, ti[:2], tw[:2], 8192, threads=8)
-    assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+    rows = torch.rand((2, 20000), device=ix.doc_ids.device)
+    with pytest.raises(ValueError, match="8192"):
+        gs.compacted_topk(rows, torch.zeros(2, device=rows.device), 9000, max_cand=9000)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.uint8])
+def test_k_up_to_num_docs(device, dtype):
+    """k = num_docs and k just above a multiple of 8192 on a small index: every
+    doc ranked, zero-score docs by ascending id, bit for bit against the oracle
+    (uint8: int32 sums)."""
+    rng = np.random.default_rng(9)
+    csr = random_csr(rng, 17000, 40, max_len=6, dtype=dtype, empty_rate=0.3)
+    ix = gs.build_from_csr(csr, device, weight_dtype=None)
+    ref = oracle_index(csr)
+    ti, tw = random_queries(rng, 4, 40, max_len=5, dtype=np.uint8 if dtype == np.uint8 else np.float32)
+    for k in (16385, 17000):
+        print(f"k={k} of 17000 {dtype.__name__}", flush=True)
+        assert_search_equal(ix, ref, ti, tw, k)
 
 
 @pytest.mark.parametrize("width,n_q", [(3000, 6), (8192, 2)])
