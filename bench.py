@@ -65,6 +65,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-queries", type=int, default=4)
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
+    ap.add_argument("--streams", type=int, default=1,
+                    help="batches in flight, one stream each (1: each batch finishes before the next is queued)")
     ap.add_argument("--summarize-traffic", default=None, metavar="DIR",
                     help="write profiles/traffic_k_score_union_<config>.json from rocprofv3 --pmc runs under DIR")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -280,23 +282,53 @@ def main():
     k = min(a.k or cfg.k, docs.shape[0])
     del docs
 
-    def step(timing=None):
+    def step_async(timing=None):
         if a.path == "atomic":
-            return gs.atomic_fused_score(index, qt, qw, k)
-        return gs.search(index, (qt, qw), k, tile_log2=a.tile_log2, path=a.path, unroll=a.unroll,
-                         waves=a.waves, tiles_per_wg=a.tiles_per_wg, sample_tiles=a.sample_tiles, timing=timing)
+            return gs.PendingSearch(gs.atomic_fused_score(index, qt, qw, k))
+        return gs.search_async(index, (qt, qw), k, tile_log2=a.tile_log2, path=a.path, unroll=a.unroll,
+                               waves=a.waves, tiles_per_wg=a.tiles_per_wg, sample_tiles=a.sample_tiles,
+                               timing=timing)
 
-    for _ in range(a.warmup):
-        step()
-    timing = gs.timing_dict(a.steps)  # events created before the timed region
+    # Batch i is queued on stream i mod S once batch i - S has finished (its
+    # status read and any flagged rows completed), so up to S batches are in
+    # flight; S = 1 runs them one after another.
+    streams = [torch.cuda.current_stream()] + [torch.cuda.Stream() for _ in range(max(1, a.streams) - 1)]
+    for st in streams[1:]:
+        st.wait_stream(streams[0])
+
+    def run_steps(n, timing=None):
+        pend, out = [], None
+        for i in range(n):
+            if len(pend) == len(streams):
+                out = pend.pop(0).result()
+            with torch.cuda.stream(streams[i % len(streams)]):
+                pend.append(step_async(timing))
+        for p in pend:
+            out = p.result()
+        return out
+
+    run_steps(max(a.warmup, len(streams)))
+    # Events are created before the timed region.  Kernel and phase times come
+    # from batches run one at a time (with several in flight their kernels
+    # overlap): from the timed steps at S = 1, else from a second pass.
+    timing = gs.timing_dict(a.steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(a.steps):
-        out = step(timing)
+    out = run_steps(a.steps, timing if len(streams) == 1 else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = 1000.0 * wall / a.steps
     qps = B * a.steps / wall
+    one_ms = None
+    if len(streams) > 1:
+        # the same batches one at a time: a batch's own latency
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(a.steps):
+            step_async(timing).result()
+        torch.cuda.synchronize()
+        one_ms = 1000.0 * (time.perf_counter() - t1) / a.steps
+        log(f"one batch in flight: {one_ms:.2f} ms/batch")
     log(f"{a.steps} steps: {ms_per_step:.2f} ms/step, {qps:.1f} queries/s, "
         f"dense rows {timing.get('dense_rows', 0)}")
 
@@ -447,9 +479,10 @@ def main():
         "config": {"workload": f"{cfg.name}: {cfg.description}", "n_docs": n_docs,
                    "postings": int(index.lengths.sum().item()), "global_batch": B, "k": k, "max_query_terms": T,
                    "weights": str(index.scores.dtype).replace("torch.", ""), "tile_docs": 1 << a.tile_log2,
-                   "path": a.path,
+                   "path": a.path, "streams": len(streams),
                    "scorer": None if plan is None else {key: plan[key] for key in
                                                         ("group_size", "unroll", "tiles_per_wg", "seed_tiles", "packed")}},
+        "ms_per_batch_one_in_flight": None if one_ms is None else round(one_ms, 3),
         "roofline": roof, "selection": selection, "index_build": index_build,
         "cpu_baseline": cpu, "parity": parity, "components_ms": components,
         "index_build_s": round(t_build, 3), "search_state_s": round(t_bounds, 3), "generate_s": round(t_gen, 1),

@@ -14,9 +14,9 @@ import numpy as np
 import torch
 
 from . import _lib
-from .chunked import build_chunk_boundaries, triton_chunked_score_fused
-from .index import CSR, build_index  # noqa: F401  (re-exported: gpusparse_retrieval.build_index)
-from .search import triton_fused_score
+from .chunked import _check_bounds, build_chunk_boundaries
+from .index import CSR, _device_of, build_index  # noqa: F401  (re-exported: gpusparse_retrieval.build_index)
+from .search import search_async
 
 BLOCK = 32          # posting lists are padded to a multiple of this
 VOCAB_PAD = 1       # vocabulary is sized from the data, plus one
@@ -74,25 +74,46 @@ def to_query_tensors(q_csr, device, *, weight_dtype=torch.float32):
     return (torch.from_numpy(ti).to(device), torch.from_numpy(ts).to(device), max_nnz)
 
 
-def retrieve(index, q_ids, q_ti, q_ts, doc_ids, k, batch_size=200, doc_chunk=131072):
+def retrieve(index, q_ids, q_ti, q_ts, doc_ids, k, batch_size=200, doc_chunk=131072, streams=2):
     """Batched retrieval with the reference's output format (gpusparse_retrieval.py:
-    135-172): per query a list of (qid, score, docno) for the top k with score > 0."""
+    135-172): per query a list of (qid, score, docno) for the top k with score > 0.
+
+    Each batch is scored as the reference's call scores it: triton_fused_score
+    (path "auto") or, above doc_chunk docs, triton_chunked_score_fused (the fused
+    path; its chunk boundaries built and checked once).  Both are `search`; here
+    each batch is queued with `search_async` on one of `streams` streams in turn,
+    so that the next batches run on the GPU while the host builds this one's
+    rankings.  The rankings are the same for any `streams` >= 1."""
     results = []
     n = q_ti.shape[0]
     kk = min(k, index.num_docs)
     chunked = index.num_docs > doc_chunk
-    bounds = build_chunk_boundaries(index, doc_chunk) if chunked else None
-    for s0 in range(0, n, batch_size):
+    if chunked:
+        bounds = build_chunk_boundaries(index, doc_chunk)
+        _check_bounds(index, bounds, doc_chunk)  # what triton_chunked_score_fused checks per call
+    path = "fused" if chunked else "auto"
+    dev = _device_of(index)
+    cur = torch.cuda.current_stream(dev)
+    pool = [cur] if streams <= 1 else [torch.cuda.Stream(dev) for _ in range(int(streams))]
+    for st in pool:
+        st.wait_stream(cur)  # the query tensors were written on the current stream
+    starts = list(range(0, n, batch_size))
+
+    def launch(i):
+        s0 = starts[i]
         s1 = min(s0 + batch_size, n)
-        qi = q_ti[s0:s1].contiguous()
-        qs = q_ts[s0:s1].contiguous()
-        if chunked:
-            scores, ids = triton_chunked_score_fused(index, qi, qs, top_k=kk, doc_chunk=doc_chunk,
-                                                     chunk_bounds=bounds)
-        else:
-            scores, ids = triton_fused_score(index, qi, qs, top_k=kk)
+        with torch.cuda.stream(pool[i % len(pool)]):
+            return search_async(index, (q_ti[s0:s1].contiguous(), q_ts[s0:s1].contiguous()), kk, path=path)
+
+    pending = [launch(i) for i in range(min(len(pool), len(starts)))] if len(pool) > 1 else []
+    for i, s0 in enumerate(starts):
+        s1 = min(s0 + batch_size, n)
+        p = pending.pop(0) if pending else launch(i)
+        scores, ids = p.result()
         scores = scores.cpu().numpy()
         ids = ids.cpu().numpy()
+        if len(pool) > 1 and i + len(pool) < len(starts):
+            pending.append(launch(i + len(pool)))
         for r in range(s1 - s0):
             ranking = [(q_ids[s0 + r], float(scores[r, j]), doc_ids[ids[r, j]])
                        for j in range(kk) if scores[r, j] > 0]

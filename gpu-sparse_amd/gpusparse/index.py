@@ -380,6 +380,7 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
     dev = _device_of(index)
     L = _lib.lib()
     V = int(index.vocab_size)
+    keys_before = set(a)
     if "dup" not in a:
         require_ascending(index)
     list_max_abs(index)
@@ -408,6 +409,10 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
             a["fwd"] = build_forward(index)
         except torch.cuda.OutOfMemoryError:
             a["fwd"] = None
+    if set(a) != keys_before:
+        # built on the current stream: complete before a search on another
+        # stream (search_async) reads it
+        torch.cuda.current_stream(dev).synchronize()
     return a
 
 

@@ -59,13 +59,20 @@ def query_tensors(index, query_batch):
     return qt.contiguous(), qw.contiguous()
 
 
-def _workspace(index, nbytes: int) -> torch.Tensor:
+def _workspace(index, nbytes: int, stream_key: int = 0) -> torch.Tensor:
+    """The index's fused-search workspace for one stream (searches in flight on
+    different streams must not share one; on one stream they run in order).  The
+    one last handed out is also aux()["workspace"], which search_counts reads."""
     a = index.aux()
-    ws = a.get("workspace")
+    pool = a.setdefault("workspaces", {})
+    ws = pool.get(stream_key)
     if ws is None or ws.numel() < nbytes:
-        a.pop("workspace", None)
+        pool.pop(stream_key, None)
+        if a.get("workspace") is ws:
+            a.pop("workspace", None)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=_device_of(index))
-        a["workspace"] = ws
+        pool[stream_key] = ws
+    a["workspace"] = ws
     return ws
 
 
@@ -87,6 +94,44 @@ def _dense_rows(index, gidx, qt, qw, k, rows, out_s, out_i, dense_budget):
                "gs_search_dense")
 
 
+class PendingSearch:
+    """A search whose kernels are queued on a stream (`search_async`).
+
+    `result()` waits for the fused pipeline's per-row status (one event, no
+    device-wide synchronisation), finishes the rows it flagged with the dense
+    path on the same stream and returns ``(scores [B, k], ids [B, k] int64)``.
+    The returned tensors are ordered on the search's stream: the stream current
+    at the `result()` call is made to wait for it."""
+
+    __slots__ = ("_out", "_stream", "_event", "_status_h", "_finish")
+
+    def __init__(self, out, stream=None, event=None, status_h=None, finish=None):
+        self._out = out
+        self._stream = stream
+        self._event = event
+        self._status_h = status_h
+        self._finish = finish
+
+    def done(self) -> bool:
+        """True when result() would not wait for the GPU."""
+        return self._finish is None or self._event.query()
+
+    def result(self):
+        if self._finish is not None:
+            self._event.synchronize()
+            bad = np.nonzero(self._status_h.numpy() != _lib.GS_ROW_DONE)[0]
+            finish, self._finish = self._finish, None
+            self._status_h = None
+            finish(bad)
+        if self._stream is not None:
+            cur = torch.cuda.current_stream(self._stream.device)
+            if cur != self._stream:
+                cur.wait_stream(self._stream)
+                for t in self._out:
+                    t.record_stream(cur)  # freed only after the current stream's uses
+        return self._out
+
+
 def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, path: str = "auto",
            sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 0, waves: int = 0,
            tiles_per_wg: int = 0, dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None,
@@ -104,6 +149,20 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     from timing["event_pool"] while it lasts (see `timing_dict`).
     batch_order: score queries in groups of consecutive queries instead of groups of
     queries sharing frequent terms (same results; for comparisons)."""
+    return search_async(index, query_batch, k, tile_log2=tile_log2, path=path, sample_tiles=sample_tiles,
+                        cand_cap=cand_cap, unroll=unroll, waves=waves, tiles_per_wg=tiles_per_wg,
+                        dense_budget=dense_budget, timing=timing, batch_order=batch_order).result()
+
+
+def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = None, path: str = "auto",
+                 sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 0, waves: int = 0,
+                 tiles_per_wg: int = 0, dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None,
+                 batch_order: bool = False) -> PendingSearch:
+    """`search` without waiting: queues the batch on the current stream and
+    returns a `PendingSearch` (same arguments and results as `search`).  The host
+    can queue the next batch, or post-process the previous one, while this one
+    runs; batches in flight on one stream run in order and share the index's
+    workspace, batches on different streams get one workspace per stream."""
     dev = _lib.require_gpu(_device_of(index))
     N = int(index.num_docs)
     kk = min(int(k), N)
@@ -115,7 +174,7 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     out_s = torch.empty((B, kk), dtype=out_dtype, device=dev)
     out_i = torch.empty((B, kk), dtype=torch.int64, device=dev)
     if B == 0:
-        return out_s, out_i
+        return PendingSearch((out_s, out_i))
     if T == 0:
         qt = torch.full((B, 1), -1, dtype=torch.int32, device=dev)
         qw = torch.zeros((B, 1), dtype=qw.dtype, device=dev)
@@ -128,17 +187,18 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     dense_bytes = B * gidx.n_tiles * (1 << tile_log2) * acc_bytes
     if path not in ("auto", "fused", "dense"):
         raise ValueError(f"unknown path {path!r}")
+    stream = torch.cuda.current_stream(dev)
     # k above MAX_K: the dense path, whose selection takes any k (rounds of MAX_K)
     use_dense = path == "dense" or kk > MAX_K or (path == "auto" and dense_bytes <= dense_budget)
     if use_dense:
         _dense_rows(index, gidx, qt, qw, kk, None, out_s, out_i, max(dense_budget, 1))
-        return out_s, out_i
+        return PendingSearch((out_s, out_i), stream)
     opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, waves, None, None, tiles_per_wg)
     opts.batch_order = int(bool(batch_order))
     need = _lib.C.c_size_t()
     _lib.check(L.gs_search_workspace(_lib.C.byref(gidx), B, T, kk, _lib.C.byref(opts), _lib.C.byref(need)),
                "gs_search_workspace")
-    ws = _workspace(index, int(need.value))
+    ws = _workspace(index, int(need.value), stream.cuda_stream)
     status = torch.empty(B, dtype=torch.int32, device=dev)
     s = _lib.stream_ptr(dev)
     if timing is not None:
@@ -158,14 +218,20 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
         timing.setdefault("search", []).append((evs[2], evs[3]))
         if ph:
             timing.setdefault("phases", []).append(ph)
-    st = status.cpu().numpy()
-    bad = np.nonzero(st != _lib.GS_ROW_DONE)[0]
-    if timing is not None:
-        timing["dense_rows"] = timing.get("dense_rows", 0) + int(bad.size)
-    if bad.size:
-        rows = torch.from_numpy(bad.astype(np.int32)).to(dev)
-        _dense_rows(index, gidx, qt, qw, kk, rows, out_s, out_i, max(dense_budget, 1))
-    return out_s, out_i
+    status_h = torch.empty(B, dtype=torch.int32, pin_memory=True)
+    status_h.copy_(status, non_blocking=True)
+    done = torch.cuda.Event()
+    done.record(stream)
+
+    def finish(bad):
+        if timing is not None:
+            timing["dense_rows"] = timing.get("dense_rows", 0) + int(bad.size)
+        if bad.size:
+            with torch.cuda.stream(stream):
+                rows = torch.from_numpy(bad.astype(np.int32)).to(dev)
+                _dense_rows(index, gidx, qt, qw, kk, rows, out_s, out_i, max(dense_budget, 1))
+
+    return PendingSearch((out_s, out_i), stream, done, status_h, finish)
 
 
 def _call_events(phases: bool = True):

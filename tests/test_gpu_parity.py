@@ -333,6 +333,62 @@ def test_search_dense_fallback_rows(c1):
     assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
 
 
+def test_search_async_batches_in_flight(c1):
+    """Batches queued with search_async before any result is read, on one stream
+    and round-robin over two and three streams, every other one with a candidate
+    cap that sends rows to the dense path (finished at result()): each returns
+    what the oracle returns for it."""
+    ix, ref, ti, tw = c1
+    dev = ix.doc_ids.device
+    batches = [(0, 40), (40, 96), (96, 100), (100, 164)]
+    want = {}
+    for b0, b1 in batches:
+        vs, _, vi = O.c_search(ref, ti[b0:b1], tw[b0:b1], 200, threads=8)
+        want[(b0, b1)] = (vs, vi)
+    qt, qw = torch.from_numpy(ti).to(dev), torch.from_numpy(tw).to(dev)
+    for n_streams in (1, 2, 3):
+        print(f"search_async streams={n_streams}", flush=True)
+        streams = [torch.cuda.current_stream(dev)] + [torch.cuda.Stream(dev) for _ in range(n_streams - 1)]
+        for st in streams[1:]:
+            st.wait_stream(streams[0])
+        pend = []
+        for j, key in enumerate(batches * 2):
+            b0, b1 = key
+            timing = {}
+            with torch.cuda.stream(streams[j % n_streams]):
+                p = gs.search_async(ix, (qt[b0:b1], qw[b0:b1]), 200, path="fused", cand_cap=400 if j % 2 else 0,
+                                    timing=timing)
+            pend.append((key, timing, p))
+        n_dense = 0
+        for key, timing, p in pend:
+            s, i = p.result()
+            n_dense += timing["dense_rows"]
+            vs, vi = want[key]
+            assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs), (n_streams, key)
+        assert n_dense > 0
+        torch.cuda.synchronize(dev)
+
+
+@pytest.mark.parametrize("streams", [1, 3])
+def test_retrieve_streams(device, streams):
+    """retrieve's batches in flight on `streams` streams: the reference's rankings
+    (checked against the oracle's), for the plain and the chunked entry point."""
+    rng = np.random.default_rng(43)
+    csr = random_csr(rng, 2500, 300, max_len=16, sort_rows=True)
+    ti, tw = random_queries(rng, 23, 300, max_len=8)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    vs, _, vi = O.c_search(ref, ti, tw, 15, threads=4)
+    q_ids = [f"Q{q}" for q in range(23)]
+    doc_ids = [f"D{d}" for d in range(2500)]
+    want = O.rankings(q_ids, vs, vi, doc_ids, 15)
+    qt, qw = torch.from_numpy(ti).to(device), torch.from_numpy(tw).to(device)
+    for doc_chunk in (131072, 1000):
+        print(f"retrieve streams={streams} doc_chunk={doc_chunk}", flush=True)
+        got = gs.retrieve(ix, q_ids, qt, qw, doc_ids, 15, batch_size=5, doc_chunk=doc_chunk, streams=streams)
+        assert got == want
+
+
 def test_search_small_sample_and_single_tile(c1):
     ix, ref, ti, tw = c1
     assert_search_equal(ix, ref, ti[:16], tw[:16], 30, path="fused", sample_tiles=1)
