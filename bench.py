@@ -86,6 +86,7 @@ def lds_peak():
     except (OSError, ValueError):
         return None
     return {"peak": float(r["ds_add_u32_random"]["lane_ops_per_s"]),
+            "conflict_free": float(r["ds_add_u32_conflict_free"]["lane_ops_per_s"]),
             "source": os.path.relpath(path, ROOT) + ": ds_add_u32, random addresses"}
 
 
@@ -370,6 +371,9 @@ def main():
                 "frac": None if lds is None else round(adds_per_s / lds["peak"], 4),
                 "traffic": phys,
                 "peak_source": None if lds is None else lds["source"],
+                # the packed copy's bank-aware order brings the adds close to the
+                # conflict-free rate, the higher ceiling
+                "frac_of_conflict_free_rate": None if lds is None else round(adds_per_s / lds["conflict_free"], 4),
                 "hbm_physical": None if phys is None else {
                     "achieved": round(phys / (avg_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(phys / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
