@@ -510,6 +510,7 @@ __global__ void k_fill_pads(const int64_t *__restrict__ offsets, const int32_t *
 // ------------------------------------------------------------------ per-list scans
 
 constexpr int kListParts = 16;  // waves per list for the per-list passes
+constexpr int kListUnroll = 8;  // loads in flight per lane in those passes
 
 template <int WT>
 __device__ __forceinline__ float weight_as_float(const void *w, int64_t i) {
@@ -533,11 +534,20 @@ __global__ void k_list_max(const void *__restrict__ w, const int64_t *__restrict
     const int64_t b = part * per, e = b + per < L ? b + per : L;
     if (b >= e) return;
     uint32_t mk = 0, ma = 0;
-    for (int64_t i = b + lane; i < e; i += 64) {
-        float v = weight_as_float<WT>(w, o + i);
-        uint32_t k = gs_key_f32(v), a = __float_as_uint(fabsf(v));
-        mk = k > mk ? k : mk;
-        ma = a > ma ? a : ma;
+    // kListUnroll loads in flight per lane (a long list's parts are latency-bound)
+    for (int64_t i0 = b + lane; i0 < e; i0 += 64 * kListUnroll) {
+        float v[kListUnroll];
+#pragma unroll
+        for (int u = 0; u < kListUnroll; ++u) {
+            const int64_t i = i0 + 64 * u;
+            v[u] = i < e ? weight_as_float<WT>(w, o + i) : weight_as_float<WT>(w, o + b);
+        }
+#pragma unroll
+        for (int u = 0; u < kListUnroll; ++u) {
+            const uint32_t k = gs_key_f32(v[u]), a = __float_as_uint(fabsf(v[u]));
+            mk = k > mk ? k : mk;
+            ma = a > ma ? a : ma;
+        }
     }
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
@@ -575,10 +585,20 @@ __global__ void k_check_lists(const int32_t *__restrict__ doc, const int64_t *__
     if (b < 1) b = 1;
     if (b >= e) return;
     uint32_t nbad = 0, ndup = 0;
-    for (int64_t i = b + lane; i < e; i += 64) {
-        int32_t cur = doc[o + i], prev = doc[o + i - 1];
-        nbad += cur < prev;
-        ndup += cur == prev;
+    for (int64_t i0 = b + lane; i0 < e; i0 += 64 * kListUnroll) {
+        int32_t cur[kListUnroll], prev[kListUnroll];
+#pragma unroll
+        for (int u = 0; u < kListUnroll; ++u) {
+            const int64_t i = i0 + 64 * u < e ? i0 + 64 * u : b;  // past the end: a pair counted below as neither
+            cur[u] = doc[o + i];
+            prev[u] = doc[o + i - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < kListUnroll; ++u) {
+            const bool in = i0 + 64 * u < e;
+            nbad += in && cur[u] < prev[u];
+            ndup += in && cur[u] == prev[u];
+        }
     }
     nbad = gs_wave_sum(nbad);
     ndup = gs_wave_sum(ndup);
