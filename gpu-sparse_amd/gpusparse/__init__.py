@@ -8,7 +8,7 @@ in hand-written HIP kernels (libgpusparse.so) called through a C ABI
 from .index import (BLOCK_SIZE, CSR, VOCAB_SIZE, GPUInvertedIndex, build_from_csr, build_gpu_index_from_csr,
                     build_gpu_inverted_index, build_gpu_inverted_index_from_sparse, build_index, check_lists,
                     index_memory_stats, require_ascending)
-from .search import (MAX_K, PendingSearch, atomic_fused_score, compacted_topk, scatter_add, search, search_async,
+from .search import (MAX_K, MAX_T, PendingSearch, atomic_fused_score, compacted_topk, scatter_add, search, search_async,
                      search_counts, search_plan, timing_dict, topk_rows, triton_fused_score)
 from .chunked import build_chunk_boundaries, triton_chunked_score, triton_chunked_score_fused
 from .engine import determine_dimension, retrieve, run_engine, to_csr, to_query_tensors, write_run
@@ -17,7 +17,7 @@ from .storage import load_index, save_index
 __all__ = [
     "BLOCK_SIZE", "CSR", "VOCAB_SIZE", "GPUInvertedIndex", "build_from_csr", "build_gpu_index_from_csr",
     "build_gpu_inverted_index", "build_gpu_inverted_index_from_sparse", "build_index", "check_lists",
-    "index_memory_stats", "require_ascending", "MAX_K", "PendingSearch", "atomic_fused_score", "compacted_topk",
+    "index_memory_stats", "require_ascending", "MAX_K", "MAX_T", "PendingSearch", "atomic_fused_score", "compacted_topk",
     "scatter_add", "search", "search_async", "search_counts", "search_plan", "timing_dict", "topk_rows", "triton_fused_score", "build_chunk_boundaries",
     "triton_chunked_score", "triton_chunked_score_fused", "determine_dimension", "retrieve", "run_engine", "to_csr", "to_query_tensors",
     "write_run", "load_index", "save_index",

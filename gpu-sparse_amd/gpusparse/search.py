@@ -20,6 +20,7 @@ from . import _lib
 from .index import default_tile_log2, gs_index_struct, _device_of
 
 MAX_K = 8192  # largest k of the fused path and of compacted_topk; search answers larger k densely
+MAX_T = 8192  # widest query batch of the fused path (terms per query); search answers wider ones densely
 DEFAULT_DENSE_BUDGET = 1 << 30   # bytes of [B, N] score rows below which the dense path is used
 
 
@@ -140,7 +141,8 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
 
     tile_log2: doc-tile size of the scorer (default: index.default_tile_log2).
     path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense";
-    k above MAX_K (8192) always takes the dense path (any k up to the doc count).
+    k above MAX_K (8192) or queries wider than MAX_T (8192 terms) always take the
+    dense path (any k up to the doc count, any width).
     timing: optional dict; receives event pairs on the launch stream bracketing the
     fused scoring kernel ("score_kernel") and the whole gs_search call ("search"),
     the GS_SEARCH_PHASES events of each call ("phases": start, query prep,
@@ -188,8 +190,9 @@ def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = Non
     if path not in ("auto", "fused", "dense"):
         raise ValueError(f"unknown path {path!r}")
     stream = torch.cuda.current_stream(dev)
-    # k above MAX_K: the dense path, whose selection takes any k (rounds of MAX_K)
-    use_dense = path == "dense" or kk > MAX_K or (path == "auto" and dense_bytes <= dense_budget)
+    # k above MAX_K or queries wider than MAX_T terms: the dense path, whose
+    # selection takes any k (rounds of MAX_K) and whose scorer any width
+    use_dense = path == "dense" or kk > MAX_K or T > MAX_T or (path == "auto" and dense_bytes <= dense_budget)
     if use_dense:
         _dense_rows(index, gidx, qt, qw, kk, None, out_s, out_i, max(dense_budget, 1))
         return PendingSearch((out_s, out_i), stream)

@@ -733,8 +733,8 @@ def test_chunked_entry_points_ignore_bound_contents_and_block_pl(c1):
 def test_k_above_8192_and_width_limit(c1):
     """k above 8192 (the LDS selection's capacity) is answered by the dense path
     in rounds of 8192 and equals the oracle bit for bit, up to k = num_docs, for
-    any path argument; query widths above 8192 terms on the fused path raise
-    ValueError, as does compacted_topk above its capacity."""
+    any path argument; so are queries wider than 8192 terms (repeated terms
+    included); compacted_topk raises ValueError above its capacity."""
     ix, ref, ti, tw = c1
     assert gs.MAX_K == 8192
     q = (torch.from_numpy(ti[:3]), torch.from_numpy(tw[:3]))
@@ -747,9 +747,15 @@ def test_k_above_8192_and_width_limit(c1):
     s, i = gs.triton_fused_score(ix, q[0], q[1], top_k=9000)
     vs, _, vi = O.c_search(ref, ti[:3], tw[:3], 9000, threads=8)
     assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
-    wide_t = torch.full((1, 8193), 5, dtype=torch.int32)
-    with pytest.raises(ValueError, match="8192"):
-        gs.search(ix, (wide_t, torch.ones((1, 8193))), 10, path="fused")
+    assert gs.MAX_T == 8192
+    rng = np.random.default_rng(12)
+    wt = rng.integers(-1, 4000, size=(2, 9000)).astype(np.int32)  # -1: padding
+    ww = rng.random((2, 9000), dtype=np.float32)
+    for path in ("fused", "auto"):
+        print(f"width 9000 path={path}", flush=True)
+        s, i = gs.search(ix, (torch.from_numpy(wt), torch.from_numpy(ww)), 100, path=path)
+        vs, _, vi = O.c_search(ref, wt, ww, 100, threads=8)
+        assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
     rows = torch.rand((2, 20000), device=ix.doc_ids.device)
     with pytest.raises(ValueError, match="8192"):
         gs.compacted_topk(rows, torch.zeros(2, device=rows.device), 9000, max_cand=9000)
