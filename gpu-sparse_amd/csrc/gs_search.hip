@@ -980,7 +980,9 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
             }
         }
     }
-    __builtin_amdgcn_s_setprio(0);
+    // Emission and the next tile's set-up are latency-bound: they issue at the
+    // highest priority, ahead of the other workgroup's adds.
+    __builtin_amdgcn_s_setprio(3);
     __syncthreads();
 
     // ---- emission of candidates >= tau - margin.  The slices are scanned in
