@@ -94,7 +94,12 @@ def retrieve(index, q_ids, q_ti, q_ts, doc_ids, k, batch_size=200, doc_chunk=131
     path = "fused" if chunked else "auto"
     dev = _device_of(index)
     cur = torch.cuda.current_stream(dev)
-    pool = [cur] if streams <= 1 else [torch.cuda.Stream(dev) for _ in range(int(streams))]
+    # side streams are kept with the index, so that repeated calls reuse them and
+    # their workspaces (one per stream) instead of adding new ones
+    side = index.aux().setdefault("retrieve_streams", [])
+    while len(side) < int(streams):
+        side.append(torch.cuda.Stream(dev))
+    pool = [cur] if streams <= 1 else side[:int(streams)]
     for st in pool:
         st.wait_stream(cur)  # the query tensors were written on the current stream
     starts = list(range(0, n, batch_size))
