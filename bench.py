@@ -65,8 +65,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-queries", type=int, default=4)
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
+    ap.add_argument("--inflight", type=int, default=2,
+                    help="batches in flight: batch i is queued before batch i - D's status is read (1: one at a time)")
     ap.add_argument("--streams", type=int, default=1,
-                    help="batches in flight, one stream each (1: each batch finishes before the next is queued)")
+                    help="streams the batches in flight take in turn (at most --inflight; 1: all on one stream, "
+                         "so their kernels run one after another)")
     ap.add_argument("--summarize-traffic", default=None, metavar="DIR",
                     help="write profiles/traffic_k_score_union_<config>.json from rocprofv3 --pmc runs under DIR")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -290,9 +293,12 @@ def main():
                                waves=a.waves, tiles_per_wg=a.tiles_per_wg, sample_tiles=a.sample_tiles,
                                timing=timing)
 
-    # Batch i is queued on stream i mod S once batch i - S has finished (its
-    # status read and any flagged rows completed), so up to S batches are in
-    # flight; S = 1 runs them one after another.
+    # Batch i is queued on stream i mod S once batch i - D has finished (its
+    # status read and any flagged rows completed), so up to D batches are in
+    # flight.  D = 1 runs them one at a time; with S = 1 the batches in flight
+    # share one stream, so only the host's work (the next batch's launches, the
+    # previous one's status read) overlaps the GPU's.
+    depth = max(1, a.inflight, a.streams)
     streams = [torch.cuda.current_stream()] + [torch.cuda.Stream() for _ in range(max(1, a.streams) - 1)]
     for st in streams[1:]:
         st.wait_stream(streams[0])
@@ -300,7 +306,7 @@ def main():
     def run_steps(n, timing=None):
         pend, out = [], None
         for i in range(n):
-            if len(pend) == len(streams):
+            if len(pend) == depth:
                 out = pend.pop(0).result()
             with torch.cuda.stream(streams[i % len(streams)]):
                 pend.append(step_async(timing))
@@ -308,10 +314,10 @@ def main():
             out = p.result()
         return out
 
-    run_steps(max(a.warmup, len(streams)))
+    run_steps(max(a.warmup, depth))
     # Events are created before the timed region.  Kernel and phase times come
-    # from batches run one at a time (with several in flight their kernels
-    # overlap): from the timed steps at S = 1, else from a second pass.
+    # from kernels that do not overlap: from the timed steps on one stream, else
+    # from a second pass with one batch at a time.
     timing = gs.timing_dict(a.steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -321,12 +327,12 @@ def main():
     ms_per_step = 1000.0 * wall / a.steps
     qps = B * a.steps / wall
     one_ms = None
-    if len(streams) > 1:
+    if depth > 1:
         # the same batches one at a time: a batch's own latency
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         for _ in range(a.steps):
-            step_async(timing).result()
+            step_async(timing if len(streams) > 1 else None).result()
         torch.cuda.synchronize()
         one_ms = 1000.0 * (time.perf_counter() - t1) / a.steps
         log(f"one batch in flight: {one_ms:.2f} ms/batch")
@@ -483,7 +489,7 @@ def main():
         "config": {"workload": f"{cfg.name}: {cfg.description}", "n_docs": n_docs,
                    "postings": int(index.lengths.sum().item()), "global_batch": B, "k": k, "max_query_terms": T,
                    "weights": str(index.scores.dtype).replace("torch.", ""), "tile_docs": 1 << a.tile_log2,
-                   "path": a.path, "streams": len(streams),
+                   "path": a.path, "inflight": depth, "streams": len(streams),
                    "scorer": None if plan is None else {key: plan[key] for key in
                                                         ("group_size", "unroll", "tiles_per_wg", "seed_tiles", "packed")}},
         "ms_per_batch_one_in_flight": None if one_ms is None else round(one_ms, 3),
