@@ -1338,8 +1338,10 @@ __global__ void __launch_bounds__(256)
 constexpr int kRescoreWaves = 4;
 constexpr int kRowStage = 512;  // row entries staged in LDS per wave
 
+// Eight workgroups (eight waves per SIMD) per CU: the waves wait on row loads, so
+// more of them in flight pay for the 64-register cap (a 16-byte spill).
 template <int WT>
-__global__ void __launch_bounds__(64 * kRescoreWaves)
+__global__ void __launch_bounds__(64 * kRescoreWaves, 8)
     k_rescore_fwd(const int64_t *__restrict__ row_ptr, const int32_t *__restrict__ fterm,
                   const void *__restrict__ fw, int32_t V, const int32_t *__restrict__ qt,
                   const float *__restrict__ qw, int32_t T, const uint32_t *__restrict__ resc_doc,
