@@ -767,23 +767,25 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
             int32_t doc[UNROLL];
             store_t wv[UNROLL];
         };
-        // Waves of a SIMD are served oldest first, so with equal shares the
-        // youngest wave of each SIMD would finish last.  A wave instead lowers
-        // its issue priority as its share of the chunks completes (3 for the
-        // first quarter, then 2, 1, 0): waves that are behind are served first.
+        // A wave raises its issue priority as its share of the chunks completes
+        // (0 for the first quarter, then 1, 2, 3).  The two workgroups of a CU
+        // share its SIMDs: serving the waves that are further along first keeps
+        // the workgroups apart, so that one's emission and set-up overlap the
+        // other's adds.  (Lowering it instead, 3, 2, 1, 0, evened out the waves
+        // of a workgroup but drew the two workgroups into step.)
         const int my_total = (total - wave + NW - 1) / NW;  // chunks of this wave in the batch
         // level = floor(4 done / my_total), i.e. level >= L once done >= ceil(L
         // my_total / 4); only the next boundary is compared per chunk
         auto quarter = [&](int L) { return (L * my_total + 3) >> 2; };
         int level = 0, next_at = quarter(1);
-        __builtin_amdgcn_s_setprio(3);
+        __builtin_amdgcn_s_setprio(0);
         auto progress = [&](int done) {
             if (done < next_at) return;
             while (level < 3 && done >= quarter(level + 1)) ++level;
             next_at = level < 3 ? quarter(level + 1) : 0x7FFFFFFF;
-            if (level == 1) __builtin_amdgcn_s_setprio(2);
-            else if (level == 2) __builtin_amdgcn_s_setprio(1);
-            else __builtin_amdgcn_s_setprio(0);
+            if (level == 1) __builtin_amdgcn_s_setprio(1);
+            else if (level == 2) __builtin_amdgcn_s_setprio(2);
+            else __builtin_amdgcn_s_setprio(3);
         };
         for (int cb = wave; cb < total; cb += 64 * NW) {
             const int nmine = min(64, (total - cb + NW - 1) / NW);  // chunks of this wave in the block
