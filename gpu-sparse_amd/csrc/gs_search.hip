@@ -47,7 +47,8 @@ constexpr int kRescoreCap = 16384;   // candidates rescored per query before the
 constexpr int64_t kSeedMinDocs = 4096;    // fewest docs of the default first tiles scored with tau = 0
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
-constexpr int64_t kPairMinWgs = 12288;    // workgroups (~48 per CU) needed before a workgroup scores several tiles
+constexpr int64_t kPairMinWgs = 12288;    // workgroups (~48 per CU) needed before a workgroup scores two tiles
+constexpr int64_t kTripleMinWgs = 49152;  // and before it scores three
 constexpr size_t kTileLds = 144 * 1024;  // LDS of the fp64 / uint32 row tiles of one dense-path workgroup
 // LDS of the score slices of one fused-scoring workgroup (2 queries x 8192 docs):
 // two such workgroups share a CU, so one's set-up and emission (latency-bound)
@@ -1652,8 +1653,8 @@ bool packed_usable(const gs_index *ix) {
 
 // default tiles per scoring workgroup of a launch over `tiles` tiles
 int default_tiles_per_wg(int tiles, int n_groups) {
-    for (int t = 3; t > 1; --t)
-        if ((int64_t)((tiles + t - 1) / t) * n_groups >= kPairMinWgs) return t;
+    if ((int64_t)((tiles + 2) / 3) * n_groups >= kTripleMinWgs) return 3;
+    if ((int64_t)((tiles + 1) / 2) * n_groups >= kPairMinWgs) return 2;
     return 1;
 }
 
@@ -1819,8 +1820,8 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     auto run_union = [&](int tile_begin, int tiles) -> int {
         e.tile_begin = tile_begin;
         e.tiles = tiles;
-        // Default: three tiles per workgroup when that still leaves kPairMinWgs
-        // workgroups, else two, else one.  A further tile saves a workgroup launch
+        // Default: three tiles per workgroup when that still leaves kTripleMinWgs
+        // workgroups, else two when that leaves kPairMinWgs, else one.  A further tile saves a workgroup launch
         // and the term set-up (its bounds are loaded while the previous tile is
         // scored); with few workgroups the last, partly filled round of workgroups
         // costs more.  The

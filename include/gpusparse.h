@@ -87,7 +87,8 @@ typedef struct gs_search_opts {
     void *ev_score_begin;  /* optional hipEvent_t recorded on `stream` right before the fused */
     void *ev_score_end;    /* scoring kernel and right after it (per-kernel timing); may be NULL */
     int32_t tiles_per_wg;  /* consecutive doc tiles walked by one scoring workgroup, 1..64 (default 3
-                              when that leaves at least 12288 workgroups, else 2 if that does, else 1) */
+                              when that leaves at least 49152 workgroups, else 2 when that leaves at
+                              least 12288, else 1) */
     void **ev_phases;      /* optional array of GS_SEARCH_PHASES hipEvent_t (entries may be NULL)
                               recorded on `stream` at the phase boundaries of gs_search: start,
                               query prep, threshold seed, scoring, candidate selection, fp64
