@@ -242,7 +242,8 @@ def main():
         return
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
-              "see DESIGN.md for how the index would shard.", file=sys.stderr)
+              "the index would shard by doc range, one shard per GPU, with the per-GPU top-k merged.",
+              file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
