@@ -65,6 +65,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-queries", type=int, default=4)
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
+    ap.add_argument("--scorer", default="auto", choices=["auto", "hybrid", "lds"],
+                    help="fused scorer: hybrid (heavy terms as int8 MFMA products, 512-doc tiles), lds (LDS adds "
+                         "for every term) or auto (hybrid when the index allows it and no tile size is named)")
     ap.add_argument("--inflight", type=int, default=2,
                     help="batches in flight: batch i is queued before batch i - D's status is read (1: one at a time)")
     ap.add_argument("--streams", type=int, default=1,
@@ -250,7 +253,8 @@ def main():
 
     import gpusparse as gs
     from gpusparse import synth
-    from gpusparse.index import default_tile_log2, ensure_search_state
+    from gpusparse.index import ensure_search_state
+    from gpusparse.search import scorer_choice
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -275,9 +279,9 @@ def main():
     torch.cuda.synchronize()
     t_build = time.perf_counter() - t0
     t0 = time.perf_counter()
-    if not a.tile_log2:
-        a.tile_log2 = default_tile_log2(index)
-    ensure_search_state(index, a.tile_log2)
+    want_hybrid = {"auto": None, "hybrid": True, "lds": False}[a.scorer]
+    a.tile_log2, hyb = scorer_choice(index, a.tile_log2 or None, want_hybrid)
+    ensure_search_state(index, a.tile_log2, hybrid=hyb)
     torch.cuda.synchronize()
     t_bounds = time.perf_counter() - t0
     log(f"index built in {t_build:.2f}s (incl. H2D of the CSR); search state (tile bounds, doc-major copy) "
@@ -292,7 +296,7 @@ def main():
             return gs.PendingSearch(gs.atomic_fused_score(index, qt, qw, k))
         return gs.search_async(index, (qt, qw), k, tile_log2=a.tile_log2, path=a.path, unroll=a.unroll,
                                waves=a.waves, tiles_per_wg=a.tiles_per_wg, sample_tiles=a.sample_tiles,
-                               timing=timing)
+                               timing=timing, hybrid=hyb)
 
     # Batch i is queued on stream i mod S once batch i - D has finished (its
     # status read and any flagged rows completed), so up to D batches are in
@@ -355,7 +359,7 @@ def main():
         n_tiles = (index.num_docs + (1 << a.tile_log2) - 1) >> a.tile_log2
         # the main launch scores the tiles after the seed tiles
         plan = gs.search_plan(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles, unroll=a.unroll,
-                              tiles_per_wg=a.tiles_per_wg)
+                              tiles_per_wg=a.tiles_per_wg, hybrid=hyb)
         S = min(plan["seed_tiles"], n_tiles)
         tb = index.aux()[("tile_bounds", a.tile_log2)]
         cols = tb[:, [S, n_tiles]].cpu().numpy().astype(np.int64)
@@ -410,7 +414,7 @@ def main():
     selection = None
     if a.path == "fused" and timing.get("phases"):
         cand, resc = gs.search_counts(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles,
-                                      unroll=a.unroll, tiles_per_wg=a.tiles_per_wg)
+                                      unroll=a.unroll, tiles_per_wg=a.tiles_per_wg, hybrid=hyb)
         per = np.array([[ev[i].elapsed_time(ev[i + 1]) for i in range(len(ev) - 1)] for ev in timing["phases"]])
         sel_ms = float(np.median(per[:, 3:6].sum(axis=1)))
         n_cand = int(np.minimum(cand.astype(np.int64), 65536).sum())
@@ -492,7 +496,8 @@ def main():
                    "weights": str(index.scores.dtype).replace("torch.", ""), "tile_docs": 1 << a.tile_log2,
                    "path": a.path, "inflight": depth, "streams": len(streams),
                    "scorer": None if plan is None else {key: plan[key] for key in
-                                                        ("group_size", "unroll", "tiles_per_wg", "seed_tiles", "packed")}},
+                                                        ("group_size", "unroll", "tiles_per_wg", "seed_tiles", "packed",
+                                                         "hybrid")}},
         "ms_per_batch_one_in_flight": None if one_ms is None else round(one_ms, 3),
         "roofline": roof, "selection": selection, "index_build": index_build,
         "cpu_baseline": cpu, "parity": parity, "components_ms": components,

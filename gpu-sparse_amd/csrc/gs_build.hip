@@ -929,6 +929,47 @@ __global__ void __launch_bounds__(1024) k_heavy_terms(const int32_t *__restrict_
     }
 }
 
+// Dense copy of the heavy terms' packed integer weights, the B operand of the
+// hybrid scorer's int8 matrix products: row d holds two limb vectors of
+// GS_HEAVY_TERMS bytes, low = wq & 127 and high = wq >> 7 (arithmetic), for wq
+// the packed copy's integer weight of (d, heavy[h]) (pack_word_of) and 0 where
+// doc d lacks term h.  Every |wq| <= 16383 fits: low in [0, 127], high in
+// [-128, 127].  One thread per posting of one heavy list (blockIdx.y = h); the
+// lists hold each doc at most once (checked by the caller).
+template <int WT>
+__global__ void k_head_fill(const int32_t *__restrict__ doc, const void *__restrict__ w,
+                            const int64_t *__restrict__ offsets, const int32_t *__restrict__ lengths,
+                            const int32_t *__restrict__ heavy, int32_t shift, int64_t n_docs, int8_t *__restrict__ head) {
+    const int h = blockIdx.y;
+    const int32_t t = heavy[h];
+    if (t < 0) return;
+    const int64_t o = offsets[t];
+    const int32_t n = lengths[t];
+    const auto *wall = reinterpret_cast<const typename gs_weight<WT>::store_t *>(w);
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t d = doc[o + i];
+        if (d < 0 || d >= n_docs) continue;
+        // the packed word's weight half: uint8 0..255, or int16 rint(w 2^shift)
+        const int32_t wq = (int32_t)(int16_t)(pack_word_of<WT>(d, wall[o + i], 0u, shift) >> 16);
+        int8_t *row = head + (int64_t)d * (2 * kHeavyTerms);
+        row[h] = (int8_t)(wq & 127);
+        row[kHeavyTerms + h] = (int8_t)(wq >> 7);
+    }
+}
+
+// rank[t] = h for t = heavy[h], -1 for every other term
+__global__ void k_head_rank(int32_t V, int8_t *__restrict__ rank) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < V; i += (int64_t)gridDim.x * blockDim.x)
+        rank[i] = -1;
+}
+__global__ void k_head_rank_set(const int32_t *__restrict__ heavy, int32_t V, int8_t *__restrict__ rank) {
+    const int h = threadIdx.x;
+    if (h < kHeavyTerms) {
+        const int32_t t = heavy[h];
+        if (t >= 0 && t < V) rank[t] = (int8_t)h;
+    }
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -1341,6 +1382,41 @@ extern "C" int gs_heavy_terms(const int32_t *lengths_d, int32_t vocab, int32_t *
     GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
     GS_REQUIRE(lengths_d && heavy_d, "null pointer");
     k_heavy_terms<<<1, 1024, 0, gs_stream(stream)>>>(lengths_d, vocab, heavy_d);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
+extern "C" int gs_head_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, const int64_t *offsets_d,
+                            const int32_t *lengths_d, int32_t vocab, const int32_t *heavy_d, int32_t w_shift,
+                            int64_t n_docs, int64_t n_rows, int8_t *head_d, int8_t *head_rank_d, void *stream) {
+    GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
+    GS_REQUIRE(n_docs >= 0 && n_rows >= n_docs, "head rows %lld fewer than the %lld docs", (long long)n_rows,
+               (long long)n_docs);
+    GS_REQUIRE(wtype >= GS_W_F32 && wtype <= GS_W_U8, "unknown weight type %d", wtype);
+    GS_REQUIRE(wtype == GS_W_U8 || (w_shift >= -200 && w_shift <= 200), "w_shift %d outside [-200, 200]", w_shift);
+    GS_REQUIRE(doc_ids_d && weights_d && offsets_d && lengths_d && heavy_d && head_d && head_rank_d,
+               "null pointer");
+    hipStream_t s = gs_stream(stream);
+    const int64_t bytes = n_rows * 2 * kHeavyTerms;
+    k_fill<uint32_t><<<gs_blocks(bytes / 4, 256, 1 << 16), 256, 0, s>>>(reinterpret_cast<uint32_t *>(head_d),
+                                                                         bytes / 4, 0u);
+    k_head_rank<<<gs_blocks(vocab, 256), 256, 0, s>>>(vocab, head_rank_d);
+    k_head_rank_set<<<1, kHeavyTerms, 0, s>>>(heavy_d, vocab, head_rank_d);
+    const dim3 g(gs_blocks(n_docs, 256, 4096), kHeavyTerms);
+    switch (wtype) {
+        case GS_W_F32:
+            k_head_fill<GS_W_F32><<<g, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d, w_shift,
+                                                    n_docs, head_d);
+            break;
+        case GS_W_F16:
+            k_head_fill<GS_W_F16><<<g, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d, w_shift,
+                                                    n_docs, head_d);
+            break;
+        default:
+            k_head_fill<GS_W_U8><<<g, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d, 0, n_docs,
+                                                   head_d);
+            break;
+    }
     GS_CHECK_LAUNCH();
     return GS_OK;
 }

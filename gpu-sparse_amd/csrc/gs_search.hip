@@ -341,12 +341,14 @@ __global__ void __launch_bounds__(512) k_score_dense(const DenseArgs a) {
 // the distinct terms (see the reordering at the end) with u_ebeg = entry count
 // << 16 | first entry.  Entry weights are stored pre-scaled: q * 2^e_q as fp32
 // bits for float weights, or with the packed copy (pk != 0) the integer rint(q *
-// 2^f) (k_query_prep), and the uint8 weight for impacts.
+// 2^f) (k_query_prep), and the uint8 weight for impacts.  With `hrank` (the
+// hybrid scorer) the heavy terms are left out: the unions hold the tail terms.
 template <int WT>
 __global__ void __launch_bounds__(1024)
     k_group_terms(const int32_t *__restrict__ qt, const void *__restrict__ qw, const float *__restrict__ scale,
-                  int32_t pk, int32_t B, int32_t T, int32_t V, int32_t G, int32_t ecap, int32_t *__restrict__ u_term,
-                  int32_t *__restrict__ u_ebeg, int32_t *__restrict__ u_count, uint2 *__restrict__ e_sw) {
+                  int32_t pk, int32_t B, int32_t T, int32_t V, int32_t G, int32_t ecap,
+                  const int8_t *__restrict__ hrank, int32_t *__restrict__ u_term, int32_t *__restrict__ u_ebeg,
+                  int32_t *__restrict__ u_count, uint2 *__restrict__ e_sw) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     __shared__ int32_t s_sh[17];
     __shared__ int32_t s_tot;
@@ -365,7 +367,7 @@ __global__ void __launch_bounds__(1024)
             const int q = grp * G + g;
             const int64_t src = (int64_t)q * T + j;
             const int32_t t = qt[src];
-            if ((uint32_t)t < (uint32_t)V) {
+            if ((uint32_t)t < (uint32_t)V && !(hrank && hrank[t] >= 0)) {
                 kk = ((uint64_t)(uint32_t)t << 32) | ((uint64_t)g << 20) | (uint64_t)j;
                 if (WT == GS_W_U8) {
                     w = (uint32_t) reinterpret_cast<const uint8_t *>(qw)[src];
@@ -606,6 +608,145 @@ constexpr size_t kUnionMetaLds =
     (size_t)kUnionBatch * 8 + (size_t)kUnionBatch * 4 + (size_t)(kUnionBatch + 2) * 8 + (size_t)kUnionBatch * 12;
 static_assert(kUnionTileLds + kUnionMetaLds + kStaticLdsBudget <= kLdsPerWg / 2,
               "two scoring workgroups must fit the 160 KiB of LDS of a CU");
+
+// ---------------------------------------------------------------------- candidate emission
+
+struct EmitArgs {
+    uint32_t *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key;
+    int32_t G, cap, k;
+};
+
+// Emission of one tile's slices (G int32 slices of 1 << (cps_log2 + 8) docs at
+// LDS word `acc`, slot g's slice at word g << (cps_log2 + 8)): every doc at or
+// above its slot's threshold s_thr[g] (set and fenced by the caller) becomes a
+// candidate (doc, key) of query grp * G + g, counted in that query's histogram,
+// and tau is raised from the histogram as the counts grow.  The slices are
+// scanned in 256-doc chunks, 4 docs per lane (one 16-byte LDS read); slices are
+// zero or hold sums of every doc of the tile (docs past n_docs add nothing), and
+// thresholds >= 1 make the signed compare also reject zero and negative sums.
+// Pass 1 counts each chunk's candidates; one wave per slot scans the slot's
+// chunk counts (one per lane) and reserves the slot's range with one global
+// atomic; pass 2 revisits only the chunks holding candidates (a wave reads its
+// chunk counts at once, one per lane).  Whole workgroup (kUnionThreads) calls it.
+__device__ __forceinline__ void emit_slices(const EmitArgs &a, const uint32_t *acc, int nq, int cps_log2,
+                                            int64_t doc0, int grp, uint32_t *s_thr, uint32_t *s_off,
+                                            uint32_t *s_ccnt, uint32_t *s_base, uint32_t *s_emit, uint32_t *s_maxb) {
+    constexpr int NW = kUnionThreads / 64;
+    const int tid = threadIdx.x, lane = gs_lane();
+    const int wave = gs_uniform(tid >> 6);
+    const int cps = 1 << cps_log2;
+    const int nce = nq << cps_log2;  // <= kEmitChunks
+    (void)tid;
+    auto scan4 = [&](int ch, uint32_t vv[4], bool keep[4], uint64_t mk[4]) {
+        const int g = ch >> cps_log2;
+        const int thr = (int)s_thr[g];
+        const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
+        vv[0] = v4.x;
+        vv[1] = v4.y;
+        vv[2] = v4.z;
+        vv[3] = v4.w;
+        uint32_t tot = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            keep[u] = (int32_t)vv[u] >= thr;
+            mk[u] = __ballot(keep[u]);
+            tot += (uint32_t)__popcll(mk[u]);
+        }
+        return tot;
+    };
+    // Pass 1 reads a wave's chunks kEmitReads at a time, so that many LDS reads
+    // are in flight instead of one read-wait-count round trip per chunk; lane g
+    // holds slot g's threshold (a group holds at most 32 queries).
+    {
+        const int thr_l = lane < nq ? (int)s_thr[lane] : 0;
+        for (int c0 = wave; c0 < nce; c0 += NW * kEmitReads) {
+            uint4 v4[kEmitReads];
+#pragma unroll
+            for (int u = 0; u < kEmitReads; ++u) {  // past the end: the last chunk again, not counted
+                const int ch = min(c0 + u * NW, nce - 1);
+                v4[u] = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
+            }
+#pragma unroll
+            for (int u = 0; u < kEmitReads; ++u) {
+                const int ch = c0 + u * NW;
+                if (ch >= nce) break;
+                const int thr = __builtin_amdgcn_readlane(thr_l, ch >> cps_log2);
+                const uint32_t cnt = (uint32_t)__popcll(__ballot((int32_t)v4[u].x >= thr)) +
+                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].y >= thr)) +
+                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].z >= thr)) +
+                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].w >= thr));
+                if (lane == 0) {
+                    s_off[ch] = cnt;
+                    s_ccnt[ch] = cnt;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int g = wave; g < nq; g += NW) {
+        const uint32_t c = lane < cps ? s_off[(g << cps_log2) + lane] : 0u;
+        const uint32_t inc = gs_wave_incl_scan(c);
+        const uint32_t run = (uint32_t)__shfl((int)inc, 63, 64);
+        if (lane < cps) s_off[(g << cps_log2) + lane] = inc - c;
+        if (lane == 0) {
+            s_base[g] = run ? atomicAdd(a.cnt + grp * a.G + g, run) : 0u;
+            s_emit[g] = run;
+            s_maxb[g] = 0;
+        }
+    }
+    __syncthreads();
+    const int my_ch = wave + lane * NW;
+    uint64_t live = __ballot(my_ch < nce && s_ccnt[min(my_ch, kEmitChunks - 1)] != 0);
+    while (live) {
+        const int ch = wave + (__ffsll((unsigned long long)live) - 1) * NW;
+        live &= live - 1;
+        uint32_t vv[4];
+        bool keep[4];
+        uint64_t mk[4];
+        scan4(ch, vv, keep, mk);
+        const int g = ch >> cps_log2;
+        const int d = ((ch & (cps - 1)) << 8) + 4 * lane;
+        const int q = grp * a.G + g;
+        uint32_t base = s_base[g] + s_off[ch];
+        uint32_t mb = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (keep[u]) {
+                const uint32_t slot = base + (uint32_t)__popcll(mk[u] & gs_lanemask_lt());
+                if (slot < (uint32_t)a.cap) {
+                    a.cand_doc[(int64_t)q * a.cap + slot] = (uint32_t)(doc0 + d + u);
+                    a.cand_key[(int64_t)q * a.cap + slot] = vv[u];
+                }
+                const uint32_t b = gs_bin_of((float)vv[u]);
+                atomicAdd(a.hist + (int64_t)q * GS_HIST_BINS + b, 1u);
+                mb = b > mb ? b : mb;
+            }
+            base += (uint32_t)__popcll(mk[u]);
+        }
+        if (mb) atomicMax(&s_maxb[g], mb);  // lanes holding candidates
+    }
+    __syncthreads();
+    // tau is recomputed from the histogram when a slot's candidate count crosses
+    // a multiple of max(k / 8, 64) at or above k; otherwise only the max bin is
+    // published
+    const uint32_t step = (uint32_t)max(a.k >> 3, 64);
+    for (int g = wave; g < nq; g += NW) {
+        const uint32_t e = s_emit[g];
+        if (!e) continue;
+        const int q = grp * a.G + g;
+        const uint32_t c0 = s_base[g], c1 = c0 + e;
+        const bool raise = c1 >= (uint32_t)a.k && (c0 < (uint32_t)a.k || c0 / step != c1 / step);
+        if (!raise) {
+            if (lane == 0) atomicMax(a.maxbin + q, s_maxb[g]);
+            continue;
+        }
+        uint32_t top = 0;
+        if (lane == 0) top = atomicMax(a.maxbin + q, s_maxb[g]);
+        top = __shfl(top, 0, 64);
+        top = top > s_maxb[g] ? top : s_maxb[g];
+        raise_tau(a.tau + q, a.hist + (int64_t)q * GS_HIST_BINS, top, a.k);
+    }
+}
 
 // One workgroup = one doc tile x one query group; the G query slices of the
 // tile live in LDS as int32.  Per batch of union terms, every thread fetches one
@@ -988,16 +1129,9 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
     __builtin_amdgcn_s_setprio(3);
     __syncthreads();
 
-    // ---- emission of candidates >= tau - margin.  The slices are scanned in
-    // 256-doc chunks, 4 docs per lane (one 16-byte LDS read).  Slices are zeroed
-    // whole and docs past n_docs get no adds, so no bound check is needed, and
-    // thr >= 1 makes the signed compare also reject zero and negative sums.
-    // Pass 1 counts each chunk's candidates; one wave per slot scans the slot's
-    // chunk counts (one per lane) and reserves the slot's range with one global
-    // atomic; pass 2 revisits only the chunks holding candidates (a wave reads
-    // its chunk counts at once, one per lane).
+    // ---- emission of candidates >= tau - margin (emit_slices), the seed
+    // launch's thresholds first raised to the slots' local k-th scores
     const int cps_log2 = a.tile_log2 - 8;  // 256-doc chunks per slice = 1 << cps_log2
-    const int cps = 1 << cps_log2;
     const int nce = nq << cps_log2;        // <= kEmitChunks (G * TILE <= kUnionTileLds / 4)
     if (tid < nq) s_thr[tid] = emit_threshold(r_tau, s_mfix[tid]);
     if (a.local_k > 0 && nq <= kLocalSlots) {
@@ -1050,116 +1184,501 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
         if (tid < nq) s_maxb[tid] = 0;
     }
     __syncthreads();
-    auto scan4 = [&](int ch, uint32_t vv[4], bool keep[4], uint64_t mk[4]) {
-        const int g = ch >> cps_log2;
-        const int thr = (int)s_thr[g];
-        const uint4 v4 = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
-        vv[0] = v4.x;
-        vv[1] = v4.y;
-        vv[2] = v4.z;
-        vv[3] = v4.w;
-        uint32_t tot = 0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            keep[u] = (int32_t)vv[u] >= thr;
-            mk[u] = __ballot(keep[u]);
-            tot += (uint32_t)__popcll(mk[u]);
-        }
-        return tot;
-    };
-    // Pass 1 reads a wave's chunks kEmitReads at a time, so that many LDS reads
-    // are in flight instead of one read-wait-count round trip per chunk; lane g
-    // holds slot g's threshold (a group holds at most 32 queries).
-    {
-        const int thr_l = lane < nq ? (int)s_thr[lane] : 0;
-        for (int c0 = wave; c0 < nce; c0 += NW * kEmitReads) {
-            uint4 v4[kEmitReads];
-#pragma unroll
-            for (int u = 0; u < kEmitReads; ++u) {  // past the end: the last chunk again, not counted
-                const int ch = min(c0 + u * NW, nce - 1);
-                v4[u] = *reinterpret_cast<const uint4 *>(acc + ((size_t)ch << 8) + 4 * lane);
-            }
-#pragma unroll
-            for (int u = 0; u < kEmitReads; ++u) {
-                const int ch = c0 + u * NW;
-                if (ch >= nce) break;
-                const int thr = __builtin_amdgcn_readlane(thr_l, ch >> cps_log2);
-                const uint32_t cnt = (uint32_t)__popcll(__ballot((int32_t)v4[u].x >= thr)) +
-                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].y >= thr)) +
-                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].z >= thr)) +
-                                     (uint32_t)__popcll(__ballot((int32_t)v4[u].w >= thr));
-                if (lane == 0) {
-                    s_off[ch] = cnt;
-                    s_ccnt[ch] = cnt;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    for (int g = wave; g < nq; g += NW) {
-        const uint32_t c = lane < cps ? s_off[(g << cps_log2) + lane] : 0u;
-        const uint32_t inc = gs_wave_incl_scan(c);
-        const uint32_t run = (uint32_t)__shfl((int)inc, 63, 64);
-        if (lane < cps) s_off[(g << cps_log2) + lane] = inc - c;
-        if (lane == 0) {
-            s_base[g] = run ? atomicAdd(a.cnt + grp * a.G + g, run) : 0u;
-            s_emit[g] = run;
-            s_maxb[g] = 0;
-        }
-    }
-    __syncthreads();
-    const int my_ch = wave + lane * NW;
-    uint64_t live = __ballot(my_ch < nce && s_ccnt[min(my_ch, kEmitChunks - 1)] != 0);
-    while (live) {
-        const int ch = wave + (__ffsll((unsigned long long)live) - 1) * NW;
-        live &= live - 1;
-        uint32_t vv[4];
-        bool keep[4];
-        uint64_t mk[4];
-        scan4(ch, vv, keep, mk);
-        const int g = ch >> cps_log2;
-        const int d = ((ch & (cps - 1)) << 8) + 4 * lane;
-        const int q = grp * a.G + g;
-        uint32_t base = s_base[g] + s_off[ch];
-        uint32_t mb = 0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (keep[u]) {
-                const uint32_t slot = base + (uint32_t)__popcll(mk[u] & gs_lanemask_lt());
-                if (slot < (uint32_t)a.cap) {
-                    a.cand_doc[(int64_t)q * a.cap + slot] = (uint32_t)(doc0 + d + u);
-                    a.cand_key[(int64_t)q * a.cap + slot] = vv[u];
-                }
-                const uint32_t b = gs_bin_of((float)vv[u]);
-                atomicAdd(a.hist + (int64_t)q * GS_HIST_BINS + b, 1u);
-                mb = b > mb ? b : mb;
-            }
-            base += (uint32_t)__popcll(mk[u]);
-        }
-        if (mb) atomicMax(&s_maxb[g], mb);  // lanes holding candidates
-    }
-    __syncthreads();
-    // tau is recomputed from the histogram when a slot's candidate count crosses
-    // a multiple of max(k / 8, 64) at or above k; otherwise only the max bin is
-    // published
-    const uint32_t step = (uint32_t)max(a.k >> 3, 64);
-    for (int g = wave; g < nq; g += NW) {
-        const uint32_t e = s_emit[g];
-        if (!e) continue;
-        const int q = grp * a.G + g;
-        const uint32_t c0 = s_base[g], c1 = c0 + e;
-        const bool raise = c1 >= (uint32_t)a.k && (c0 < (uint32_t)a.k || c0 / step != c1 / step);
-        if (!raise) {
-            if (lane == 0) atomicMax(a.maxbin + q, s_maxb[g]);
-            continue;
-        }
-        uint32_t top = 0;
-        if (lane == 0) top = atomicMax(a.maxbin + q, s_maxb[g]);
-        top = __shfl(top, 0, 64);
-        top = top > s_maxb[g] ? top : s_maxb[g];
-        raise_tau(a.tau + q, a.hist + (int64_t)q * GS_HIST_BINS, top, a.k);
-    }
+    const EmitArgs ea{a.tau, a.cnt, a.maxbin, a.hist, a.cand_doc, a.cand_key, a.G, a.cap, a.k};
+    emit_slices(ea, acc, nq, cps_log2, doc0, grp, s_thr, s_off, s_ccnt, s_base, s_emit, s_maxb);
     }  // tile
+}
+
+// ---------------------------------------------------------------------- hybrid scoring
+
+// The heavy terms (the index's GS_HEAVY_TERMS longest lists) hold most of the
+// postings a batch scores: at C3 the 64 of them carry 91% of the scored
+// postings, 32 of them 83%.  The hybrid scorer computes their part of every
+// (query, doc) sum as an int8 matrix product on the MFMA units and adds only
+// the other ("tail") terms' postings into the LDS slices.
+//
+// Exactness.  The slices hold the same kind of fixed-point integer sums as
+// k_score_union's: a tail occurrence j adds qi_j * wq (qi_j = rint(q_j 2^f), wq
+// the packed copy's integer weight); a heavy term h adds 2^r a_h wq with a_h =
+// sum over the query's occurrences of h of rint(q_j 2^(f - r)), |a_h| <= 16383
+// (k_query_prep_hybrid picks f and the query's shift r and bounds the error).
+// With a_h = 128 ah + al and wq = 128 wh + wl (al, wl in [0, 127], ah, wh
+// signed bytes):
+//   sum_h a_h wq_h = sum al wl + 2^7 (sum al wh + sum ah wl) + 2^14 sum ah wh,
+// four v_mfma_i32_16x16x64_i8 per 16 queries x 16 docs over the 64 heavy terms,
+// each an exact int32 sum (|.| <= 64 * 128 * 128); the combination is exact in
+// wrapping 32-bit arithmetic because the total fits int32.
+struct HybridArgs {
+    const uint32_t *pk;     // packed scoring copy made for tile_log2 = GS_HYBRID_TILE_LOG2
+    const int64_t *offsets;
+    const int32_t *tb;      // [V][n_tiles + 1]
+    const int8_t *head;     // [n_tiles << tile_log2][2][GS_HEAVY_TERMS]
+    const int8_t *alimb;    // [n_groups * G][2][GS_HEAVY_TERMS] query limbs, slot order
+    const int32_t *hshift;  // [B] r per slot
+    int32_t n_tiles;
+    int32_t B, G, n_groups, ecap;
+    const int32_t *u_term, *u_ebeg, *u_count;  // the groups' tail-term unions (k_group_terms)
+    const uint2 *e_sw;
+    int32_t tile_begin, tiles, tiles_per_wg, per_xcd;
+    uint32_t *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key;
+    const uint32_t *mfix;
+    int32_t cap, k;
+};
+
+constexpr int kHybBatch = kUnionThreads;  // tail terms described in LDS at a time (one per thread)
+constexpr int kHybMapGroups = 512;        // 64-posting groups mapped to their terms per pass
+constexpr int kHybGroups = 4;             // 64-posting groups a wave handles at once (loads in flight)
+constexpr int kHybEnt = 512;              // a group's first (slot, weight) entries staged in LDS
+// LDS of k_score_hybrid besides the slices: per non-empty sub-range of a batch
+// (slot index - position, entry word), per mapped group (start mask, first
+// term), the staged entries
+constexpr size_t kHybMetaLds = (size_t)kHybBatch * 8 + (size_t)kHybMapGroups * 12 + (size_t)kHybEnt * 8;
+constexpr size_t kHybStaticLds = 2048;    // static LDS of k_score_hybrid (1.3 KiB measured)
+static_assert(kUnionTileLds + kHybMetaLds + kHybStaticLds <= kLdsPerWg / 2,
+              "two hybrid workgroups must fit the 160 KiB of LDS of a CU");
+
+typedef int32_t gs_v4i __attribute__((ext_vector_type(4)));
+
+// One workgroup = one run of 512-doc tiles x one group of G = 16 RB queries.
+// Per tile:
+//  1. heavy terms: each wave takes 4 of the tile's 32 blocks of 16 docs and
+//     loads their head rows (lane: doc lane % 16, terms 16 (lane / 16) .. + 15,
+//     both limbs) and the query limbs.  Per block of 16 queries the four MFMAs
+//     run; the combined sums, shifted by the row's r, initialise the slices
+//     (no clearing pass).
+//  2. tail terms, in batches of up to 512 (one per thread; the first batch's
+//     tile bounds are loaded one tile ahead): the non-empty sub-ranges are
+//     numbered densely, their postings consecutively, and each 64-posting group
+//     of that numbering gets its first sub-range and a 64-bit mask of the
+//     sub-ranges starting inside it (written by the sub-ranges' threads).  A
+//     lane's sub-range is then the group's first plus the starts at or before
+//     its position (a popcount); waves take runs of 4 groups round-robin, the
+//     next run's packed words and first entries loaded while the current run's
+//     adds issue.  Each posting is added to every slot holding its term.
+//  3. emission (emit_slices).
+template <int WT, int RB>
+__global__ void __launch_bounds__(kUnionThreads, 4) k_score_hybrid(const HybridArgs a) {
+    constexpr int NW = kUnionThreads / 64;
+    constexpr int G = 16 * RB;
+    constexpr int TL = GS_HYBRID_TILE_LOG2;
+    constexpr int CB = (1 << TL) / 16;  // blocks of 16 docs per tile
+    constexpr int CPW = CB / NW;        // per wave
+    constexpr int SS = TL + 2;          // bytes per slice = 1 << SS
+    constexpr int HT = kHeavyTerms;
+    constexpr int NG = kHybGroups;
+    static_assert(CB % NW == 0 && HT == 64, "tile and heavy-term count fixed by the MFMA shape");
+    static_assert(((size_t)G << SS) <= kUnionTileLds, "slices exceed their LDS");
+
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    __shared__ int32_t s_scl[NW], s_scn[NW];
+    __shared__ int32_t s_hsh[32];
+    __shared__ uint32_t s_thr[32], s_emit[32], s_maxb[32], s_base[32], s_mfix[32];
+    __shared__ uint32_t s_off[kEmitChunks], s_ccnt[kEmitChunks];
+
+    const int tid = threadIdx.x, lane = gs_lane();
+    const int wave = gs_uniform(tid >> 6);
+    const int64_t lin = (int64_t)(blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+    const int n_blk = (a.tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
+    if (lin >= (int64_t)n_blk * a.n_groups) return;
+    const int blk = (int)(lin / a.n_groups);
+    const int grp = (int)(lin % a.n_groups);
+    const int tile_lo = a.tile_begin + blk * a.tiles_per_wg;
+    const int tile_hi = min(tile_lo + a.tiles_per_wg, a.tile_begin + a.tiles);
+    const int nq = min(G, a.B - grp * G);
+
+    uint32_t *acc = reinterpret_cast<uint32_t *>(lds_raw);
+    uint64_t *s_mask = reinterpret_cast<uint64_t *>(lds_raw + ((size_t)G << SS));  // [kHybMapGroups]
+    int32_t *s_first = reinterpret_cast<int32_t *>(s_mask + kHybMapGroups);          // [kHybMapGroups]
+    uint32_t *s_adj = reinterpret_cast<uint32_t *>(s_first + kHybMapGroups);         // slot index - position
+    int32_t *s_ew = reinterpret_cast<int32_t *>(s_adj + kHybBatch);                   // (entries << 16) | first entry
+    uint2 *s_ent = reinterpret_cast<uint2 *>(s_ew + kHybBatch);                       // (slot byte offset, weight)
+
+    if (tid < nq) {
+        s_mfix[tid] = a.mfix[grp * G + tid];
+        s_hsh[tid] = a.hshift[grp * G + tid];
+    }
+    const int U = a.u_count[grp];
+    const int32_t *uterm = a.u_term + (int64_t)grp * a.ecap;
+    const int32_t *uebeg = a.u_ebeg + (int64_t)grp * (a.ecap + 1);
+    const uint2 *esw = a.e_sw + (int64_t)grp * a.ecap;
+    const int64_t row = (int64_t)a.n_tiles + 1;
+    // The group's first kHybEnt entries (in union order: the terms held by the
+    // most slots first, so these cover the terms with more than one entry).
+    for (int x = tid, n = min(uebeg[U], kHybEnt); x < n; x += kUnionThreads) {
+        const uint2 en = esw[x];
+        s_ent[x] = make_uint2(en.x << SS, en.y);
+    }
+    // (the stage addressed from lds_raw itself: through a captured pointer the
+    // compiler loses its address space)
+    constexpr size_t ent_off = ((size_t)G << SS) + (size_t)kHybMapGroups * 12 + (size_t)kHybBatch * 8;
+    auto entry = [&](int x) -> uint2 {
+        if (x < kHybEnt) return reinterpret_cast<const uint2 *>(lds_raw + ent_off)[x];
+        const uint2 en = esw[x];
+        return make_uint2(en.x << SS, en.y);
+    };
+
+    // query limbs (A operand rows 16 rb + lane % 16, terms 16 (lane / 16) .. +
+    // 15) and the head rows of this wave's doc blocks, loaded at each tile's
+    // start (held through the tail phase or the emission they would spill)
+    gs_v4i af[RB][2], bl[CPW], bh[CPW];
+    auto load_head = [&](int tile) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int8_t *ap = a.alimb + (int64_t)(grp * G + 16 * rb + (lane & 15)) * (2 * HT) + (lane >> 4) * 16;
+            af[rb][0] = *reinterpret_cast<const gs_v4i *>(ap);
+            af[rb][1] = *reinterpret_cast<const gs_v4i *>(ap + HT);
+        }
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            const int8_t *hp = a.head + (((int64_t)tile << TL) + (wave + NW * c) * 16 + (lane & 15)) * (2 * HT) +
+                               (lane >> 4) * 16;
+            bl[c] = *reinterpret_cast<const gs_v4i *>(hp);
+            bh[c] = *reinterpret_cast<const gs_v4i *>(hp + HT);
+        }
+    };
+    // the first batch's term of this thread, its bounds one tile ahead
+    int32_t f_t = 0, f_ew = 0, f_lo = 0, f_hi = 0;
+    int64_t f_off = 0;
+    if (tid < min(U, kHybBatch)) {
+        f_t = uterm[tid];
+        f_ew = uebeg[tid];
+        f_off = a.offsets[f_t];
+        f_lo = a.tb[(int64_t)f_t * row + tile_lo];
+        f_hi = a.tb[(int64_t)f_t * row + tile_lo + 1];
+    }
+
+    for (int tile = tile_lo; tile < tile_hi; ++tile) {
+        const int64_t doc0 = (int64_t)tile << TL;
+        uint32_t r_tau = 0;
+        if (tid < nq) r_tau = gs_load_relaxed(a.tau + grp * G + tid);
+        load_head(tile);
+        if (tile > tile_lo) __syncthreads();  // the previous tile's emission is done with the slices
+        // ---- 1. heavy terms
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+            for (int c = 0; c < CPW; ++c) {
+                const int col = (wave + NW * c) * 16 + (lane & 15);
+                const gs_v4i z = {0, 0, 0, 0};
+                const gs_v4i c00 = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rb][0], bl[c], z, 0, 0, 0);
+                gs_v4i cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rb][0], bh[c], z, 0, 0, 0);
+                cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rb][1], bl[c], cm, 0, 0, 0);
+                const gs_v4i c11 = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rb][1], bh[c], z, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * rb + 4 * (lane >> 4) + i;  // slot; rows past nq hold zero limbs
+                    const uint32_t v = ((uint32_t)c00[i] + ((uint32_t)cm[i] << 7) + ((uint32_t)c11[i] << 14))
+                                       << (r < nq ? s_hsh[r] : 0);
+                    acc[(r << TL) + col] = v;
+                }
+            }
+        }
+        __syncthreads();  // slices initialised
+
+        // ---- 2. tail terms
+        for (int b0 = 0; b0 < U; b0 += kHybBatch) {
+            const int nb = min(kHybBatch, U - b0);
+            int t_lo = 0, t_hi = 0;
+            int32_t t_ew = 0;
+            int64_t t_off = 0;
+            if (b0 == 0) {
+                t_lo = f_lo;
+                t_hi = f_hi;
+                t_ew = f_ew;
+                t_off = f_off;
+                if (tid < nb && tile + 1 < tile_hi) {
+                    f_lo = a.tb[(int64_t)f_t * row + tile + 1];
+                    f_hi = a.tb[(int64_t)f_t * row + tile + 2];
+                }
+            } else if (tid < nb) {
+                const int32_t t = uterm[b0 + tid];
+                t_lo = a.tb[(int64_t)t * row + tile];
+                t_hi = a.tb[(int64_t)t * row + tile + 1];
+                t_ew = uebeg[b0 + tid];
+                t_off = a.offsets[t];
+            }
+            const int len = tid < nb ? t_hi - t_lo : 0;
+            const int nz = len > 0 ? 1 : 0;
+            // the first pass's start masks cleared (the previous batch's runs are
+            // past the barrier that ended them)
+            for (int x = tid; x < kHybMapGroups; x += kUnionThreads) s_mask[x] = 0;
+            // exclusive scans: first position of the sub-range, dense index of the non-empty ones
+            int xl = len, xn = nz;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int ol = __shfl_up(xl, d, 64), on = __shfl_up(xn, d, 64);
+                if (lane >= d) {
+                    xl += ol;
+                    xn += on;
+                }
+            }
+            if (lane == 63) {
+                s_scl[wave] = xl;
+                s_scn[wave] = xn;
+            }
+            __syncthreads();
+            int bl_ = 0, bn_ = 0, P = 0;
+            for (int w = 0; w < NW; ++w) {
+                const int l = s_scl[w];
+                bl_ += w < wave ? l : 0;
+                bn_ += w < wave ? s_scn[w] : 0;
+                P += l;
+            }
+            const int pre = bl_ + xl - len, dix = bn_ + xn - nz;
+            if (nz) {
+                s_adj[dix] = (uint32_t)(t_off + t_lo - pre);
+                s_ew[dix] = t_ew;
+            }
+            // passes over kHybMapGroups groups of positions
+            for (int q0 = 0; q0 < P; q0 += kHybMapGroups * 64) {
+                const int q1 = min(P, q0 + kHybMapGroups * 64);
+                const int ng = (q1 - q0 + 63) >> 6;
+                if (q0 > 0) {  // a further pass (more than kHybMapGroups groups): masks cleared again
+                    __syncthreads();  // the previous pass's runs are done with the maps
+                    for (int x = tid; x < ng; x += kUnionThreads) s_mask[x] = 0;
+                    __syncthreads();
+                }
+                if (nz) {
+                    const int a0 = max(pre, q0), a1 = min(pre + len, q1);
+                    // the groups whose first position is one of this sub-range's
+                    for (int u = (a0 - q0 + 63) >> 6; q0 + (u << 6) < a1; ++u) s_first[u] = dix;
+                    if (pre >= q0 && pre < q1)
+                        __hip_atomic_fetch_or(&s_mask[(pre - q0) >> 6], 1ull << ((pre - q0) & 63), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                __syncthreads();  // maps written
+                struct Run {
+                    uint32_t word[NG];
+                    int32_t ew[NG];
+                };
+                auto fetch = [&](int r, Run &k) {
+                    int seg[NG];
+                    bool ok[NG];
+#pragma unroll
+                    for (int g = 0; g < NG; ++g) {
+                        const int u = r * NG + g;
+                        const int uc = min(u, ng - 1);
+                        ok[g] = u < ng && q0 + (u << 6) + lane < q1;
+                        seg[g] = s_first[uc] + __popcll(s_mask[uc] & ((2ull << lane) - 2ull));
+                    }
+#pragma unroll
+                    for (int g = 0; g < NG; ++g) {
+                        const int p = q0 + ((r * NG + g) << 6) + lane;
+                        k.ew[g] = ok[g] ? s_ew[seg[g]] : 0;
+                        const uint32_t slot = s_adj[seg[g]] + (uint32_t)p;
+                        k.word[g] = ok[g] ? a.pk[slot] : 0u;
+                    }
+                };
+                auto apply = [&](const Run &k) {
+                    uint2 en0[NG];  // each posting's first entry, read for the run at once
+#pragma unroll
+                    for (int g = 0; g < NG; ++g) en0[g] = k.ew[g] ? entry(k.ew[g] & 0xFFFF) : make_uint2(0u, 0u);
+#pragma unroll
+                    for (int g = 0; g < NG; ++g) {
+                        const int m = k.ew[g] >> 16;
+                        const int e0 = k.ew[g] & 0xFFFF;
+                        const uint32_t off = k.word[g] & 0xFFFFu;
+                        if (m > 0)
+                            lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + en0[g].x + off),
+                                              packed_contrib<WT>(en0[g].y, k.word[g]));
+                        for (int e = 1; __ballot(e < m); ++e) {
+                            if (e < m) {
+                                const uint2 en = entry(e0 + e);
+                                lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + en.x + off),
+                                                  packed_contrib<WT>(en.y, k.word[g]));
+                            }
+                        }
+                    }
+                };
+                const int n_runs = (ng + NG - 1) / NG;
+                if (wave < n_runs) {
+                    Run ra, rb_;
+                    fetch(wave, ra);
+                    for (int r = wave;; r += 2 * NW) {
+                        if (r + NW < n_runs) fetch(r + NW, rb_);
+                        apply(ra);
+                        if (r + NW >= n_runs) break;
+                        if (r + 2 * NW < n_runs) fetch(r + 2 * NW, ra);
+                        apply(rb_);
+                        if (r + 2 * NW >= n_runs) break;
+                    }
+                }
+            }
+            __syncthreads();  // the batch's descriptors and maps are free again
+        }
+
+        // ---- 3. emission, the next tile's operands in flight
+        if (tid < nq) s_thr[tid] = emit_threshold(r_tau, s_mfix[tid]);
+        __syncthreads();
+        const EmitArgs ea{a.tau, a.cnt, a.maxbin, a.hist, a.cand_doc, a.cand_key, G, a.cap, a.k};
+        emit_slices(ea, acc, nq, TL - 8, doc0, grp, s_thr, s_off, s_ccnt, s_base, s_emit, s_maxb);
+    }
+}
+
+// Query prep of the hybrid scorer: one wave per slot (slots past B get zero
+// limbs).  As k_query_prep, plus the heavy terms' limbs and shift.  Float
+// weights (packed copy, pk_shift = s, W_t = rint(max|w(t)| 2^s)):
+//  * tail occurrence j: qi_j = rint(q_j 2^f), |qi_j| < 2^23 (v_mul_i32_i24);
+//  * heavy term h: a_h = sum over its occurrences of rint(q_j 2^(f - r)),
+//    |a_h| <= 16383 (two limbs), contributing 2^r a_h wq;
+//  * per product the error is <= W_t / 2 + |q| 2^f / 2 (tail) or
+//    2^(r-1) W_t + |q| 2^f / 2 (heavy), so a doc's sum is within
+//    E = Bw_t / 2 + 2^(r-1) Bw_h + Q 2^f / 2 of exact in fixed-point units
+//    (scale 2^(f+s)), and sum |contributions| <= A 2^f + Bw_t / 2 + 2^(r-1) Bw_h,
+//    A = sum_j |q_j| W_j (1 + dup), Bw_* = sum W_j (1 + dup) over tail / heavy
+//    occurrences, Q = sum |q_j| (1 + dup);
+//  * f is the largest exponent keeping that below 2^31 and the tail operands
+//    below 2^23, with r the smallest shift keeping every a_h in range (from
+//    s_h = sum of |q_j| over h's occurrences); the margin is as in k_query_prep.
+// A query without feasible (f, r), or whose limbs do not fit after all, gets
+// mfix = 2^31 - 1 (float; its row is finished by the dense path).
+// uint8: f = r = 0, a_h = sum of the uint8 query weights; beyond 16383 the row
+// gets mfix = 2^31 - 1 (0 otherwise), which k_select_cands sends to the dense
+// path.
+template <int WT>
+__global__ void __launch_bounds__(256)
+    k_query_prep_hybrid(const int32_t *__restrict__ qt, const void *__restrict__ qw, int32_t B, int32_t Bpad, int32_t T,
+                        int32_t V, const float *__restrict__ max_abs, const int32_t *__restrict__ dup,
+                        const int8_t *__restrict__ hrank, int32_t pk_shift, float *__restrict__ scale,
+                        uint32_t *__restrict__ mfix, uint32_t *__restrict__ tau, uint32_t *__restrict__ cnt,
+                        uint32_t *__restrict__ maxbin, int32_t *__restrict__ hshift, int8_t *__restrict__ alimb) {
+    constexpr int HT = kHeavyTerms;
+    __shared__ float s_hs[4][HT];
+    __shared__ int32_t s_hn[4][HT], s_ha[4][HT];
+    const int wv = threadIdx.x >> 6;
+    const int q = (int)((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6);
+    const int lane = gs_lane();
+    if (q >= Bpad) return;
+    s_hs[wv][lane] = 0.0f;
+    s_hn[wv][lane] = 0;
+    s_ha[wv][lane] = 0;
+    gs_wave_sync();
+    int8_t *lim = alimb + (int64_t)q * (2 * HT);
+    if (q >= B) {
+        lim[lane] = 0;
+        lim[HT + lane] = 0;
+        return;
+    }
+    if (lane == 0) {
+        tau[q] = 0;
+        cnt[q] = 0;
+        maxbin[q] = 0;
+    }
+    const int32_t *qrow = qt + (int64_t)q * T;
+    if (WT == GS_W_U8) {
+        const uint8_t *wrow = reinterpret_cast<const uint8_t *>(qw) + (int64_t)q * T;
+        for (int j = lane; j < T; j += 64) {
+            const int32_t t = qrow[j];
+            if ((uint32_t)t >= (uint32_t)V) continue;
+            const int h = hrank[t];
+            if (h >= 0) atomicAdd(&s_ha[wv][h], (int32_t)wrow[j]);
+        }
+        gs_wave_sync();
+        const int32_t av = s_ha[wv][lane];
+        const bool bad = __ballot(av > 16383) != 0;
+        lim[lane] = bad ? 0 : (int8_t)(av & 127);
+        lim[HT + lane] = bad ? 0 : (int8_t)(av >> 7);
+        if (lane == 0) {
+            scale[q] = 1.0f;
+            mfix[q] = bad ? 0x7FFFFFFFu : 0u;
+            hshift[q] = 0;
+        }
+        return;
+    }
+    const float *wrow = reinterpret_cast<const float *>(qw) + (int64_t)q * T;
+    double M = 0.0, n = 0.0, At = 0.0, Ah = 0.0, Bt = 0.0, Bh = 0.0, Q = 0.0, qmax = 0.0, Wmax = 0.0, Whmax = 0.0;
+    for (int j = lane; j < T; j += 64) {
+        const int32_t t = qrow[j];
+        if ((uint32_t)t >= (uint32_t)V) continue;
+        const double m = 1.0 + (double)dup[t];
+        const double aq = fabs((double)wrow[j]);
+        const double W = rint(ldexp((double)max_abs[t], pk_shift));
+        M += aq * (double)max_abs[t] * m;
+        n += m;
+        Q += aq * m;
+        Wmax = fmax(Wmax, W);
+        const int h = hrank[t];
+        if (h >= 0) {
+            Ah += aq * W * m;
+            Bh += W * m;
+            Whmax = fmax(Whmax, W);
+            atomicAdd(&s_hs[wv][h], (float)aq);
+            atomicAdd(&s_hn[wv][h], 1);
+        } else {
+            At += aq * W * m;
+            Bt += W * m;
+            qmax = fmax(qmax, aq);
+        }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        M += __shfl_xor(M, d, 64);
+        n += __shfl_xor(n, d, 64);
+        At += __shfl_xor(At, d, 64);
+        Ah += __shfl_xor(Ah, d, 64);
+        Bt += __shfl_xor(Bt, d, 64);
+        Bh += __shfl_xor(Bh, d, 64);
+        Q += __shfl_xor(Q, d, 64);
+        qmax = fmax(qmax, __shfl_xor(qmax, d, 64));
+        Wmax = fmax(Wmax, __shfl_xor(Wmax, d, 64));
+        Whmax = fmax(Whmax, __shfl_xor(Whmax, d, 64));
+    }
+    gs_wave_sync();
+    // the largest |q| sum and occurrence count over the heavy terms; the fp32
+    // sums are lifted by 1e-5 to cover their rounding (the limbs are checked
+    // exactly below in any case)
+    double smax = (double)s_hs[wv][lane] * (1.0 + 1e-5);
+    int nmax = s_hn[wv][lane];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        smax = fmax(smax, __shfl_xor(smax, d, 64));
+        nmax = max(nmax, __shfl_xor(nmax, d, 64));
+    }
+    M *= 1.0 + 1e-12;  // fp64 rounding of the sums themselves
+    At *= 1.0 + 1e-12;
+    Ah *= 1.0 + 1e-12;
+    Bt *= 1.0 + 1e-12;
+    Bh *= 1.0 + 1e-12;
+    Q *= 1.0 + 1e-12;
+    const double g64 = (2.0 * n + 2.0) * 0x1p-53 / (1.0 - (2.0 * n + 2.0) * 0x1p-53);
+    const double hcap = 16383.0 - 0.5 * nmax;  // a_h <= s_h 2^(f-r) + n_h / 2 <= 16383
+    const double room = 2147483646.0;
+    auto r_of = [&](int f) {  // the smallest r >= 0 keeping smax 2^(f-r) <= hcap
+        int r = 0;
+        while (r < 40 && smax * ldexp(1.0, f - r) > hcap) ++r;
+        return r;
+    };
+    auto fits = [&](int f, int r) {
+        return (At + Ah) * ldexp(1.0, f) + 0.5 * Bt + ldexp(Bh, r - 1) < room &&
+               qmax * ldexp(1.0, f) + 0.5 < 8388608.0 && r <= 30;
+    };
+    int f = 100;
+    if (At + Ah > 0.0) f = (int)floor(log2(room / (At + Ah)));
+    if (qmax > 0.0) f = min(f, (int)floor(log2(8388607.0 / qmax)));
+    f = f > 100 ? 100 : (f < -100 ? -100 : f);
+    int r = r_of(f);
+    while (f > -100 && !fits(f, r)) r = r_of(--f);
+    bool ok = hcap >= 1.0 && Wmax <= 32767.0 && Whmax <= 16383.0 && fits(f, r);
+    // the heavy terms' limbs, exactly as the scorer will use them
+    const float hsc = ldexpf(1.0f, f - r);
+    for (int j = lane; j < T; j += 64) {
+        const int32_t t = qrow[j];
+        if ((uint32_t)t >= (uint32_t)V) continue;
+        const int h = hrank[t];
+        if (h >= 0) atomicAdd(&s_ha[wv][h], (int32_t)rintf(wrow[j] * hsc));
+    }
+    gs_wave_sync();
+    const int32_t av = s_ha[wv][lane];
+    ok = ok && __ballot(av > 16383 || av < -16384) == 0;
+    lim[lane] = ok ? (int8_t)(av & 127) : 0;
+    lim[HT + lane] = ok ? (int8_t)(av >> 7) : 0;
+    if (lane != 0) return;
+    const double Ef = 0.5 * Bt + ldexp(Bh, r - 1) + 0.5 * Q * ldexp(1.0, f);  // fixed-point units
+    double mf = ceil(2.0 * (Ef * (1.0 + 1e-9) + g64 * M * ldexp(1.0, f + pk_shift))) + 2.0;
+    if (!ok || mf > 2147483647.0) mf = 2147483647.0;
+    scale[q] = ldexpf(1.0f, f);
+    mfix[q] = (uint32_t)mf;
+    hshift[q] = ok ? r : 0;
 }
 
 // ---------------------------------------------------------------------- seeding
@@ -1193,7 +1712,8 @@ __global__ void __launch_bounds__(kSelThreads)
     const int q = blockIdx.x;                 // slot
     const int row = perm ? perm[q] : q;       // query: output row
     const uint32_t n = cnt[q];
-    if (n > (uint32_t)cap || n < (uint32_t)k) {
+    // uint8 rows carry mfix 0, or 2^31 - 1 when their heavy-term limbs did not fit (k_query_prep_hybrid)
+    if (n > (uint32_t)cap || n < (uint32_t)k || (!FP && mfix[q] != 0u)) {
         if (threadIdx.x == 0) {
             status[row] = GS_ROW_DENSE;
             if (FP) resc_cnt[q] = 0;
@@ -1614,7 +2134,30 @@ int launch_union(UnionArgs e, hipStream_t s) {
     return GS_OK;
 }
 
+template <int WT>
+int launch_hybrid(HybridArgs h, hipStream_t s) {
+    static std::atomic<bool> attr{false};
+    auto fn = h.G == 16 ? k_score_hybrid<WT, 1> : k_score_hybrid<WT, 2>;
+    if (!attr.load()) {
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_hybrid<WT, 1>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_hybrid<WT, 2>));
+        attr.store(true);
+    }
+    const size_t lds = ((size_t)h.G << (GS_HYBRID_TILE_LOG2 + 2)) + kHybMetaLds;
+    const int64_t total = (int64_t)((h.tiles + h.tiles_per_wg - 1) / h.tiles_per_wg) * h.n_groups;
+    if (total == 0) return GS_OK;
+    h.per_xcd = (int32_t)((total + 7) / 8);
+    const int64_t grid = (int64_t)h.per_xcd * 8;
+    GS_REQUIRE(grid < 0x7FFFFFFFll, "scoring grid too large (%lld workgroups)", (long long)grid);
+    fn<<<(unsigned)grid, kUnionThreads, lds, s>>>(h);
+    GS_CHECK_LAUNCH();
+    return GS_OK;
+}
+
 struct SearchPlan {
+    bool hyb;  // hybrid scorer (heavy terms as int8 matrix products)
+    int8_t *alimb;
+    int32_t *hshift;
     int S, cap, rcap, unroll, G, n_groups, ecap, gt_np, tiles_per_wg;
     int32_t *u_term, *u_ebeg, *u_count;
     uint2 *e_sw;
@@ -1658,21 +2201,38 @@ int default_tiles_per_wg(int tiles, int n_groups) {
     return 1;
 }
 
+int next_pow2_of(int64_t n) {
+    int np = 1;
+    while (np < n) np <<= 1;
+    return np;
+}
+
+// query group of the hybrid scorer: two 16-row MFMA blocks, one for batches of at most 16
+int hybrid_group(int32_t B) { return B <= 16 ? 16 : 32; }
+
+// The hybrid scorer runs when the index carries the heavy terms' dense copy and
+// the packed copy at the hybrid tile size, the caller did not opt out, slot
+// indexes fit 32 bits, and a group's term entries fit the LDS sort.
+bool hybrid_usable(const gs_index *ix, int32_t B, int32_t T, const gs_search_opts *o) {
+    if (!ix->head_d || !ix->head_rank_d || !ix->heavy_d || (o && o->no_hybrid)) return false;
+    if (ix->tile_log2 != GS_HYBRID_TILE_LOG2 || !packed_usable(ix)) return false;
+    if ((uint64_t)ix->n_slots >= (1ull << 32)) return false;
+    return next_pow2_of((int64_t)hybrid_group(B) * T) <= kGroupSortCap;
+}
+
 SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, const gs_search_opts *o,
                        gs_arena &ar) {
     SearchPlan p;
+    p.hyb = hybrid_usable(ix, B, T, o);
     // queries per group: G int32 slices of one tile fill kUnionTileLds; the group's
     // sorted term entries (next_pow2(G * T) of them) must fit the LDS sort
     int G = (int)(kUnionTileLds / 4) >> ix->tile_log2;
     if (G > 32) G = 32;
     if (G < 1) G = 1;
     if (G > B) G = B;
-    auto np_of = [&](int g) {
-        int np = 1;
-        while (np < g * T) np <<= 1;
-        return np;
-    };
+    auto np_of = [&](int g) { return next_pow2_of((int64_t)g * T); };
     while (G > 1 && np_of(G) > kGroupSortCap) G >>= 1;
+    if (p.hyb) G = hybrid_group(B);  // the MFMA rows: slots past B hold zero limbs
     p.G = G;
     p.n_groups = (B + G - 1) / G;
     p.ecap = G * T;
@@ -1683,7 +2243,9 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     const int64_t s_min = std::max<int64_t>(1, kSeedMinDocs >> ix->tile_log2);
     const int64_t s_max = std::max<int64_t>(s_min, kSeedDocs >> ix->tile_log2);
     int64_t s_def = (4ll * k + TILE - 1) >> ix->tile_log2;
-    s_def = std::min<int64_t>(std::max<int64_t>(s_def, s_min), s_max);
+    // (the hybrid scorer has no local thresholds: its seed tiles emit every
+    // positive doc, so small k seeds from fewer docs)
+    s_def = std::min<int64_t>(std::max<int64_t>(s_def, p.hyb ? 1 : s_min), s_max);
     p.S = (o && o->sample_tiles > 0) ? o->sample_tiles : (int)s_def;
     if (p.S > ix->n_tiles) p.S = ix->n_tiles;
     p.cap = (o && o->cand_cap > 0) ? o->cand_cap : kDefaultCandCap;
@@ -1712,6 +2274,12 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.perm = ar.take<int32_t>((size_t)B);
     p.qt_p = ar.take<int32_t>((size_t)B * T);
     p.qw_p = ar.take<float>((size_t)B * T);  // room for fp32 or uint8 query weights
+    p.alimb = nullptr;
+    p.hshift = nullptr;
+    if (p.hyb) {
+        p.alimb = ar.take<int8_t>((size_t)p.n_groups * p.G * 2 * kHeavyTerms);
+        p.hshift = ar.take<int32_t>((size_t)B);
+    }
     return p;
 }
 
@@ -1755,7 +2323,8 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     // them (heavy_d): the queries are copied in slot order and every kernel below
     // works on slots; outputs and status go to the query's own row.
     const int32_t *perm = nullptr;
-    if (ix->heavy_d && !(o && o->batch_order) && p.G > 1 && B > p.G) {
+    // (the hybrid scorer adds the heavy terms densely, so grouping by them saves nothing)
+    if (!p.hyb && ix->heavy_d && !(o && o->batch_order) && p.G > 1 && B > p.G) {
         const int NB = p.G * (1024 / p.G);
         k_group_order<<<(B + NB - 1) / NB, 1024, 0, s>>>(qt, B, T, ix->vocab, ix->heavy_d, p.G, p.perm);
         k_permute_queries<WT><<<gs_blocks((int64_t)B * T, 256, 4096), 256, 0, s>>>(qt, qw, p.perm, B, T, p.qt_p,
@@ -1768,9 +2337,16 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     // the fused scorer reads the packed copy when it was made for this tile size
     const void *pk = packed_usable(ix) ? ix->packed_d : nullptr;
     const int32_t pkf = pk && WT != GS_W_U8 ? 1 : 0;  // integer products of the packed float weights
-    k_query_prep<WT><<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d, ix->dup_d,
-                                                                     pkf, ix->packed_shift, p.scale, p.mfix, p.tau,
-                                                                     p.cnt, p.maxbin);
+    if (p.hyb) {
+        const int32_t Bpad = p.n_groups * p.G;
+        k_query_prep_hybrid<WT><<<gs_blocks((int64_t)Bpad * 64, 256), 256, 0, s>>>(
+            qt, qw, B, Bpad, T, ix->vocab, ix->max_abs_d, ix->dup_d, ix->head_rank_d, ix->packed_shift, p.scale,
+            p.mfix, p.tau, p.cnt, p.maxbin, p.hshift, p.alimb);
+    } else {
+        k_query_prep<WT><<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d,
+                                                                         ix->dup_d, pkf, ix->packed_shift, p.scale,
+                                                                         p.mfix, p.tau, p.cnt, p.maxbin);
+    }
     k_fill<uint32_t><<<gs_blocks((int64_t)B * GS_HIST_BINS, 256, 4096), 256, 0, s>>>(
         p.hist, (int64_t)B * GS_HIST_BINS, 0u);
     GS_CHECK_LAUNCH();
@@ -1781,7 +2357,8 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
             attr.store(true);
         }
         k_group_terms<WT><<<p.n_groups, 1024, (size_t)p.gt_np * 12, s>>>(
-            qt, qw, p.scale, pkf, B, T, ix->vocab, p.G, p.ecap, p.u_term, p.u_ebeg, p.u_count, p.e_sw);
+            qt, qw, p.scale, pkf, B, T, ix->vocab, p.G, p.ecap, p.hyb ? ix->head_rank_d : nullptr, p.u_term,
+            p.u_ebeg, p.u_count, p.e_sw);
         GS_CHECK_LAUNCH();
     }
     if ((rc = phase(1))) return rc;
@@ -1837,15 +2414,49 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
             default: return launch_union<WT, 8>(e, s);
         }
     };
-    e.local_k = k;  // seed launch: local k-th score thresholds
-    if ((rc = run_union(0, p.S))) return rc;
+    HybridArgs h{};
+    if (p.hyb) {
+        h.pk = reinterpret_cast<const uint32_t *>(pk);
+        h.offsets = ix->offsets_d;
+        h.tb = ix->tile_bounds_d;
+        h.head = ix->head_d;
+        h.alimb = p.alimb;
+        h.hshift = p.hshift;
+        h.n_tiles = ix->n_tiles;
+        h.B = B;
+        h.G = p.G;
+        h.n_groups = p.n_groups;
+        h.ecap = p.ecap;
+        h.u_term = p.u_term;
+        h.u_ebeg = p.u_ebeg;
+        h.u_count = p.u_count;
+        h.e_sw = p.e_sw;
+        h.tau = p.tau;
+        h.cnt = p.cnt;
+        h.maxbin = p.maxbin;
+        h.hist = p.hist;
+        h.cand_doc = p.cand_doc;
+        h.cand_key = p.cand_key;
+        h.mfix = p.mfix;
+        h.cap = p.cap;
+        h.k = k;
+    }
+    auto run_scorer = [&](int tile_begin, int tiles) -> int {
+        if (!p.hyb) return run_union(tile_begin, tiles);
+        h.tile_begin = tile_begin;
+        h.tiles = tiles;
+        h.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : default_tiles_per_wg(tiles, p.n_groups);
+        return launch_hybrid<WT>(h, s);
+    };
+    e.local_k = k;  // seed launch: local k-th score thresholds (LDS-add scorer)
+    if ((rc = run_scorer(0, p.S))) return rc;
     e.local_k = 0;
     k_tau_seed<<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(p.tau, p.maxbin, p.hist, B, k);
     GS_CHECK_LAUNCH();
     if ((rc = phase(2))) return rc;
     if (ix->n_tiles > p.S) {
         if (o && o->ev_score_begin) GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_score_begin), s));
-        if ((rc = run_union(p.S, ix->n_tiles - p.S))) return rc;
+        if ((rc = run_scorer(p.S, ix->n_tiles - p.S))) return rc;
         if (o && o->ev_score_end) GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_score_end), s));
     }
     if ((rc = phase(3))) return rc;
@@ -1957,6 +2568,7 @@ extern "C" int gs_search_plan(const gs_index *index, int32_t B, int32_t T, int32
     const int rest = index->n_tiles - p.S;
     out->tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : (rest > 0 ? default_tiles_per_wg(rest, p.n_groups) : 1);
     out->packed = packed_usable(index);
+    out->hybrid = p.hyb;
     return GS_OK;
 }
 

@@ -23,7 +23,7 @@ GS_ROW_DONE, GS_ROW_DENSE = 0, 1
 GS_SEARCH_PHASES = 7
 NOALLOC_SCRATCH_BYTES = 256 << 20   # GS_NOALLOC_SCRATCH_BYTES
 PHASE_NAMES = ("query_prep", "threshold_seed", "scoring", "candidate_select", "fp64_rescore", "final_sort")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 WTYPE_OF_DTYPE = {torch.float32: GS_W_F32, torch.float16: GS_W_F16, torch.uint8: GS_W_U8}
 
@@ -52,9 +52,12 @@ class GsIndex(C.Structure):
         ("packed_tile_log2", C.c_int32),
         ("packed_shift", C.c_int32),
         ("heavy_d", C.c_void_p),
+        ("head_d", C.c_void_p),
+        ("head_rank_d", C.c_void_p),
     ]
 
 HEAVY_TERMS = 64  # GS_HEAVY_TERMS
+HYBRID_TILE_LOG2 = 9  # GS_HYBRID_TILE_LOG2
 
 
 class GsSearchOpts(C.Structure):
@@ -70,6 +73,7 @@ class GsSearchOpts(C.Structure):
         ("tiles_per_wg", C.c_int32),
         ("ev_phases", C.POINTER(C.c_void_p)),
         ("batch_order", C.c_int32),
+        ("no_hybrid", C.c_int32),
     ]
 
 
@@ -103,7 +107,7 @@ class GsSearchPlanInfo(C.Structure):
     """Mirror of ``struct gs_search_plan_info`` in include/gpusparse.h."""
 
     _fields_ = [("seed_tiles", C.c_int32), ("group_size", C.c_int32), ("unroll", C.c_int32),
-                ("tiles_per_wg", C.c_int32), ("packed", C.c_int32)]
+                ("tiles_per_wg", C.c_int32), ("packed", C.c_int32), ("hybrid", C.c_int32)]
 
 
 SIGNATURES = {
@@ -123,6 +127,7 @@ SIGNATURES = {
     "gs_rows_sorted": (C.c_int, [_P, _P, _I64, _P, _P]),
     "gs_pack_shift": (C.c_int, [C.c_float, C.POINTER(C.c_int32)]),
     "gs_heavy_terms": (C.c_int, [_P, _I32, _P, _P]),
+    "gs_head_fill": (C.c_int, [_P, _P, _I32, _P, _P, _I32, _P, _I32, _I64, _I64, _P, _P, _P]),
     "gs_search_workspace": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts),
                                       C.POINTER(_SZ)]),
     "gs_search_plan": (C.c_int, [C.POINTER(GsIndex), _I32, _I32, _I32, C.POINTER(GsSearchOpts),

@@ -32,10 +32,14 @@ DEFAULT_TILE_LOG2_PACKED = 13   # 8192 docs per LDS tile: postings read from the
 
 
 def default_tile_log2(index) -> int:
-    """Doc-tile size (log2) used when a search names none: 8192 docs (the scorer
-    reads one packed word per posting, and its per-tile set-up weighs more than the
-    9-query groups of 4096-doc tiles save)."""
+    """Doc-tile size (log2) of the LDS-add scorer when a search names none: 8192
+    docs (the scorer reads one packed word per posting, and its per-tile set-up
+    weighs more than the 9-query groups of 4096-doc tiles save).  The hybrid
+    scorer always uses 512-doc tiles (HYBRID_TILE_LOG2)."""
     return DEFAULT_TILE_LOG2_PACKED
+
+
+HYBRID_TILE_LOG2 = _lib.HYBRID_TILE_LOG2
 
 
 class CSR(NamedTuple):
@@ -365,7 +369,42 @@ def heavy_terms(index) -> torch.Tensor:
     return out
 
 
-def ensure_search_state(index, tile_log2: int | None = None, forward: bool = True) -> dict:
+def hybrid_eligible(index) -> bool:
+    """Whether the hybrid scorer can serve the index: a packed copy exists (finite
+    weights), the heavy lists hold each doc at most once, and slot indexes fit 32
+    bits.  Reads the heavy lists' duplicate counts once (one host sync)."""
+    a = index.aux()
+    if "hybrid_ok" not in a:
+        ok = int(index.doc_ids.numel()) < (1 << 32) and int(index.num_docs) > 0
+        if ok:
+            if "dup" not in a:
+                require_ascending(index)
+            if "heavy" not in a:
+                a["heavy"] = heavy_terms(index)
+            h = a["heavy"]
+            h = h[h >= 0].long()
+            ok = h.numel() > 0 and int(a["dup"][h].max().item()) == 0 and pack_shift(index) is not None
+        a["hybrid_ok"] = bool(ok)
+    return a["hybrid_ok"]
+
+
+def build_head(index):
+    """Dense copy of the heavy terms' packed integer weights (gs_head_fill): int8
+    [n_tiles * 512][2][64] limbs, and the [vocab] int8 heavy rank of each term."""
+    a = index.aux()
+    dev = _device_of(index)
+    N, V = int(index.num_docs), int(index.vocab_size)
+    n_rows = ((N + (1 << HYBRID_TILE_LOG2) - 1) >> HYBRID_TILE_LOG2) << HYBRID_TILE_LOG2
+    head = torch.empty((n_rows, 2, _lib.HEAVY_TERMS), dtype=torch.int8, device=dev)
+    rank = torch.empty(V, dtype=torch.int8, device=dev)
+    _lib.check(_lib.lib().gs_head_fill(_lib.ptr(index.doc_ids), _lib.ptr(index.scores), index.wtype,
+                                       _lib.ptr(index.offsets), _lib.ptr(index.lengths), V, _lib.ptr(a["heavy"]),
+                                       pack_shift(index), N, n_rows, _lib.ptr(head), _lib.ptr(rank),
+                                       _lib.stream_ptr(dev)), "gs_head_fill")
+    return head, rank
+
+
+def ensure_search_state(index, tile_log2: int | None = None, forward: bool = True, hybrid: bool = False) -> dict:
     """Derived arrays gs_search needs: max |w|, duplicate counts, the most frequent
     terms (query grouping), tile bounds, the
     packed scoring copy for this tile size (skipped when the GPU has no room for it
@@ -373,7 +412,9 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
     same results), and for
     float weights the doc-major copy used by the exact rescoring (skipped when
     `forward` is false or the GPU has no room for it: the rescoring then searches
-    the term lists, with the same results)."""
+    the term lists, with the same results).  With `hybrid` (tile_log2 =
+    HYBRID_TILE_LOG2) also the heavy terms' dense copy (skipped when it does not
+    fit: the search then runs the LDS-add scorer, with the same results)."""
     if tile_log2 is None:
         tile_log2 = default_tile_log2(index)
     a = index.aux()
@@ -404,6 +445,11 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
             a[key] = build_packed(index, tile_log2)
         except torch.cuda.OutOfMemoryError:
             a[key] = None
+    if hybrid and "head" not in a and a.get(("packed", tile_log2)) is not None:
+        try:
+            a["head"] = build_head(index)
+        except torch.cuda.OutOfMemoryError:
+            a["head"] = None
     if forward and "fwd" not in a and index.wtype != _lib.GS_W_U8 and int(index.num_docs) > 0:
         try:
             a["fwd"] = build_forward(index)
@@ -464,10 +510,14 @@ def build_packed(index, tile_log2: int, arrange: bool = True) -> Packed | None:
     return Packed(out, shift)
 
 
-def gs_index_struct(index, tile_log2: int | None = None) -> _lib.GsIndex:
+def gs_index_struct(index, tile_log2: int | None = None, hybrid: bool = False) -> _lib.GsIndex:
+    """The C view of the index for tile_log2; with `hybrid` (tile_log2 must be
+    HYBRID_TILE_LOG2) it carries the heavy terms' dense copy as well."""
     if tile_log2 is None:
         tile_log2 = default_tile_log2(index)
-    a = ensure_search_state(index, tile_log2)
+    if hybrid and tile_log2 != HYBRID_TILE_LOG2:
+        raise ValueError(f"the hybrid scorer uses tile_log2 = {HYBRID_TILE_LOG2}, got {tile_log2}")
+    a = ensure_search_state(index, tile_log2, hybrid=hybrid)
     N = int(index.num_docs)
     s = _lib.GsIndex()
     s.doc_ids_d = index.doc_ids.data_ptr()
@@ -490,6 +540,9 @@ def gs_index_struct(index, tile_log2: int | None = None) -> _lib.GsIndex:
     pk = a.get(("packed", tile_log2))
     if pk is not None:
         s.packed_d, s.packed_tile_log2, s.packed_shift = pk.words.data_ptr(), tile_log2, pk.shift
+    hd = a.get("head") if hybrid else None
+    if hd is not None:
+        s.head_d, s.head_rank_d = hd[0].data_ptr(), hd[1].data_ptr()
     return s
 
 

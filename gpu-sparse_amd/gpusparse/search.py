@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .index import default_tile_log2, gs_index_struct, _device_of
+from .index import HYBRID_TILE_LOG2, default_tile_log2, gs_index_struct, hybrid_eligible, _device_of
 
 MAX_K = 8192  # largest k of the fused path and of compacted_topk; search answers larger k densely
 MAX_T = 8192  # widest query batch of the fused path (terms per query); search answers wider ones densely
@@ -58,6 +58,34 @@ def query_tensors(index, query_batch):
                 raise ValueError("a uint8 index takes uint8 query weights: float weights must be integers in [0, 255]")
         qw = qw.to(want)
     return qt.contiguous(), qw.contiguous()
+
+
+HYBRID_DEFAULT = False  # whether searches that name no scorer take the hybrid one
+
+
+def scorer_choice(index, tile_log2: int | None = None, hybrid: bool | None = None) -> tuple[int, bool]:
+    """(tile_log2, hybrid) of a search.  hybrid=None: the default scorer
+    (HYBRID_DEFAULT: the hybrid scorer -- heavy terms as int8 matrix products --
+    when no tile size is named and the index allows it), else the LDS-add scorer
+    at tile_log2 (default 8192 docs).  hybrid=True requires an eligible index and
+    no other tile size."""
+    if hybrid is None:
+        hybrid = HYBRID_DEFAULT and tile_log2 is None and hybrid_eligible(index)
+    if hybrid:
+        if tile_log2 not in (None, HYBRID_TILE_LOG2):
+            raise ValueError(f"the hybrid scorer uses tile_log2 = {HYBRID_TILE_LOG2}, got {tile_log2}")
+        if not hybrid_eligible(index):
+            raise ValueError("the hybrid scorer needs finite weights, heavy lists without repeated docs "
+                             "and fewer than 2^32 slots")
+        return HYBRID_TILE_LOG2, True
+    return (default_tile_log2(index) if tile_log2 is None else int(tile_log2)), False
+
+
+def _opts(sample_tiles=0, cand_cap=0, unroll=0, waves=0, tiles_per_wg=0, batch_order=False, hybrid=False):
+    o = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, waves, None, None, tiles_per_wg)
+    o.batch_order = int(bool(batch_order))
+    o.no_hybrid = 0 if hybrid else 1
+    return o
 
 
 def _workspace(index, nbytes: int, stream_key: int = 0) -> torch.Tensor:
@@ -136,10 +164,14 @@ class PendingSearch:
 def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, path: str = "auto",
            sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 0, waves: int = 0,
            tiles_per_wg: int = 0, dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None,
-           batch_order: bool = False):
+           batch_order: bool = False, hybrid: bool | None = None):
     """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
 
-    tile_log2: doc-tile size of the scorer (default: index.default_tile_log2).
+    tile_log2, hybrid: the scorer (scorer_choice): by default the hybrid scorer
+    (the index's 64 longest lists as int8 matrix products on 512-doc tiles, the
+    other terms as LDS adds) when the index allows it; a named tile_log2 or
+    hybrid=False selects the LDS-add scorer for every term (default tile:
+    index.default_tile_log2).  Results are the same either way.
     path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense";
     k above MAX_K (8192) or queries wider than MAX_T (8192 terms) always take the
     dense path (any k up to the doc count, any width).
@@ -153,13 +185,14 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     queries sharing frequent terms (same results; for comparisons)."""
     return search_async(index, query_batch, k, tile_log2=tile_log2, path=path, sample_tiles=sample_tiles,
                         cand_cap=cand_cap, unroll=unroll, waves=waves, tiles_per_wg=tiles_per_wg,
-                        dense_budget=dense_budget, timing=timing, batch_order=batch_order).result()
+                        dense_budget=dense_budget, timing=timing, batch_order=batch_order,
+                        hybrid=hybrid).result()
 
 
 def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = None, path: str = "auto",
                  sample_tiles: int = 0, cand_cap: int = 0, unroll: int = 0, waves: int = 0,
                  tiles_per_wg: int = 0, dense_budget: int = DEFAULT_DENSE_BUDGET, timing: dict | None = None,
-                 batch_order: bool = False) -> PendingSearch:
+                 batch_order: bool = False, hybrid: bool | None = None) -> PendingSearch:
     """`search` without waiting: queues the batch on the current stream and
     returns a `PendingSearch` (same arguments and results as `search`).  The host
     can queue the next batch, or post-process the previous one, while this one
@@ -181,9 +214,8 @@ def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = Non
         qt = torch.full((B, 1), -1, dtype=torch.int32, device=dev)
         qw = torch.zeros((B, 1), dtype=qw.dtype, device=dev)
         T = 1
-    if tile_log2 is None:
-        tile_log2 = default_tile_log2(index)
-    gidx = gs_index_struct(index, tile_log2)
+    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid)
+    gidx = gs_index_struct(index, tile_log2, hyb)
     L = _lib.lib()
     acc_bytes = 4 if index.scores.dtype == torch.uint8 else 8
     dense_bytes = B * gidx.n_tiles * (1 << tile_log2) * acc_bytes
@@ -196,8 +228,7 @@ def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = Non
     if use_dense:
         _dense_rows(index, gidx, qt, qw, kk, None, out_s, out_i, max(dense_budget, 1))
         return PendingSearch((out_s, out_i), stream)
-    opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, waves, None, None, tiles_per_wg)
-    opts.batch_order = int(bool(batch_order))
+    opts = _opts(sample_tiles, cand_cap, unroll, waves, tiles_per_wg, batch_order, hyb)
     need = _lib.C.c_size_t()
     _lib.check(L.gs_search_workspace(_lib.C.byref(gidx), B, T, kk, _lib.C.byref(opts), _lib.C.byref(need)),
                "gs_search_workspace")
@@ -262,34 +293,36 @@ def timing_dict(n_calls: int, phases: bool = True) -> dict:
 
 
 def search_plan(index, B: int, T: int, k: int, *, tile_log2: int | None = None, sample_tiles: int = 0,
-                cand_cap: int = 0, unroll: int = 0, tiles_per_wg: int = 0) -> dict:
+                cand_cap: int = 0, unroll: int = 0, tiles_per_wg: int = 0, batch_order: bool = False,
+                hybrid: bool | None = None) -> dict:
     """How the fused path of `search` runs a batch of B queries of width T
     (gs_search_plan): seed tiles, queries per group, postings per lane per chunk,
-    tiles per scoring workgroup and whether the packed copy is read."""
-    if tile_log2 is None:
-        tile_log2 = default_tile_log2(index)
-    gidx = gs_index_struct(index, tile_log2)
-    opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, 0, None, None, tiles_per_wg)
+    tiles per scoring workgroup, whether the packed copy is read and whether the
+    hybrid scorer runs."""
+    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid)
+    gidx = gs_index_struct(index, tile_log2, hyb)
+    opts = _opts(sample_tiles, cand_cap, unroll, 0, tiles_per_wg, batch_order, hyb)
     info = _lib.GsSearchPlanInfo()
     _lib.check(_lib.lib().gs_search_plan(_lib.C.byref(gidx), int(B), int(T), min(int(k), int(index.num_docs)),
                                          _lib.C.byref(opts), _lib.C.byref(info)), "gs_search_plan")
     return {"tile_log2": tile_log2, "seed_tiles": info.seed_tiles, "group_size": info.group_size,
-            "unroll": info.unroll, "tiles_per_wg": info.tiles_per_wg, "packed": bool(info.packed)}
+            "unroll": info.unroll, "tiles_per_wg": info.tiles_per_wg, "packed": bool(info.packed),
+            "hybrid": bool(info.hybrid)}
 
 
 def search_counts(index, B: int, T: int, k: int, *, tile_log2: int | None = None, sample_tiles: int = 0,
-                  cand_cap: int = 0, unroll: int = 0, tiles_per_wg: int = 0):
+                  cand_cap: int = 0, unroll: int = 0, tiles_per_wg: int = 0, batch_order: bool = False,
+                  hybrid: bool | None = None):
     """Per scoring slot of the fused search that last ran with these arguments:
     (docs the scorer emitted as candidates, candidates rescored in fp64), two
     numpy uint32 [B] arrays (gs_search_counts on the index's cached workspace)."""
-    if tile_log2 is None:
-        tile_log2 = default_tile_log2(index)
+    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid)
     ws = index.aux().get("workspace")
     if ws is None:
         raise ValueError("no fused search has run on this index")
     dev = _device_of(index)
-    gidx = gs_index_struct(index, tile_log2)
-    opts = _lib.GsSearchOpts(sample_tiles, cand_cap, unroll, 0, None, None, tiles_per_wg)
+    gidx = gs_index_struct(index, tile_log2, hyb)
+    opts = _opts(sample_tiles, cand_cap, unroll, 0, tiles_per_wg, batch_order, hyb)
     cand = torch.empty(B, dtype=torch.int32, device=dev)
     resc = torch.empty(B, dtype=torch.int32, device=dev)
     _lib.check(_lib.lib().gs_search_counts(_lib.C.byref(gidx), int(B), int(T), min(int(k), int(index.num_docs)),

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 8
+#define GS_ABI_VERSION 9
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -71,7 +71,16 @@ typedef struct gs_index {
     int32_t packed_shift;         /* the w_shift packed_d was made with (float weights) */
     const int32_t *heavy_d;       /* optional [GS_HEAVY_TERMS] most frequent terms (gs_heavy_terms):
                                      gs_search then groups queries that share them; NULL: batch order */
+    const int8_t *head_d;         /* optional dense copy of the heavy terms' weights (gs_head_fill),
+                                     [n_tiles << tile_log2][2][GS_HEAVY_TERMS]: with it (and a packed
+                                     copy for tile_log2 = GS_HYBRID_TILE_LOG2) gs_search runs the hybrid
+                                     scorer -- heavy terms as int8 matrix products, the rest as LDS adds */
+    const int8_t *head_rank_d;    /* [vocab] h for term heavy_d[h], -1 for the others (gs_head_fill) */
 } gs_index;
+
+/* Doc tile of the hybrid scorer: 512 docs, slices of 32 queries (16 for batches
+ * of at most 16 queries). */
+#define GS_HYBRID_TILE_LOG2 9
 
 #define GS_HEAVY_TERMS 64
 
@@ -95,6 +104,7 @@ typedef struct gs_search_opts {
                               rescoring, final sort; may be NULL */
     int32_t batch_order;   /* 1: score queries in groups of consecutive queries even when the
                               index has heavy_d (default 0: group by shared frequent terms) */
+    int32_t no_hybrid;     /* 1: the LDS-add scorer for every term even when the index has head_d */
 } gs_search_opts;
 
 #define GS_SEARCH_PHASES 7
@@ -198,6 +208,19 @@ int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wt
  * lists.  lengths_d int32 [vocab] (gs_index.lengths_d), heavy_d int32
  * [GS_HEAVY_TERMS]. */
 int gs_heavy_terms(const int32_t *lengths_d, int32_t vocab, int32_t *heavy_d, void *stream);
+/* Dense copy of the heavy terms' weights for the hybrid scorer (no counterpart in
+ * the reference: the B operand of gs_search's int8 matrix products).  head_d
+ * int8 [n_rows][2][GS_HEAVY_TERMS], n_rows >= n_docs (the hybrid scorer reads
+ * n_tiles << tile_log2 rows): row d holds, for h < GS_HEAVY_TERMS, the packed
+ * copy's integer weight wq of (d, heavy_d[h]) -- the uint8 weight, or
+ * rint(w * 2^w_shift) clamped to +-32767 -- as two limbs, wq & 127 at [d][0][h]
+ * and wq >> 7 (arithmetic) at [d][1][h]; 0 where doc d lacks the term.  The
+ * heavy lists must hold each doc at most once (gs_check_lists dup = 0) and their
+ * |wq| <= 16383 (w_shift from gs_pack_shift keeps every |wq| <= 8191).
+ * head_rank_d int8 [vocab] <- h for heavy_d[h], -1 for other terms. */
+int gs_head_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, const int64_t *offsets_d,
+                 const int32_t *lengths_d, int32_t vocab, const int32_t *heavy_d, int32_t w_shift,
+                 int64_t n_docs, int64_t n_rows, int8_t *head_d, int8_t *head_rank_d, void *stream);
 /* Weight scale of a packed copy of float weights: the largest `shift` with
  * max_abs * 2^shift <= 8191, for max_abs = the largest |weight| of the index (0 for
  * max_abs == 0).  GS_EINVAL for a negative or non-finite max_abs. */
@@ -228,6 +251,7 @@ typedef struct gs_search_plan_info {
     int32_t unroll;        /* postings per lane per chunk */
     int32_t tiles_per_wg;  /* doc tiles per scoring workgroup after the seed tiles */
     int32_t packed;        /* 1 when the scorer reads the packed copy */
+    int32_t hybrid;        /* 1 when heavy terms are scored as int8 matrix products (head_d) */
 } gs_search_plan_info;
 int gs_search_plan(const gs_index *index, int32_t B, int32_t T, int32_t k, const gs_search_opts *opts,
                    gs_search_plan_info *out);

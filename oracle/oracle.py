@@ -18,6 +18,9 @@ products, exhaustive sorting, closed forms):
   pack_shift             pinned: closed forms at powers of two and scaled cases
   pack_postings          pinned: per-slot decoding + a scalar loop with exact
                          rational rounding (fractions.Fraction, half to even)
+  head_limbs             pinned: 128 * high + low == the packed weight of every
+                         heavy posting, zero cells exactly where a doc lacks the
+                         term, limbs in range, on hand-made and random lists
   scores_f64 / _u32      pinned: dense Q @ D^T (float64 / int64) on small inputs
   scores_f32_sequential  pinned: scalar float32 loop of gpu_scoring.py:246-251
   topk                   pinned: Python sorted() with the same key
@@ -175,6 +178,27 @@ def pack_postings(index: dict, tile_log2: int, shift: int | None = None, arrange
             if hi - lo > 64:
                 src = o + lo + arrange_order(lst[lo:hi])
                 out[o + lo: o + hi] = words[src]
+    return out
+
+
+def head_limbs(index: dict, heavy, n_rows: int, shift: int | None = None) -> np.ndarray:
+    """Dense copy of the heavy terms' packed weights (gs_head_fill; no reference
+    counterpart: the B operand of the hybrid scorer's int8 products), int8
+    [n_rows, 2, len(heavy)]: for h with heavy[h] >= 0 and each posting (d, w) of
+    that list, the packed copy's integer weight wq (pack_postings' weight half)
+    as wq & 127 at [d, 0, h] and wq >> 7 (floor) at [d, 1, h]; zero elsewhere."""
+    words = pack_postings(index, 0, shift, arrange=False).view(np.uint32)
+    out = np.zeros((n_rows, 2, len(heavy)), dtype=np.int8)
+    u8 = index["scores"].dtype == np.uint8
+    for h, t in enumerate(heavy):
+        if t < 0:
+            continue
+        o, L = int(index["offsets"][t]), int(index["lengths"][t])
+        d = index["doc_ids"][o:o + L].astype(np.int64)
+        half = (words[o:o + L] >> 16).astype(np.uint16)
+        wq = half.astype(np.int64) if u8 else half.view(np.int16).astype(np.int64)
+        out[d, 0, h] = (wq & 127).astype(np.int8)
+        out[d, 1, h] = (wq >> 7).astype(np.int8)
     return out
 
 

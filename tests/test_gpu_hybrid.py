@@ -1,0 +1,258 @@
+"""GPU parity of the hybrid scorer: the heavy terms as int8 matrix products
+(MFMA), the other terms as LDS adds, against the CPU oracle.
+
+Same bar as the other search tests: ids and scores bit-identical to the oracle
+(fp64 scatter-add rounded to fp32; exact uint32 sums for uint8 indexes).  The
+cases aim at what the hybrid adds: the dense head copy, the query limbs and
+shift (negative and repeated weights, limbs that do not fit), tail batches and
+their LDS entry stage, groups of 16 and 32 queries with partial groups, tiles
+past the last doc, vocabularies with fewer than 64 terms."""
+import numpy as np
+import pytest
+import torch
+
+import gpusparse as gs
+from gpusparse import synth
+from gpusparse.index import CSR, HYBRID_TILE_LOG2, ensure_search_state
+from helpers import random_csr, random_queries
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_index(csr: CSR):
+    return O.build_index(csr.indptr, csr.indices, csr.data, csr.shape[0], csr.shape[1])
+
+
+def check(ix, ref, ti, tw, k, **opts):
+    """Hybrid search (asserted to run hybrid) equals the oracle bit for bit."""
+    B, T = ti.shape
+    opts = dict(opts, hybrid=True)
+    assert gs.search_plan(ix, B, T, k, **opts)["hybrid"]
+    timing = {}
+    s, i = gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), k, path="fused", timing=timing, **opts)
+    vs, s64, vi = O.c_search(ref, ti, tw, min(k, ix.num_docs), threads=8)
+    s, i = s.cpu().numpy(), i.cpu().numpy()
+    assert np.array_equal(i, vi)
+    assert s.dtype == vs.dtype and np.array_equal(s, vs)
+    if s.dtype == np.float32:
+        # 1e-5, or half an fp32 unit for scores above 2^7 (the scores equal the
+        # fp64 sums rounded to fp32, checked above)
+        tol = np.maximum(1e-5, np.abs(s64) * 2.0 ** -24)
+        assert np.all(np.abs(s.astype(np.float64) - s64) <= tol)
+    return timing
+
+
+def zipf_csr(rng, n_docs, vocab, dtype, max_len=30, s=1.1):
+    """Docs whose term ids follow a Zipf law (a few terms in most docs, like the
+    synthetic configurations), no repeated (doc, term) pairs."""
+    p = 1.0 / np.arange(1, vocab + 1) ** s
+    p /= p.sum()
+    indptr, idx, val = [0], [], []
+    for _ in range(n_docs):
+        n = int(rng.integers(1, max_len + 1))
+        t = rng.choice(vocab, size=min(n, vocab), replace=False, p=p)
+        idx.extend(t.tolist())
+        indptr.append(len(idx))
+        if dtype == np.uint8:
+            val.extend(rng.integers(1, 256, size=len(t)).tolist())
+        else:
+            val.extend(rng.lognormal(-0.5, 0.8, size=len(t)).tolist())
+    return CSR(np.asarray(indptr, np.int64), np.asarray(idx, np.int32), np.asarray(val).astype(dtype),
+               (n_docs, vocab))
+
+
+def zipf_queries(rng, n, vocab, dtype, max_len=25, s=1.1):
+    p = 1.0 / np.arange(1, vocab + 1) ** s
+    p /= p.sum()
+    T = max_len
+    ti = np.full((n, T), -1, np.int32)
+    tw = np.zeros((n, T), dtype)
+    for q in range(n):
+        L = int(rng.integers(1, max_len + 1))
+        ti[q, :L] = rng.choice(vocab, size=L, replace=False, p=p)
+        tw[q, :L] = rng.integers(1, 256, size=L) if dtype == np.uint8 else rng.lognormal(-0.5, 0.8, size=L)
+    return ti, tw
+
+
+# ------------------------------------------------------------------ the dense head copy
+
+
+@pytest.mark.parametrize("dtype,n_docs", [(np.float32, 5000), (np.float16, 1537), (np.uint8, 700)])
+def test_head_copy_matches_oracle(device, dtype, n_docs):
+    """gs_head_fill against oracle.head_limbs, byte for byte, rows up to the
+    last 512-doc tile (zero past the docs), and the heavy-rank table."""
+    from gpusparse.index import build_head
+    rng = np.random.default_rng(n_docs)
+    csr = zipf_csr(rng, n_docs, 400, dtype)
+    if dtype != np.uint8:
+        csr.data[::4] *= -1
+    ix = gs.build_from_csr(csr, device)
+    ensure_search_state(ix, HYBRID_TILE_LOG2)
+    head, rank = build_head(ix)
+    ref = oracle_index(csr)
+    heavy = O.heavy_terms(ref["lengths"])
+    n_rows = ((n_docs + 511) // 512) * 512
+    assert head.shape == (n_rows, 2, 64)
+    assert np.array_equal(head.cpu().numpy(), O.head_limbs(ref, heavy, n_rows))
+    want_rank = np.full(400, -1, np.int8)
+    want_rank[heavy[heavy >= 0]] = np.arange((heavy >= 0).sum())
+    assert np.array_equal(rank.cpu().numpy(), want_rank)
+
+
+# ------------------------------------------------------------------ search
+
+
+@pytest.mark.parametrize("cfg,n_docs", [("C1", 100_000), ("C3", 120_000), ("C5", 120_000), ("C2", 60_001)])
+@pytest.mark.parametrize("B,k", [(1, 10), (16, 1000), (17, 100), (40, 1000)])
+def test_hybrid_synthetic_configs(device, cfg, n_docs, B, k):
+    """The configurations' generators at reduced sizes: batches of 1, 16, 17 and
+    40 queries (groups of 16 and 32, partial last groups), k from 10 to 1000."""
+    c = synth.scaled(synth.CONFIGS[cfg], n_docs=n_docs, n_queries=B)
+    docs, queries = synth.generate(c)
+    ix = gs.build_from_csr(docs, device)
+    ref = oracle_index(docs)
+    ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
+    print(f"hybrid {cfg} n_docs={n_docs} B={B} k={k}", flush=True)
+    check(ix, ref, ti, tw, k)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_hybrid_negative_and_repeated_weights(device, dtype):
+    """Negative doc and query weights (negative limbs), heavy terms repeated in
+    a query with different weights (their rounded weights summed into one
+    limb pair), invalid term ids, an empty query and ties planted by copying docs."""
+    rng = np.random.default_rng(3)
+    csr = zipf_csr(rng, 20000, 500, dtype)
+    csr.data[::3] *= -1
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = zipf_queries(rng, 37, 500, np.float32, max_len=12)
+    tw[::2, :4] *= -1
+    heavy = O.heavy_terms(ref["lengths"])
+    ti = np.ascontiguousarray(np.concatenate([ti, np.tile(heavy[:3], (37, 1)), np.tile(heavy[:2], (37, 1))], axis=1))
+    tw = np.ascontiguousarray(np.concatenate([tw, rng.uniform(-1, 2, (37, 5)).astype(np.float32)], axis=1))
+    ti[5, :] = -1
+    ti[7, 3] = 500 + 7
+    ti[8, 2] = -9
+    for k in (1, 25, 400):
+        print(f"negative/repeated {dtype.__name__} k={k}", flush=True)
+        check(ix, ref, ti, tw, k)
+
+
+def test_hybrid_u8_limbs_too_large_go_dense(device):
+    """uint8: a heavy term repeated 80 times at weight 255 sums to 20400 > 16383,
+    which two limbs cannot hold: those rows are finished by the dense path and
+    the answers stay exact; the other rows stay on the hybrid path."""
+    rng = np.random.default_rng(4)
+    csr = zipf_csr(rng, 9000, 300, np.uint8)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = zipf_queries(rng, 20, 300, np.uint8, max_len=10)
+    h0 = int(O.heavy_terms(ref["lengths"])[0])
+    extra_t = np.full((20, 80), -1, np.int32)
+    extra_w = np.zeros((20, 80), np.uint8)
+    extra_t[::5] = h0
+    extra_w[::5] = 255
+    ti = np.ascontiguousarray(np.concatenate([ti, extra_t], axis=1))
+    tw = np.ascontiguousarray(np.concatenate([tw, extra_w], axis=1))
+    timing = check(ix, ref, ti, tw, 50)
+    assert timing["dense_rows"] == 4
+
+
+@pytest.mark.parametrize("vocab", [20, 64, 70])
+def test_hybrid_small_vocabularies(device, vocab):
+    """Vocabularies of 20 and 64 terms: every term is heavy (no tail term at all;
+    unused heavy slots hold -1); 70: six tail terms."""
+    rng = np.random.default_rng(vocab)
+    csr = zipf_csr(rng, 7000, vocab, np.float32, max_len=min(12, vocab))
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = zipf_queries(rng, 33, vocab, np.float32, max_len=min(9, vocab))
+    for k in (5, 300):
+        print(f"small vocab {vocab} k={k}", flush=True)
+        check(ix, ref, ti, tw, k)
+
+
+def test_hybrid_many_tail_terms_and_large_entry_lists(device):
+    """150 distinct tail terms per query (a group's union spans several LDS
+    batches of 256 terms) and one tail term repeated 30 times in every query
+    (960 (slot, weight) entries per group: more than the LDS stage holds, read
+    from the union instead)."""
+    rng = np.random.default_rng(6)
+    V = 3000
+    csr = zipf_csr(rng, 30000, V, np.float32, max_len=60, s=0.9)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    heavy = set(O.heavy_terms(ref["lengths"]).tolist())
+    tail = np.array([t for t in range(V) if t not in heavy], np.int32)
+    B = 40
+    ti = np.stack([rng.choice(tail, 150, replace=False) for _ in range(B)]).astype(np.int32)
+    rep = int(tail[rng.integers(len(tail))])
+    ti = np.ascontiguousarray(np.concatenate([ti, np.full((B, 30), rep, np.int32)], axis=1))
+    tw = rng.uniform(0.05, 2.0, ti.shape).astype(np.float32)
+    print("many tail terms", flush=True)
+    check(ix, ref, ti, tw, 200)
+
+
+@pytest.mark.parametrize("n_docs", [300, 512, 513, 1100])
+def test_hybrid_tiles_past_the_docs(device, n_docs):
+    """Collections of less than one tile to a little over two: the last tile's
+    head rows past the docs are zero and its docs never become candidates."""
+    rng = np.random.default_rng(n_docs)
+    csr = zipf_csr(rng, n_docs, 200, np.float16, max_len=15)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = zipf_queries(rng, 18, 200, np.float32, max_len=8)
+    for k in (1, min(100, n_docs), n_docs):
+        check(ix, ref, ti, tw, k)
+
+
+@pytest.mark.parametrize("tiles_per_wg,sample_tiles", [(1, 0), (2, 1), (7, 3), (64, 0)])
+def test_hybrid_launch_shapes_and_dirty_workspace(device, tiles_per_wg, sample_tiles):
+    """Several tiles per workgroup, seed launches of 1 and 3 tiles, and a
+    workspace filled with garbage before the call."""
+    rng = np.random.default_rng(tiles_per_wg)
+    csr = zipf_csr(rng, 25000, 800, np.float32)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = zipf_queries(rng, 48, 800, np.float32)
+    check(ix, ref, ti, tw, 60, tiles_per_wg=tiles_per_wg, sample_tiles=sample_tiles)
+    ix.aux()["workspace"].fill_(0xCD)
+    check(ix, ref, ti, tw, 60, tiles_per_wg=tiles_per_wg, sample_tiles=sample_tiles)
+
+
+def test_hybrid_not_used_when_heavy_lists_repeat_docs(device):
+    """An index whose heavy lists repeat a doc cannot hold a single dense cell
+    per (doc, heavy term): hybrid=True raises and the default search runs the
+    LDS-add scorer (same answers)."""
+    rng = np.random.default_rng(8)
+    csr = random_csr(rng, 3000, 30, dup_rate=0.2)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    ti, tw = random_queries(rng, 10, 30, max_len=6)
+    assert not gs.search_plan(ix, 10, ti.shape[1], 20)["hybrid"]
+    s, i = gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), 20, path="fused")
+    vs, _, vi = O.c_search(ref, ti, tw, 20, threads=8)
+    assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+    with pytest.raises(ValueError, match="hybrid"):
+        gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), 20, hybrid=True)
+    with pytest.raises(ValueError, match="tile_log2"):
+        gs.search_plan(ix, 10, ti.shape[1], 20, tile_log2=12, hybrid=True)
+
+
+def test_hybrid_wide_queries_use_groups_that_fit(device):
+    """A group's term entries must fit the LDS sort (8192): 300-term queries
+    run hybrid in groups of 16 (batches of at most 16) and the LDS-add scorer
+    for larger batches, with the same answers."""
+    rng = np.random.default_rng(9)
+    csr = zipf_csr(rng, 8000, 2000, np.float32, max_len=40)
+    ix = gs.build_from_csr(csr, device)
+    ref = oracle_index(csr)
+    ti = np.stack([rng.choice(2000, 300, replace=False) for _ in range(24)]).astype(np.int32)
+    tw = rng.uniform(0.01, 1.0, ti.shape).astype(np.float32)
+    check(ix, ref, ti[:16], tw[:16], 100)
+    assert not gs.search_plan(ix, 24, 300, 100, hybrid=True)["hybrid"]
+    s, i = gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), 100, path="fused", hybrid=True)
+    vs, _, vi = O.c_search(ref, ti, tw, 100, threads=8)
+    assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)

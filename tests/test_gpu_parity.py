@@ -136,13 +136,13 @@ def test_search_without_packed_copy(device, dtype):
     ref = oracle_index(csr)
     ti, tw = random_queries(rng, 24, 60, max_len=9, dtype=np.uint8 if dtype == np.uint8 else np.float32)
     print(f"packed vs plain scorer {dtype.__name__}", flush=True)
-    assert_search_equal(ix, ref, ti, tw, 300, path="fused")
+    assert_search_equal(ix, ref, ti, tw, 300, path="fused", hybrid=False)
     tl = default_tile_log2(ix)
     a = ensure_search_state(ix, tl)
     assert a[("packed", tl)] is not None
     a[("packed", tl)] = None
-    assert_search_equal(ix, ref, ti, tw, 300, path="fused")
-    assert_search_equal(ix, ref, ti, tw, 300, path="fused", unroll=8)
+    assert_search_equal(ix, ref, ti, tw, 300, path="fused", hybrid=False)
+    assert_search_equal(ix, ref, ti, tw, 300, path="fused", unroll=8, hybrid=False)
 
 
 def test_rescoring_without_forward_copy(c1):
@@ -171,7 +171,7 @@ def test_search_with_packed_copy_in_slot_order(c1):
     try:
         assert not torch.equal(a[("packed", tl)].words, saved.words)
         assert torch.equal(torch.sort(a[("packed", tl)].words).values, torch.sort(saved.words).values)
-        assert_search_equal(ix, ref, ti[:64], tw[:64], 100, path="fused")
+        assert_search_equal(ix, ref, ti[:64], tw[:64], 100, path="fused", hybrid=False)
     finally:
         a[("packed", tl)] = saved
 
@@ -298,12 +298,16 @@ def c1(device):
     return ix, oracle_index(docs), ti, tw
 
 
-@pytest.mark.parametrize("path", ["fused", "dense"])
+@pytest.mark.parametrize("path,hybrid", [("fused", True), ("fused", False), ("dense", None)])
 @pytest.mark.parametrize("k", [10, 1000])
-def test_search_c1(c1, path, k):
+def test_search_c1(c1, path, hybrid, k):
+    """The whole C1 batch: the hybrid scorer, the LDS-add scorer for every term,
+    and the dense path."""
     ix, ref, ti, tw = c1
-    print(f"search C1 path={path} k={k}", flush=True)
-    assert_search_equal(ix, ref, ti, tw, k, path=path)
+    print(f"search C1 path={path} hybrid={hybrid} k={k}", flush=True)
+    if path == "fused":
+        assert gs.search_plan(ix, len(ti), ti.shape[1], k, hybrid=hybrid)["hybrid"] == hybrid
+    assert_search_equal(ix, ref, ti, tw, k, path=path, hybrid=hybrid)
 
 
 @pytest.mark.parametrize("tile_log2", [8, 10, 13])
@@ -313,12 +317,13 @@ def test_search_c1_tile_sizes(c1, tile_log2):
     assert_search_equal(ix, ref, ti[:64], tw[:64], 100, path="fused", tile_log2=tile_log2)
 
 
+@pytest.mark.parametrize("hybrid", [True, False])
 @pytest.mark.parametrize("unroll,waves,tiles_per_wg", [(1, 0, 1), (2, 4, 3), (16, 2, 64), (8, 0, 5)])
-def test_search_c1_launch_shapes(c1, unroll, waves, tiles_per_wg):
+def test_search_c1_launch_shapes(c1, unroll, waves, tiles_per_wg, hybrid):
     ix, ref, ti, tw = c1
-    print(f"C1 unroll={unroll} waves={waves} tiles_per_wg={tiles_per_wg}", flush=True)
+    print(f"C1 unroll={unroll} waves={waves} tiles_per_wg={tiles_per_wg} hybrid={hybrid}", flush=True)
     assert_search_equal(ix, ref, ti[:32], tw[:32], 50, path="fused", unroll=unroll, waves=waves,
-                        tiles_per_wg=tiles_per_wg)
+                        tiles_per_wg=tiles_per_wg, hybrid=hybrid)
 
 
 def test_search_dense_fallback_rows(c1):
@@ -451,7 +456,8 @@ def test_rescoring_stops_at_last_valid_term(device, dtype):
     assert_search_equal(ix, ref, ti, tw, 120, path="fused")
 
 
-def test_search_f16_config_reduced(device):
+@pytest.mark.parametrize("hybrid", [True, False])
+def test_search_f16_config_reduced(device, hybrid):
     cfg = synth.scaled(synth.CONFIGS["C3"], n_docs=300_000, n_queries=64)
     docs, queries = synth.generate(cfg)
     ix = gs.build_from_csr(docs, device)
@@ -459,8 +465,8 @@ def test_search_f16_config_reduced(device):
     ref = oracle_index(docs)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
     for k in (10, 1000):
-        print(f"C3 reduced k={k}", flush=True)
-        assert_search_equal(ix, ref, ti, tw, k, path="fused")
+        print(f"C3 reduced k={k} hybrid={hybrid}", flush=True)
+        assert_search_equal(ix, ref, ti, tw, k, path="fused", hybrid=hybrid)
 
 
 @pytest.fixture(scope="module")
@@ -486,15 +492,24 @@ def test_search_packed_launch_shapes(c3_small, unroll, tile_log2, tiles_per_wg):
 
 
 def test_search_plan_reports_defaults(c1, c3_small):
-    """The plan of the default fused search: postings from the packed copy in
-    8192-doc tiles, 16 per lane per chunk; 2 queries per group (64 KiB of LDS)."""
+    """The plans: the hybrid scorer on 512-doc tiles, 32 queries per group (16 for
+    batches of at most 16), postings from the packed copy; the LDS-add scorer
+    (hybrid=False or a named tile size): the packed copy in 8192-doc tiles, 16
+    postings per lane per chunk, 2 queries per group (64 KiB of LDS)."""
     ix32, _, ti, _ = c1
-    p32 = gs.search_plan(ix32, 32, ti.shape[1], 100)
+    h = gs.search_plan(ix32, 32, ti.shape[1], 100, hybrid=True)
+    assert h["hybrid"] and h["tile_log2"] == 9 and h["packed"] and h["group_size"] == 32
+    assert gs.search_plan(ix32, 16, ti.shape[1], 100, hybrid=True)["group_size"] == 16
+    assert gs.search_plan(ix32, 17, ti.shape[1], 100, hybrid=True)["group_size"] == 32
+    assert gs.search_plan(ix32, 32, ti.shape[1], 100)["hybrid"] == gs.search.HYBRID_DEFAULT
+    p32 = gs.search_plan(ix32, 32, ti.shape[1], 100, hybrid=False)
+    assert not p32["hybrid"]
     assert p32["tile_log2"] == 13 and p32["packed"] and p32["unroll"] == 16 and p32["group_size"] == 2
     assert p32["seed_tiles"] >= 1 and p32["tiles_per_wg"] in (1, 2, 3)
-    assert gs.search_plan(ix32, 32, ti.shape[1], 100, tile_log2=12)["group_size"] == 4
+    p12 = gs.search_plan(ix32, 32, ti.shape[1], 100, tile_log2=12)
+    assert p12["group_size"] == 4 and not p12["hybrid"]
     ix16, _, ti16, _ = c3_small
-    p16 = gs.search_plan(ix16, 24, ti16.shape[1], 1000)
+    p16 = gs.search_plan(ix16, 24, ti16.shape[1], 1000, hybrid=False)
     assert p16["tile_log2"] == 13 and p16["packed"] and p16["unroll"] == 16 and p16["group_size"] == 2
     assert gs.search_plan(ix16, 24, ti16.shape[1], 1000, sample_tiles=3, unroll=4)["seed_tiles"] == 3
 
@@ -516,8 +531,8 @@ def test_grouped_queries_equal_batch_order(c3_small, B, k):
     ix, ref, ti, tw = c3_small
     ti, tw = ti[:B], tw[:B]
     print(f"grouped vs batch order B={B} k={k}", flush=True)
-    s0, i0 = assert_search_equal(ix, ref, ti, tw, k, path="fused")
-    s1, i1 = assert_search_equal(ix, ref, ti, tw, k, path="fused", batch_order=True)
+    s0, i0 = assert_search_equal(ix, ref, ti, tw, k, path="fused", hybrid=False)
+    s1, i1 = assert_search_equal(ix, ref, ti, tw, k, path="fused", batch_order=True, hybrid=False)
     assert np.array_equal(i0, i1) and np.array_equal(s0, s1)
 
 
@@ -531,12 +546,13 @@ def test_grouped_queries_many_blocks(device):
     ti, tw = random_queries(rng, 1503, 200, max_len=10)
     ti[::11, 1] = ti[::11, 0]
     print("grouped queries, 1503 queries", flush=True)
-    assert gs.search_plan(ix, 1503, ti.shape[1], 20)["group_size"] == 2
-    assert_search_equal(ix, ref, ti, tw, 20, path="fused")
+    assert gs.search_plan(ix, 1503, ti.shape[1], 20, hybrid=False)["group_size"] == 2
+    assert_search_equal(ix, ref, ti, tw, 20, path="fused", hybrid=False)
 
 
+@pytest.mark.parametrize("hybrid", [True, False])
 @pytest.mark.parametrize("dtype,pattern", [(np.float32, "fine"), (np.float16, "coarse"), (np.float32, "coarse")])
-def test_packed_scores_exact_under_near_ties(device, dtype, pattern):
+def test_packed_scores_exact_under_near_ties(device, dtype, pattern, hybrid):
     """The packed copy holds rounded weights, so many docs share one fixed-point
     score while their fp64 scores differ: 'fine' weights 1 + j 2^-20 all round to
     a few values of the 2^-12 grid; 'coarse' puts one weight of 600 in the index,
@@ -566,13 +582,15 @@ def test_packed_scores_exact_under_near_ties(device, dtype, pattern):
     ti = np.array([[0, 1, 2, 3, 4, 5], [2, 3, 5, -1, -1, -1], [0, 0, 1, 4, -1, -1], [5, 4, 3, 2, 1, 0]], np.int32)
     tw = np.array([[0.7, 1.3, 0.9, 2.1, 0.4, 1.0], [1.0, 1.0, 1.0, 0, 0, 0], [0.5, 0.25, 3.0, 1.0, 0, 0],
                    [1e-3, 2.0, 0.3, 0.3, 7.0, 0.11]], np.float32)
-    print(f"near ties {dtype.__name__} {pattern}", flush=True)
-    assert gs.search_plan(ix, 4, ti.shape[1], 200)["packed"]
+    print(f"near ties {dtype.__name__} {pattern} hybrid={hybrid}", flush=True)
+    plan = gs.search_plan(ix, 4, ti.shape[1], 200, hybrid=hybrid)
+    assert plan["packed"] and plan["hybrid"] == hybrid
     for k in (1, 50, 200):
-        assert_search_equal(ix, ref, ti, tw, k, path="fused")
+        assert_search_equal(ix, ref, ti, tw, k, path="fused", hybrid=hybrid)
 
 
-def test_search_u8_config_reduced(device):
+@pytest.mark.parametrize("hybrid", [True, False])
+def test_search_u8_config_reduced(device, hybrid):
     cfg = synth.scaled(synth.CONFIGS["C5"], n_docs=300_000, n_queries=64)
     docs, queries = synth.generate(cfg)
     ix = gs.build_from_csr(docs, device)
@@ -581,7 +599,8 @@ def test_search_u8_config_reduced(device):
     assert_index_equal(ix, ref)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
     assert tw.dtype == np.uint8
-    assert_search_equal(ix, ref, ti, tw, 1000, path="fused")
+    assert gs.search_plan(ix, len(ti), ti.shape[1], 1000, hybrid=hybrid)["hybrid"] == hybrid
+    assert_search_equal(ix, ref, ti, tw, 1000, path="fused", hybrid=hybrid)
 
 
 @pytest.mark.parametrize("tile_log2", [10, 12, 13])

@@ -132,6 +132,52 @@ def test_pack_shift_closed_forms(max_abs, want):
         O.pack_shift(float("inf"))
 
 
+def test_head_limbs_hand_made():
+    """Two heavy lists: term 1 with weights giving packed values 300, -5, 8191
+    (shift 0 after scaling by hand), term 0 with one posting; limbs by hand:
+    300 = 2 * 128 + 44, -5 = -1 * 128 + 123, 8191 = 63 * 128 + 127."""
+    indptr = np.array([0, 1, 2, 4], np.int64)
+    indices = np.array([1, 1, 1, 0], np.int32)
+    data = np.array([300.0, -5.0, 8191.0, 7.0], np.float32)
+    ix = O.build_index(indptr, indices, data, 3, 4)
+    heavy = O.heavy_terms(ix["lengths"], 4)
+    assert heavy.tolist() == [1, 0, -1, -1]
+    got = O.head_limbs(ix, heavy, 4)
+    assert O.pack_shift(8191.0) == 0
+    want = np.zeros((4, 2, 4), np.int8)
+    want[0, :, 0] = (44, 2)
+    want[1, :, 0] = (123, -1)
+    want[2, :, 0] = (127, 63)
+    want[2, :, 1] = (7, 0)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.uint8])
+def test_head_limbs_recombine_to_packed_weights(dtype):
+    """Random lists: for every heavy posting 128 * high + low equals the packed
+    weight rint(w 2^shift) (computed here from the weights, not from
+    pack_postings), low in [0, 127]; cells of docs lacking a heavy term are zero."""
+    rng = np.random.default_rng(5)
+    csr = random_csr(rng, 3000, 90, dtype=dtype)
+    if dtype != np.uint8:
+        csr.data[::3] *= -1
+    ix = O.build_index(csr.indptr, csr.indices, csr.data, 3000, 90)
+    heavy = O.heavy_terms(ix["lengths"])
+    got = O.head_limbs(ix, heavy, 3072)
+    lo, hi = got[:, 0, :].astype(np.int64), got[:, 1, :].astype(np.int64)
+    assert lo.min() >= 0 and lo.max() <= 127
+    rec = 128 * hi + lo
+    w64 = csr.data.astype(np.float64)
+    shift = 0 if dtype == np.uint8 else O.pack_shift(float(np.abs(w64).max()))
+    want = np.zeros((3072, 64), np.int64)
+    rows = np.repeat(np.arange(3000), np.diff(csr.indptr))
+    col_of = {int(t): h for h, t in enumerate(heavy) if t >= 0}
+    for r, t, w in zip(rows, csr.indices, w64):
+        if int(t) in col_of:
+            want[r, col_of[int(t)]] = int(w) if dtype == np.uint8 else int(np.rint(np.ldexp(w, shift)))
+    assert np.array_equal(rec, want)
+
+
 @pytest.mark.parametrize("tile_log2,dtype", [(12, np.float16), (8, np.uint8), (13, np.float32), (14, np.float16)])
 def test_pack_postings_decodes_and_matches_scalar_loop(tile_log2, dtype):
     from fractions import Fraction
