@@ -416,7 +416,7 @@ def main():
         cand, resc = gs.search_counts(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles,
                                       unroll=a.unroll, tiles_per_wg=a.tiles_per_wg, hybrid=hyb)
         per = np.array([[ev[i].elapsed_time(ev[i + 1]) for i in range(len(ev) - 1)] for ev in timing["phases"]])
-        sel_ms = float(np.median(per[:, 3:6].sum(axis=1)))
+        sel_ms = float(np.median(per[:, 4:7].sum(axis=1)))
         n_cand = int(np.minimum(cand.astype(np.int64), 65536).sum())
         n_resc = int(resc.astype(np.int64).sum())
         row_bytes = 16 + (int(index.lengths.sum().item()) / max(1, int(index.num_docs))) * (4 + wbytes)

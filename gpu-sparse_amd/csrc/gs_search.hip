@@ -44,6 +44,8 @@ namespace {
 using namespace gs;
 
 constexpr int kRescoreCap = 16384;   // candidates rescored per query before the dense fallback
+constexpr int kHeadShift = 16;       // bits of the heavy-term sums dropped in their coarse copy
+constexpr int kHeadBlock = GS_HEAD_BLOCK;  // docs per workgroup of k_head_scores
 constexpr int64_t kSeedMinDocs = 4096;    // fewest docs of the default first tiles scored with tau = 0
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;
@@ -594,6 +596,8 @@ struct UnionArgs {
     const uint32_t *mfix;
     int32_t cap, k;
     int32_t local_k;  // > 0: threshold each slot at its tile's local k-th score too (seed launch)
+    const int16_t *hsc;  // HD: coarse heavy-term sums, block-major (k_head_scores), the slices' start
+    int64_t hsc_ld;      // slots per 512-doc block of hsc
 };
 
 constexpr int kUnionThreads = 512;  // 8 waves; two workgroups per CU
@@ -758,8 +762,10 @@ __device__ __forceinline__ void emit_slices(const EmitArgs &a, const uint32_t *a
 // PK: postings come from the packed scoring copy (gs_pack_postings): one word
 // per posting with the doc's byte offset in a slice and the integer weight,
 // instead of the doc id and weight arrays.
-template <int WT, int UNROLL, bool PK, bool SE>
-__global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArgs a) {
+// HD: the slices start from the coarse heavy-term sums (k_head_scores) instead
+// of zero, and the group's union holds the other terms only.
+template <int WT, int UNROLL, bool PK, bool SE, bool HD>
+__global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const UnionArgs a) {
     using W = gs_weight<WT>;
     using store_t = typename W::store_t;
     using pk_t = uint32_t;
@@ -808,12 +814,50 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
     const store_t *wall = reinterpret_cast<const store_t *>(a.w);
     const pk_t *pkd = reinterpret_cast<const pk_t *>(a.pk);
 
-    // the first tile's slices are zeroed while the term loads are in flight
+    // The first tile's slices are set while the term loads are in flight: zero,
+    // or the coarse heavy-term sums c (int16) as c * 2^kHeadShift.  Those come
+    // as 8-doc (16-byte) pieces of the block-major k_head_scores output, at most
+    // kHeadPieces per thread (G * tile = 16 Ki docs), loaded for the next tile
+    // before the current tile's emission.
+    constexpr int kHeadPieces = (int)(kUnionTileLds / 4 / 8 / kUnionThreads);
+    uint4 hp[HD ? kHeadPieces : 1];
+    auto load_head = [&](int tile) {
+        if constexpr (HD) {
+            const int per_log2 = a.tile_log2 - 3;
+            const int64_t doc0 = (int64_t)tile << a.tile_log2;
+#pragma unroll
+            for (int u = 0; u < kHeadPieces; ++u) {
+                const int i = tid + u * kUnionThreads;
+                if (i < (nq << per_log2)) {
+                    const int g = i >> per_log2;
+                    const int64_t d = doc0 + ((int64_t)(i & ((1 << per_log2) - 1)) << 3);
+                    hp[u] = *reinterpret_cast<const uint4 *>(
+                        a.hsc + ((d / kHeadBlock) * a.hsc_ld + grp * a.G + g) * kHeadBlock + d % kHeadBlock);
+                }
+            }
+        } else {
+            (void)tile;
+        }
+    };
     auto zero_slices = [&]() {
         uint4 *z = reinterpret_cast<uint4 *>(acc);
-        const int n16 = (nq << slice_shift) >> 4;
-        for (int i = tid; i < n16; i += kUnionThreads) z[i] = make_uint4(0, 0, 0, 0);
+        if constexpr (HD) {
+            static_assert(kHeadShift == 16, "slices take the coarse sums' bits in place");
+#pragma unroll
+            for (int u = 0; u < kHeadPieces; ++u) {
+                const int i = tid + u * kUnionThreads;
+                if (i < (nq << (a.tile_log2 - 3))) {
+                    const uint4 v = hp[u];
+                    z[2 * i] = make_uint4(v.x << 16, v.x & 0xFFFF0000u, v.y << 16, v.y & 0xFFFF0000u);
+                    z[2 * i + 1] = make_uint4(v.z << 16, v.z & 0xFFFF0000u, v.w << 16, v.w & 0xFFFF0000u);
+                }
+            }
+        } else {
+            const int n16 = (nq << slice_shift) >> 4;
+            for (int i = tid; i < n16; i += kUnionThreads) z[i] = make_uint4(0, 0, 0, 0);
+        }
     };
+    load_head(tile_lo);
     zero_slices();
 
     // A group whose union fits one batch describes its terms in LDS once (term
@@ -1127,6 +1171,7 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
     // Emission and the next tile's set-up are latency-bound: they issue at the
     // highest priority, ahead of the other workgroup's adds.
     __builtin_amdgcn_s_setprio(3);
+    if (tile + 1 < tile_hi) load_head(tile + 1);
     __syncthreads();
 
     // ---- emission of candidates >= tau - margin (emit_slices), the seed
@@ -1189,334 +1234,120 @@ __global__ void __launch_bounds__(kUnionThreads, 2) k_score_union(const UnionArg
     }  // tile
 }
 
-// ---------------------------------------------------------------------- hybrid scoring
+// ---------------------------------------------------------------------- heavy terms on the MFMA units
 
 // The heavy terms (the index's GS_HEAVY_TERMS longest lists) hold most of the
 // postings a batch scores: at C3 the 64 of them carry 91% of the scored
-// postings, 32 of them 83%.  The hybrid scorer computes their part of every
-// (query, doc) sum as an int8 matrix product on the MFMA units and adds only
-// the other ("tail") terms' postings into the LDS slices.
+// postings, 32 of them 83%.  The hybrid search computes their part of every
+// (query, doc) sum with int8 matrix products (k_head_scores) and starts each
+// LDS slice of k_score_union from it; the slices then take the other ("tail")
+// terms' postings as LDS adds.
 //
-// Exactness.  The slices hold the same kind of fixed-point integer sums as
-// k_score_union's: a tail occurrence j adds qi_j * wq (qi_j = rint(q_j 2^f), wq
-// the packed copy's integer weight); a heavy term h adds 2^r a_h wq with a_h =
-// sum over the query's occurrences of h of rint(q_j 2^(f - r)), |a_h| <= 16383
-// (k_query_prep_hybrid picks f and the query's shift r and bounds the error).
-// With a_h = 128 ah + al and wq = 128 wh + wl (al, wl in [0, 127], ah, wh
-// signed bytes):
+// Exactness.  A tail occurrence j adds qi_j * wq (qi_j = rint(q_j 2^f), wq the
+// packed copy's integer weight), as in the LDS-add search; a heavy term h
+// contributes 2^r a_h wq with a_h = sum over the query's occurrences of h of
+// rint(q_j 2^(f - r)), |a_h| <= 16383 (k_query_prep_hybrid picks f and the
+// query's shift r and bounds the error).  With a_h = 128 ah + al and wq = 128 wh
+// + wl (al, wl in [0, 127], ah, wh signed bytes):
 //   sum_h a_h wq_h = sum al wl + 2^7 (sum al wh + sum ah wl) + 2^14 sum ah wh,
-// four v_mfma_i32_16x16x64_i8 per 16 queries x 16 docs over the 64 heavy terms,
-// each an exact int32 sum (|.| <= 64 * 128 * 128); the combination is exact in
-// wrapping 32-bit arithmetic because the total fits int32.
-struct HybridArgs {
-    const uint32_t *pk;     // packed scoring copy made for tile_log2 = GS_HYBRID_TILE_LOG2
-    const int64_t *offsets;
-    const int32_t *tb;      // [V][n_tiles + 1]
-    const int8_t *head;     // [n_tiles << tile_log2][2][GS_HEAVY_TERMS]
-    const int8_t *alimb;    // [n_groups * G][2][GS_HEAVY_TERMS] query limbs, slot order
-    const int32_t *hshift;  // [B] r per slot
-    int32_t n_tiles;
-    int32_t B, G, n_groups, ecap;
-    const int32_t *u_term, *u_ebeg, *u_count;  // the groups' tail-term unions (k_group_terms)
-    const uint2 *e_sw;
-    int32_t tile_begin, tiles, tiles_per_wg, per_xcd;
-    uint32_t *tau, *cnt, *maxbin, *hist, *cand_doc, *cand_key;
-    const uint32_t *mfix;
-    int32_t cap, k;
-};
+// four v_mfma_i32_16x16x64_i8 per 16 docs x 16 queries over the 64 heavy terms,
+// each an exact int32 sum (|.| <= 64 * 128 * 128); the combination H is exact in
+// wrapping 32-bit arithmetic because it fits int32.  The slices start from
+// floor(H / 2^16) * 2^16, which is below H by less than 2^16: the margin grows
+// by 2^16 (k_query_prep_hybrid), so every doc that can reach the top k is still
+// rescored in fp64, and the answers stay exact.
 
-constexpr int kHybBatch = kUnionThreads;  // tail terms described in LDS at a time (one per thread)
-constexpr int kHybMapGroups = 512;        // 64-posting groups mapped to their terms per pass
-constexpr int kHybGroups = 4;             // 64-posting groups a wave handles at once (loads in flight)
-constexpr int kHybEnt = 512;              // a group's first (slot, weight) entries staged in LDS
-// LDS of k_score_hybrid besides the slices: per non-empty sub-range of a batch
-// (slot index - position, entry word), per mapped group (start mask, first
-// term), the staged entries
-constexpr size_t kHybMetaLds = (size_t)kHybBatch * 8 + (size_t)kHybMapGroups * 12 + (size_t)kHybEnt * 8;
-constexpr size_t kHybStaticLds = 2048;    // static LDS of k_score_hybrid (1.3 KiB measured)
-static_assert(kUnionTileLds + kHybMetaLds + kHybStaticLds <= kLdsPerWg / 2,
-              "two hybrid workgroups must fit the 160 KiB of LDS of a CU");
 
 typedef int32_t gs_v4i __attribute__((ext_vector_type(4)));
 
-// One workgroup = one run of 512-doc tiles x one group of G = 16 RB queries.
-// Per tile:
-//  1. heavy terms: each wave takes 4 of the tile's 32 blocks of 16 docs and
-//     loads their head rows (lane: doc lane % 16, terms 16 (lane / 16) .. + 15,
-//     both limbs) and the query limbs.  Per block of 16 queries the four MFMAs
-//     run; the combined sums, shifted by the row's r, initialise the slices
-//     (no clearing pass).
-//  2. tail terms, in batches of up to 512 (one per thread; the first batch's
-//     tile bounds are loaded one tile ahead): the non-empty sub-ranges are
-//     numbered densely, their postings consecutively, and each 64-posting group
-//     of that numbering gets its first sub-range and a 64-bit mask of the
-//     sub-ranges starting inside it (written by the sub-ranges' threads).  A
-//     lane's sub-range is then the group's first plus the starts at or before
-//     its position (a popcount); waves take runs of 4 groups round-robin, the
-//     next run's packed words and first entries loaded while the current run's
-//     adds issue.  Each posting is added to every slot holding its term.
-//  3. emission (emit_slices).
-template <int WT, int RB>
-__global__ void __launch_bounds__(kUnionThreads, 4) k_score_hybrid(const HybridArgs a) {
-    constexpr int NW = kUnionThreads / 64;
-    constexpr int G = 16 * RB;
-    constexpr int TL = GS_HYBRID_TILE_LOG2;
-    constexpr int CB = (1 << TL) / 16;  // blocks of 16 docs per tile
-    constexpr int CPW = CB / NW;        // per wave
-    constexpr int SS = TL + 2;          // bytes per slice = 1 << SS
+// Coarse heavy-term sums of every (slot, doc): floor(H(s, d) / 2^16) as int16
+// (|H| < 2^31), block-major -- out[(b * Bpad + s) * 512 + (d mod 512)] for doc d
+// of 512-doc block b -- so that each workgroup writes one contiguous run, slots
+// 0..Bpad-1 (slots past B hold zero limbs); blocks past the head rows (docs
+// past the collection) hold zeros.  Eight waves, each holding its 4 blocks of
+// 16 docs as the A operand (lane: doc lane % 16, terms 16 (lane / 16) .. + 15,
+// two limbs) for every block of 16 slots (B operand: the query limbs, same lane
+// layout, loaded one block ahead).  A lane's 4 outputs are 4 consecutive docs
+// of one slot (rows 4 (lane / 16) + i, column lane % 16 of the 16x16 product);
+// they go to an LDS stage of the 16 slots' rows (double-buffered, rows padded
+// so that the 16 rows of a store fall in different banks), which the
+// workgroup then writes out as 16-byte pieces, one contiguous 16 KiB run per
+// block of slots.
+constexpr int kHeadStageRow = kHeadBlock + 16;  // int16 per staged row (bank padding)
+
+__global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ head, int64_t head_rows,
+                                                     const int8_t *__restrict__ alimb,
+                                                     const int32_t *__restrict__ hshift, int32_t B, int32_t Bpad,
+                                                     int16_t *__restrict__ out) {
     constexpr int HT = kHeavyTerms;
-    constexpr int NG = kHybGroups;
-    static_assert(CB % NW == 0 && HT == 64, "tile and heavy-term count fixed by the MFMA shape");
-    static_assert(((size_t)G << SS) <= kUnionTileLds, "slices exceed their LDS");
-
-    extern __shared__ __align__(16) unsigned char lds_raw[];
-    __shared__ int32_t s_scl[NW], s_scn[NW];
-    __shared__ int32_t s_hsh[32];
-    __shared__ uint32_t s_thr[32], s_emit[32], s_maxb[32], s_base[32], s_mfix[32];
-    __shared__ uint32_t s_off[kEmitChunks], s_ccnt[kEmitChunks];
-
-    const int tid = threadIdx.x, lane = gs_lane();
+    constexpr int CPW = kHeadBlock / 16 / 8;  // blocks of 16 docs per wave
+    __shared__ __align__(16) int16_t stage[2][16 * kHeadStageRow];
+    const int lane = gs_lane(), tid = threadIdx.x;
     const int wave = gs_uniform(tid >> 6);
-    const int64_t lin = (int64_t)(blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
-    const int n_blk = (a.tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
-    if (lin >= (int64_t)n_blk * a.n_groups) return;
-    const int blk = (int)(lin / a.n_groups);
-    const int grp = (int)(lin % a.n_groups);
-    const int tile_lo = a.tile_begin + blk * a.tiles_per_wg;
-    const int tile_hi = min(tile_lo + a.tiles_per_wg, a.tile_begin + a.tiles);
-    const int nq = min(G, a.B - grp * G);
-
-    uint32_t *acc = reinterpret_cast<uint32_t *>(lds_raw);
-    uint64_t *s_mask = reinterpret_cast<uint64_t *>(lds_raw + ((size_t)G << SS));  // [kHybMapGroups]
-    int32_t *s_first = reinterpret_cast<int32_t *>(s_mask + kHybMapGroups);          // [kHybMapGroups]
-    uint32_t *s_adj = reinterpret_cast<uint32_t *>(s_first + kHybMapGroups);         // slot index - position
-    int32_t *s_ew = reinterpret_cast<int32_t *>(s_adj + kHybBatch);                   // (entries << 16) | first entry
-    uint2 *s_ent = reinterpret_cast<uint2 *>(s_ew + kHybBatch);                       // (slot byte offset, weight)
-
-    if (tid < nq) {
-        s_mfix[tid] = a.mfix[grp * G + tid];
-        s_hsh[tid] = a.hshift[grp * G + tid];
+    const int64_t doc0 = (int64_t)blockIdx.x * kHeadBlock;
+    int16_t *ob = out + (int64_t)blockIdx.x * Bpad * kHeadBlock;
+    if (doc0 >= head_rows) {  // docs past the collection
+        for (int64_t i = tid; i < (int64_t)Bpad * kHeadBlock / 8; i += blockDim.x)
+            reinterpret_cast<uint4 *>(ob)[i] = make_uint4(0, 0, 0, 0);
+        return;
     }
-    const int U = a.u_count[grp];
-    const int32_t *uterm = a.u_term + (int64_t)grp * a.ecap;
-    const int32_t *uebeg = a.u_ebeg + (int64_t)grp * (a.ecap + 1);
-    const uint2 *esw = a.e_sw + (int64_t)grp * a.ecap;
-    const int64_t row = (int64_t)a.n_tiles + 1;
-    // The group's first kHybEnt entries (in union order: the terms held by the
-    // most slots first, so these cover the terms with more than one entry).
-    for (int x = tid, n = min(uebeg[U], kHybEnt); x < n; x += kUnionThreads) {
-        const uint2 en = esw[x];
-        s_ent[x] = make_uint2(en.x << SS, en.y);
-    }
-    // (the stage addressed from lds_raw itself: through a captured pointer the
-    // compiler loses its address space)
-    constexpr size_t ent_off = ((size_t)G << SS) + (size_t)kHybMapGroups * 12 + (size_t)kHybBatch * 8;
-    auto entry = [&](int x) -> uint2 {
-        if (x < kHybEnt) return reinterpret_cast<const uint2 *>(lds_raw + ent_off)[x];
-        const uint2 en = esw[x];
-        return make_uint2(en.x << SS, en.y);
-    };
-
-    // query limbs (A operand rows 16 rb + lane % 16, terms 16 (lane / 16) .. +
-    // 15) and the head rows of this wave's doc blocks, loaded at each tile's
-    // start (held through the tail phase or the emission they would spill)
-    gs_v4i af[RB][2], bl[CPW], bh[CPW];
-    auto load_head = [&](int tile) {
+    gs_v4i dl[CPW], dh[CPW];
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const int8_t *ap = a.alimb + (int64_t)(grp * G + 16 * rb + (lane & 15)) * (2 * HT) + (lane >> 4) * 16;
-            af[rb][0] = *reinterpret_cast<const gs_v4i *>(ap);
-            af[rb][1] = *reinterpret_cast<const gs_v4i *>(ap + HT);
-        }
+    for (int c = 0; c < CPW; ++c) {
+        const int8_t *hp = head + (doc0 + (wave * CPW + c) * 16 + (lane & 15)) * (2 * HT) + (lane >> 4) * 16;
+        dl[c] = *reinterpret_cast<const gs_v4i *>(hp);
+        dh[c] = *reinterpret_cast<const gs_v4i *>(hp + HT);
+    }
+    auto load_q = [&](int rb, gs_v4i &ql, gs_v4i &qh, int &r) {
+        const int s = rb + (lane & 15);
+        const int8_t *ap = alimb + (int64_t)s * (2 * HT) + (lane >> 4) * 16;
+        ql = *reinterpret_cast<const gs_v4i *>(ap);
+        qh = *reinterpret_cast<const gs_v4i *>(ap + HT);
+        r = s < B ? hshift[s] : 0;
+    };
+    gs_v4i ql, qh;
+    int r;
+    load_q(0, ql, qh, r);
+    for (int rb = 0, buf = 0; rb < Bpad; rb += 16, buf ^= 1) {
+        gs_v4i nl = ql, nh = qh;
+        int nr = r;
+        if (rb + 16 < Bpad) load_q(rb + 16, nl, nh, nr);
+        int16_t *st = stage[buf];
 #pragma unroll
         for (int c = 0; c < CPW; ++c) {
-            const int8_t *hp = a.head + (((int64_t)tile << TL) + (wave + NW * c) * 16 + (lane & 15)) * (2 * HT) +
-                               (lane >> 4) * 16;
-            bl[c] = *reinterpret_cast<const gs_v4i *>(hp);
-            bh[c] = *reinterpret_cast<const gs_v4i *>(hp + HT);
+            const gs_v4i z = {0, 0, 0, 0};
+            const gs_v4i c00 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dl[c], ql, z, 0, 0, 0);
+            gs_v4i cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(dh[c], ql, z, 0, 0, 0);
+            cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(dl[c], qh, cm, 0, 0, 0);
+            const gs_v4i c11 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dh[c], qh, z, 0, 0, 0);
+            uint32_t w[2];
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+                const uint32_t h0 = ((uint32_t)c00[i] + ((uint32_t)cm[i] << 7) + ((uint32_t)c11[i] << 14)) << r;
+                const uint32_t h1 =
+                    ((uint32_t)c00[i + 1] + ((uint32_t)cm[i + 1] << 7) + ((uint32_t)c11[i + 1] << 14)) << r;
+                w[i >> 1] = ((uint32_t)((int32_t)h0 >> kHeadShift) & 0xFFFFu) |
+                            ((uint32_t)((int32_t)h1 >> kHeadShift) << 16);
+            }
+            const int d = (wave * CPW + c) * 16 + 4 * (lane >> 4);
+            *reinterpret_cast<uint2 *>(st + (lane & 15) * kHeadStageRow + d) = make_uint2(w[0], w[1]);
         }
-    };
-    // the first batch's term of this thread, its bounds one tile ahead
-    int32_t f_t = 0, f_ew = 0, f_lo = 0, f_hi = 0;
-    int64_t f_off = 0;
-    if (tid < min(U, kHybBatch)) {
-        f_t = uterm[tid];
-        f_ew = uebeg[tid];
-        f_off = a.offsets[f_t];
-        f_lo = a.tb[(int64_t)f_t * row + tile_lo];
-        f_hi = a.tb[(int64_t)f_t * row + tile_lo + 1];
-    }
-
-    for (int tile = tile_lo; tile < tile_hi; ++tile) {
-        const int64_t doc0 = (int64_t)tile << TL;
-        uint32_t r_tau = 0;
-        if (tid < nq) r_tau = gs_load_relaxed(a.tau + grp * G + tid);
-        load_head(tile);
-        if (tile > tile_lo) __syncthreads();  // the previous tile's emission is done with the slices
-        // ---- 1. heavy terms
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-            for (int c = 0; c < CPW; ++c) {
-                const int col = (wave + NW * c) * 16 + (lane & 15);
-                const gs_v4i z = {0, 0, 0, 0};
-                const gs_v4i c00 = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rb][0], bl[c], z, 0, 0, 0);
-                gs_v4i cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rb][0], bh[c], z, 0, 0, 0);
-                cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rb][1], bl[c], cm, 0, 0, 0);
-                const gs_v4i c11 = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[rb][1], bh[c], z, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 16 * rb + 4 * (lane >> 4) + i;  // slot; rows past nq hold zero limbs
-                    const uint32_t v = ((uint32_t)c00[i] + ((uint32_t)cm[i] << 7) + ((uint32_t)c11[i] << 14))
-                                       << (r < nq ? s_hsh[r] : 0);
-                    acc[(r << TL) + col] = v;
-                }
-            }
-        }
-        __syncthreads();  // slices initialised
-
-        // ---- 2. tail terms
-        for (int b0 = 0; b0 < U; b0 += kHybBatch) {
-            const int nb = min(kHybBatch, U - b0);
-            int t_lo = 0, t_hi = 0;
-            int32_t t_ew = 0;
-            int64_t t_off = 0;
-            if (b0 == 0) {
-                t_lo = f_lo;
-                t_hi = f_hi;
-                t_ew = f_ew;
-                t_off = f_off;
-                if (tid < nb && tile + 1 < tile_hi) {
-                    f_lo = a.tb[(int64_t)f_t * row + tile + 1];
-                    f_hi = a.tb[(int64_t)f_t * row + tile + 2];
-                }
-            } else if (tid < nb) {
-                const int32_t t = uterm[b0 + tid];
-                t_lo = a.tb[(int64_t)t * row + tile];
-                t_hi = a.tb[(int64_t)t * row + tile + 1];
-                t_ew = uebeg[b0 + tid];
-                t_off = a.offsets[t];
-            }
-            const int len = tid < nb ? t_hi - t_lo : 0;
-            const int nz = len > 0 ? 1 : 0;
-            // the first pass's start masks cleared (the previous batch's runs are
-            // past the barrier that ended them)
-            for (int x = tid; x < kHybMapGroups; x += kUnionThreads) s_mask[x] = 0;
-            // exclusive scans: first position of the sub-range, dense index of the non-empty ones
-            int xl = len, xn = nz;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const int ol = __shfl_up(xl, d, 64), on = __shfl_up(xn, d, 64);
-                if (lane >= d) {
-                    xl += ol;
-                    xn += on;
-                }
-            }
-            if (lane == 63) {
-                s_scl[wave] = xl;
-                s_scn[wave] = xn;
-            }
-            __syncthreads();
-            int bl_ = 0, bn_ = 0, P = 0;
-            for (int w = 0; w < NW; ++w) {
-                const int l = s_scl[w];
-                bl_ += w < wave ? l : 0;
-                bn_ += w < wave ? s_scn[w] : 0;
-                P += l;
-            }
-            const int pre = bl_ + xl - len, dix = bn_ + xn - nz;
-            if (nz) {
-                s_adj[dix] = (uint32_t)(t_off + t_lo - pre);
-                s_ew[dix] = t_ew;
-            }
-            // passes over kHybMapGroups groups of positions
-            for (int q0 = 0; q0 < P; q0 += kHybMapGroups * 64) {
-                const int q1 = min(P, q0 + kHybMapGroups * 64);
-                const int ng = (q1 - q0 + 63) >> 6;
-                if (q0 > 0) {  // a further pass (more than kHybMapGroups groups): masks cleared again
-                    __syncthreads();  // the previous pass's runs are done with the maps
-                    for (int x = tid; x < ng; x += kUnionThreads) s_mask[x] = 0;
-                    __syncthreads();
-                }
-                if (nz) {
-                    const int a0 = max(pre, q0), a1 = min(pre + len, q1);
-                    // the groups whose first position is one of this sub-range's
-                    for (int u = (a0 - q0 + 63) >> 6; q0 + (u << 6) < a1; ++u) s_first[u] = dix;
-                    if (pre >= q0 && pre < q1)
-                        __hip_atomic_fetch_or(&s_mask[(pre - q0) >> 6], 1ull << ((pre - q0) & 63), __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
-                __syncthreads();  // maps written
-                struct Run {
-                    uint32_t word[NG];
-                    int32_t ew[NG];
-                };
-                auto fetch = [&](int r, Run &k) {
-                    int seg[NG];
-                    bool ok[NG];
-#pragma unroll
-                    for (int g = 0; g < NG; ++g) {
-                        const int u = r * NG + g;
-                        const int uc = min(u, ng - 1);
-                        ok[g] = u < ng && q0 + (u << 6) + lane < q1;
-                        seg[g] = s_first[uc] + __popcll(s_mask[uc] & ((2ull << lane) - 2ull));
-                    }
-#pragma unroll
-                    for (int g = 0; g < NG; ++g) {
-                        const int p = q0 + ((r * NG + g) << 6) + lane;
-                        k.ew[g] = ok[g] ? s_ew[seg[g]] : 0;
-                        const uint32_t slot = s_adj[seg[g]] + (uint32_t)p;
-                        k.word[g] = ok[g] ? a.pk[slot] : 0u;
-                    }
-                };
-                auto apply = [&](const Run &k) {
-                    uint2 en0[NG];  // each posting's first entry, read for the run at once
-#pragma unroll
-                    for (int g = 0; g < NG; ++g) en0[g] = k.ew[g] ? entry(k.ew[g] & 0xFFFF) : make_uint2(0u, 0u);
-#pragma unroll
-                    for (int g = 0; g < NG; ++g) {
-                        const int m = k.ew[g] >> 16;
-                        const int e0 = k.ew[g] & 0xFFFF;
-                        const uint32_t off = k.word[g] & 0xFFFFu;
-                        if (m > 0)
-                            lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + en0[g].x + off),
-                                              packed_contrib<WT>(en0[g].y, k.word[g]));
-                        for (int e = 1; __ballot(e < m); ++e) {
-                            if (e < m) {
-                                const uint2 en = entry(e0 + e);
-                                lds_add<uint32_t>(reinterpret_cast<uint32_t *>(lds_raw + en.x + off),
-                                                  packed_contrib<WT>(en.y, k.word[g]));
-                            }
-                        }
-                    }
-                };
-                const int n_runs = (ng + NG - 1) / NG;
-                if (wave < n_runs) {
-                    Run ra, rb_;
-                    fetch(wave, ra);
-                    for (int r = wave;; r += 2 * NW) {
-                        if (r + NW < n_runs) fetch(r + NW, rb_);
-                        apply(ra);
-                        if (r + NW >= n_runs) break;
-                        if (r + 2 * NW < n_runs) fetch(r + 2 * NW, ra);
-                        apply(rb_);
-                        if (r + 2 * NW >= n_runs) break;
-                    }
-                }
-            }
-            __syncthreads();  // the batch's descriptors and maps are free again
-        }
-
-        // ---- 3. emission, the next tile's operands in flight
-        if (tid < nq) s_thr[tid] = emit_threshold(r_tau, s_mfix[tid]);
+        // the stage is complete; the other one's copy-out (one block back) ended
+        // before any wave got here, since it precedes this barrier in every wave
         __syncthreads();
-        const EmitArgs ea{a.tau, a.cnt, a.maxbin, a.hist, a.cand_doc, a.cand_key, G, a.cap, a.k};
-        emit_slices(ea, acc, nq, TL - 8, doc0, grp, s_thr, s_off, s_ccnt, s_base, s_emit, s_maxb);
+        for (int i = tid; i < 16 * kHeadBlock / 8; i += blockDim.x) {
+            const int row = i / (kHeadBlock / 8), col = (i % (kHeadBlock / 8)) * 8;
+            reinterpret_cast<uint4 *>(ob + (int64_t)(rb + row) * kHeadBlock)[col / 8] =
+                *reinterpret_cast<const uint4 *>(st + row * kHeadStageRow + col);
+        }
+        ql = nl;
+        qh = nh;
+        r = nr;
     }
 }
 
-// Query prep of the hybrid scorer: one wave per slot (slots past B get zero
-// limbs).  As k_query_prep, plus the heavy terms' limbs and shift.  Float
+// Query prep of the hybrid search: one wave per slot (slots past B, up to the
+// multiple of 16, get zero limbs).  As k_query_prep, plus the heavy terms' limbs and shift.  Float
 // weights (packed copy, pk_shift = s, W_t = rint(max|w(t)| 2^s)):
 //  * tail occurrence j: qi_j = rint(q_j 2^f), |qi_j| < 2^23 (v_mul_i32_i24);
 //  * heavy term h: a_h = sum over its occurrences of rint(q_j 2^(f - r)),
@@ -1529,12 +1360,11 @@ __global__ void __launch_bounds__(kUnionThreads, 4) k_score_hybrid(const HybridA
 //    occurrences, Q = sum |q_j| (1 + dup);
 //  * f is the largest exponent keeping that below 2^31 and the tail operands
 //    below 2^23, with r the smallest shift keeping every a_h in range (from
-//    s_h = sum of |q_j| over h's occurrences); the margin is as in k_query_prep.
+//    s_h = sum of |q_j| over h's occurrences); the margin is k_query_prep's for
+//    this E, plus 2^kHeadShift for the coarse heavy-term start of the slices.
 // A query without feasible (f, r), or whose limbs do not fit after all, gets
 // mfix = 2^31 - 1 (float; its row is finished by the dense path).
-// uint8: f = r = 0, a_h = sum of the uint8 query weights; beyond 16383 the row
-// gets mfix = 2^31 - 1 (0 otherwise), which k_select_cands sends to the dense
-// path.
+// Float weights only (uint8 sums are exact as accumulated and not rescored).
 template <int WT>
 __global__ void __launch_bounds__(256)
     k_query_prep_hybrid(const int32_t *__restrict__ qt, const void *__restrict__ qw, int32_t B, int32_t Bpad, int32_t T,
@@ -1564,27 +1394,8 @@ __global__ void __launch_bounds__(256)
         cnt[q] = 0;
         maxbin[q] = 0;
     }
+    static_assert(WT != GS_W_U8, "float weights only");
     const int32_t *qrow = qt + (int64_t)q * T;
-    if (WT == GS_W_U8) {
-        const uint8_t *wrow = reinterpret_cast<const uint8_t *>(qw) + (int64_t)q * T;
-        for (int j = lane; j < T; j += 64) {
-            const int32_t t = qrow[j];
-            if ((uint32_t)t >= (uint32_t)V) continue;
-            const int h = hrank[t];
-            if (h >= 0) atomicAdd(&s_ha[wv][h], (int32_t)wrow[j]);
-        }
-        gs_wave_sync();
-        const int32_t av = s_ha[wv][lane];
-        const bool bad = __ballot(av > 16383) != 0;
-        lim[lane] = bad ? 0 : (int8_t)(av & 127);
-        lim[HT + lane] = bad ? 0 : (int8_t)(av >> 7);
-        if (lane == 0) {
-            scale[q] = 1.0f;
-            mfix[q] = bad ? 0x7FFFFFFFu : 0u;
-            hshift[q] = 0;
-        }
-        return;
-    }
     const float *wrow = reinterpret_cast<const float *>(qw) + (int64_t)q * T;
     double M = 0.0, n = 0.0, At = 0.0, Ah = 0.0, Bt = 0.0, Bh = 0.0, Q = 0.0, qmax = 0.0, Wmax = 0.0, Whmax = 0.0;
     for (int j = lane; j < T; j += 64) {
@@ -1674,7 +1485,9 @@ __global__ void __launch_bounds__(256)
     lim[HT + lane] = ok ? (int8_t)(av >> 7) : 0;
     if (lane != 0) return;
     const double Ef = 0.5 * Bt + ldexp(Bh, r - 1) + 0.5 * Q * ldexp(1.0, f);  // fixed-point units
-    double mf = ceil(2.0 * (Ef * (1.0 + 1e-9) + g64 * M * ldexp(1.0, f + pk_shift))) + 2.0;
+    // + 2^kHeadShift: the slices start from the heavy-term sums rounded down to a
+    // multiple of it (one-sided, k_head_scores)
+    double mf = ceil(2.0 * (Ef * (1.0 + 1e-9) + g64 * M * ldexp(1.0, f + pk_shift))) + 2.0 + ldexp(1.0, kHeadShift);
     if (!ok || mf > 2147483647.0) mf = 2147483647.0;
     scale[q] = ldexpf(1.0f, f);
     mfix[q] = (uint32_t)mf;
@@ -1712,8 +1525,7 @@ __global__ void __launch_bounds__(kSelThreads)
     const int q = blockIdx.x;                 // slot
     const int row = perm ? perm[q] : q;       // query: output row
     const uint32_t n = cnt[q];
-    // uint8 rows carry mfix 0, or 2^31 - 1 when their heavy-term limbs did not fit (k_query_prep_hybrid)
-    if (n > (uint32_t)cap || n < (uint32_t)k || (!FP && mfix[q] != 0u)) {
+    if (n > (uint32_t)cap || n < (uint32_t)k) {
         if (threadIdx.x == 0) {
             status[row] = GS_ROW_DENSE;
             if (FP) resc_cnt[q] = 0;
@@ -2108,19 +1920,19 @@ int launch_dense(DenseArgs a, int waves, hipStream_t s) {
     return launch_dense_u<WT, 4>(a, waves, acc_bytes, s);
 }
 
-template <int WT, int UNROLL>
-int launch_union(UnionArgs e, hipStream_t s) {
+template <int WT, int UNROLL, bool HD>
+int launch_union_hd(UnionArgs e, hipStream_t s) {
     static std::atomic<bool> attr{false};
     // scalar entry loads for groups of up to 4 slots (terms then have at most
     // 4 entries unless queries repeat terms)
     const bool se = e.G <= 4;
-    auto fn = e.pk ? (se ? k_score_union<WT, UNROLL, true, true> : k_score_union<WT, UNROLL, true, false>)
-                   : (se ? k_score_union<WT, UNROLL, false, true> : k_score_union<WT, UNROLL, false, false>);
+    auto fn = e.pk ? (se ? k_score_union<WT, UNROLL, true, true, HD> : k_score_union<WT, UNROLL, true, false, HD>)
+                   : (se ? k_score_union<WT, UNROLL, false, true, HD> : k_score_union<WT, UNROLL, false, false, HD>);
     if (!attr.load()) {
-        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, true, true>));
-        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, true, false>));
-        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, false, true>));
-        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, false, false>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, true, true, HD>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, true, false, HD>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, false, true, HD>));
+        GS_CHECK_HIP(allow_full_lds((const void *)k_score_union<WT, UNROLL, false, false, HD>));
         attr.store(true);
     }
     const size_t lds = ((size_t)e.G << (e.tile_log2 + 2)) + kUnionMetaLds;
@@ -2134,30 +1946,22 @@ int launch_union(UnionArgs e, hipStream_t s) {
     return GS_OK;
 }
 
-template <int WT>
-int launch_hybrid(HybridArgs h, hipStream_t s) {
-    static std::atomic<bool> attr{false};
-    auto fn = h.G == 16 ? k_score_hybrid<WT, 1> : k_score_hybrid<WT, 2>;
-    if (!attr.load()) {
-        GS_CHECK_HIP(allow_full_lds((const void *)k_score_hybrid<WT, 1>));
-        GS_CHECK_HIP(allow_full_lds((const void *)k_score_hybrid<WT, 2>));
-        attr.store(true);
-    }
-    const size_t lds = ((size_t)h.G << (GS_HYBRID_TILE_LOG2 + 2)) + kHybMetaLds;
-    const int64_t total = (int64_t)((h.tiles + h.tiles_per_wg - 1) / h.tiles_per_wg) * h.n_groups;
-    if (total == 0) return GS_OK;
-    h.per_xcd = (int32_t)((total + 7) / 8);
-    const int64_t grid = (int64_t)h.per_xcd * 8;
-    GS_REQUIRE(grid < 0x7FFFFFFFll, "scoring grid too large (%lld workgroups)", (long long)grid);
-    fn<<<(unsigned)grid, kUnionThreads, lds, s>>>(h);
-    GS_CHECK_LAUNCH();
-    return GS_OK;
+// the heavy-term start (HD) only for float weights: uint8 sums must be exact
+// without rescoring
+template <int WT, int UNROLL>
+int launch_union(UnionArgs e, hipStream_t s) {
+    if constexpr (WT != GS_W_U8)
+        if (e.hsc) return launch_union_hd<WT, UNROLL, true>(e, s);
+    return launch_union_hd<WT, UNROLL, false>(e, s);
 }
 
 struct SearchPlan {
-    bool hyb;  // hybrid scorer (heavy terms as int8 matrix products)
+    bool hyb;  // heavy terms as int8 matrix products (k_head_scores), the rest as LDS adds
+    int32_t Bpad;     // slots of the heavy-term products (B rounded up to 16)
+    int64_t hsc_ld;   // docs of the coarse heavy-term sums per slot: the tiles' docs rounded up to whole 512-doc blocks
     int8_t *alimb;
     int32_t *hshift;
+    int16_t *hsc;
     int S, cap, rcap, unroll, G, n_groups, ecap, gt_np, tiles_per_wg;
     int32_t *u_term, *u_ebeg, *u_count;
     uint2 *e_sw;
@@ -2207,23 +2011,18 @@ int next_pow2_of(int64_t n) {
     return np;
 }
 
-// query group of the hybrid scorer: two 16-row MFMA blocks, one for batches of at most 16
-int hybrid_group(int32_t B) { return B <= 16 ? 16 : 32; }
-
-// The hybrid scorer runs when the index carries the heavy terms' dense copy and
-// the packed copy at the hybrid tile size, the caller did not opt out, slot
-// indexes fit 32 bits, and a group's term entries fit the LDS sort.
-bool hybrid_usable(const gs_index *ix, int32_t B, int32_t T, const gs_search_opts *o) {
+// The hybrid search runs when the index carries the heavy terms' dense copy
+// and the packed copy (integer weights), the weights are floats (uint8 sums are
+// exact as accumulated and are not rescored), and the caller did not opt out.
+bool hybrid_usable(const gs_index *ix, const gs_search_opts *o) {
     if (!ix->head_d || !ix->head_rank_d || !ix->heavy_d || (o && o->no_hybrid)) return false;
-    if (ix->tile_log2 != GS_HYBRID_TILE_LOG2 || !packed_usable(ix)) return false;
-    if ((uint64_t)ix->n_slots >= (1ull << 32)) return false;
-    return next_pow2_of((int64_t)hybrid_group(B) * T) <= kGroupSortCap;
+    return ix->wtype != GS_W_U8 && packed_usable(ix);
 }
 
 SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, const gs_search_opts *o,
                        gs_arena &ar) {
     SearchPlan p;
-    p.hyb = hybrid_usable(ix, B, T, o);
+    p.hyb = hybrid_usable(ix, o);
     // queries per group: G int32 slices of one tile fill kUnionTileLds; the group's
     // sorted term entries (next_pow2(G * T) of them) must fit the LDS sort
     int G = (int)(kUnionTileLds / 4) >> ix->tile_log2;
@@ -2232,7 +2031,6 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     if (G > B) G = B;
     auto np_of = [&](int g) { return next_pow2_of((int64_t)g * T); };
     while (G > 1 && np_of(G) > kGroupSortCap) G >>= 1;
-    if (p.hyb) G = hybrid_group(B);  // the MFMA rows: slots past B hold zero limbs
     p.G = G;
     p.n_groups = (B + G - 1) / G;
     p.ecap = G * T;
@@ -2243,9 +2041,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     const int64_t s_min = std::max<int64_t>(1, kSeedMinDocs >> ix->tile_log2);
     const int64_t s_max = std::max<int64_t>(s_min, kSeedDocs >> ix->tile_log2);
     int64_t s_def = (4ll * k + TILE - 1) >> ix->tile_log2;
-    // (the hybrid scorer has no local thresholds: its seed tiles emit every
-    // positive doc, so small k seeds from fewer docs)
-    s_def = std::min<int64_t>(std::max<int64_t>(s_def, p.hyb ? 1 : s_min), s_max);
+    s_def = std::min<int64_t>(std::max<int64_t>(s_def, s_min), s_max);
     p.S = (o && o->sample_tiles > 0) ? o->sample_tiles : (int)s_def;
     if (p.S > ix->n_tiles) p.S = ix->n_tiles;
     p.cap = (o && o->cand_cap > 0) ? o->cand_cap : kDefaultCandCap;
@@ -2274,11 +2070,17 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     p.perm = ar.take<int32_t>((size_t)B);
     p.qt_p = ar.take<int32_t>((size_t)B * T);
     p.qw_p = ar.take<float>((size_t)B * T);  // room for fp32 or uint8 query weights
+    p.Bpad = (B + 15) & ~15;
+    // whole head blocks: with tiles under 512 docs an odd tile count ends half way
+    // through a block, whose sums the scorer still reads
+    p.hsc_ld = (((int64_t)ix->n_tiles << ix->tile_log2) + kHeadBlock - 1) / kHeadBlock * kHeadBlock;
     p.alimb = nullptr;
     p.hshift = nullptr;
+    p.hsc = nullptr;
     if (p.hyb) {
-        p.alimb = ar.take<int8_t>((size_t)p.n_groups * p.G * 2 * kHeavyTerms);
+        p.alimb = ar.take<int8_t>((size_t)p.Bpad * 2 * kHeavyTerms);
         p.hshift = ar.take<int32_t>((size_t)B);
+        p.hsc = ar.take<int16_t>((size_t)p.Bpad * (size_t)p.hsc_ld);
     }
     return p;
 }
@@ -2310,8 +2112,8 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
         gs_set_error("search workspace too small: need %zu bytes, got %zu", ar.used, ws_bytes);
         return GS_ENOSPC;
     }
-    // optional per-phase events: start, query prep, threshold seed, scoring,
-    // candidate selection, fp64 rescoring, final sort
+    // optional per-phase events: start, query prep, heavy-term sums, threshold
+    // seed, scoring, candidate selection, fp64 rescoring, final sort
     auto phase = [&](int i) -> int {
         if (o && o->ev_phases && o->ev_phases[i])
             GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_phases[i]), s));
@@ -2337,12 +2139,13 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     // the fused scorer reads the packed copy when it was made for this tile size
     const void *pk = packed_usable(ix) ? ix->packed_d : nullptr;
     const int32_t pkf = pk && WT != GS_W_U8 ? 1 : 0;  // integer products of the packed float weights
-    if (p.hyb) {
-        const int32_t Bpad = p.n_groups * p.G;
-        k_query_prep_hybrid<WT><<<gs_blocks((int64_t)Bpad * 64, 256), 256, 0, s>>>(
-            qt, qw, B, Bpad, T, ix->vocab, ix->max_abs_d, ix->dup_d, ix->head_rank_d, ix->packed_shift, p.scale,
-            p.mfix, p.tau, p.cnt, p.maxbin, p.hshift, p.alimb);
-    } else {
+    if constexpr (FP) {
+        if (p.hyb)
+            k_query_prep_hybrid<WT><<<gs_blocks((int64_t)p.Bpad * 64, 256), 256, 0, s>>>(
+                qt, qw, B, p.Bpad, T, ix->vocab, ix->max_abs_d, ix->dup_d, ix->head_rank_d, ix->packed_shift,
+                p.scale, p.mfix, p.tau, p.cnt, p.maxbin, p.hshift, p.alimb);
+    }
+    if (!p.hyb) {
         k_query_prep<WT><<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(qt, qw, B, T, ix->vocab, ix->max_abs_d,
                                                                          ix->dup_d, pkf, ix->packed_shift, p.scale,
                                                                          p.mfix, p.tau, p.cnt, p.maxbin);
@@ -2414,52 +2217,28 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
             default: return launch_union<WT, 8>(e, s);
         }
     };
-    HybridArgs h{};
-    if (p.hyb) {
-        h.pk = reinterpret_cast<const uint32_t *>(pk);
-        h.offsets = ix->offsets_d;
-        h.tb = ix->tile_bounds_d;
-        h.head = ix->head_d;
-        h.alimb = p.alimb;
-        h.hshift = p.hshift;
-        h.n_tiles = ix->n_tiles;
-        h.B = B;
-        h.G = p.G;
-        h.n_groups = p.n_groups;
-        h.ecap = p.ecap;
-        h.u_term = p.u_term;
-        h.u_ebeg = p.u_ebeg;
-        h.u_count = p.u_count;
-        h.e_sw = p.e_sw;
-        h.tau = p.tau;
-        h.cnt = p.cnt;
-        h.maxbin = p.maxbin;
-        h.hist = p.hist;
-        h.cand_doc = p.cand_doc;
-        h.cand_key = p.cand_key;
-        h.mfix = p.mfix;
-        h.cap = p.cap;
-        h.k = k;
+    if (p.hyb) {  // every slot's coarse heavy-term sums, the slices' start
+        e.hsc = p.hsc;
+        e.hsc_ld = p.Bpad;
+        const int64_t head_rows = (ix->n_docs + kHeadBlock - 1) / kHeadBlock * kHeadBlock;
+        k_head_scores<<<(unsigned)(p.hsc_ld / kHeadBlock), 512, 0, s>>>(ix->head_d, head_rows, p.alimb, p.hshift, B,
+                                                                         p.Bpad, p.hsc);
+        GS_CHECK_LAUNCH();
     }
-    auto run_scorer = [&](int tile_begin, int tiles) -> int {
-        if (!p.hyb) return run_union(tile_begin, tiles);
-        h.tile_begin = tile_begin;
-        h.tiles = tiles;
-        h.tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : default_tiles_per_wg(tiles, p.n_groups);
-        return launch_hybrid<WT>(h, s);
-    };
+    if ((rc = phase(2))) return rc;
+    auto run_scorer = [&](int tile_begin, int tiles) -> int { return run_union(tile_begin, tiles); };
     e.local_k = k;  // seed launch: local k-th score thresholds (LDS-add scorer)
     if ((rc = run_scorer(0, p.S))) return rc;
     e.local_k = 0;
     k_tau_seed<<<gs_blocks((int64_t)B * 64, 256), 256, 0, s>>>(p.tau, p.maxbin, p.hist, B, k);
     GS_CHECK_LAUNCH();
-    if ((rc = phase(2))) return rc;
+    if ((rc = phase(3))) return rc;
     if (ix->n_tiles > p.S) {
         if (o && o->ev_score_begin) GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_score_begin), s));
         if ((rc = run_scorer(p.S, ix->n_tiles - p.S))) return rc;
         if (o && o->ev_score_end) GS_CHECK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(o->ev_score_end), s));
     }
-    if ((rc = phase(3))) return rc;
+    if ((rc = phase(4))) return rc;
 
     // 3. selection (+ fp64 rescoring for float weights)
     const size_t sel_lds = sel_lds_bytes(k);
@@ -2467,7 +2246,7 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
     k_select_cands<WT><<<B, kSelThreads, sel_lds, s>>>(p.cand_doc, p.cand_key, p.cnt, p.cap, k, p.mfix, p.resc_doc,
                                                  p.resc_cnt, p.rcap, perm, out_scores, out_ids, status);
     GS_CHECK_LAUNCH();
-    if ((rc = phase(4))) return rc;
+    if ((rc = phase(5))) return rc;
     if (FP) {
         dim3 g(64u, (unsigned)B);
         // doc-major rescoring: about 16K waves over the batch (16 to 64 workgroups
@@ -2485,14 +2264,14 @@ int search_impl(const gs_index *ix, const int32_t *qt, const void *qw, int32_t B
                                             p.resc_key);
         GS_CHECK_LAUNCH();
     }
-    if ((rc = phase(5))) return rc;
+    if ((rc = phase(6))) return rc;
     if (FP) {
         GS_CHECK_HIP(sel_attr((const void *)k_select_final<WT>, sel_lds));
         k_select_final<WT><<<B, kSelThreads, sel_lds, s>>>(p.resc_doc, p.resc_key, p.resc_cnt, p.rcap, k, perm,
                                                            status, reinterpret_cast<float *>(out_scores), out_ids);
         GS_CHECK_LAUNCH();
     }
-    return phase(6);
+    return phase(7);
 }
 
 template <int WT>

@@ -20,9 +20,10 @@ SYNTH_PATH = os.path.join(_HERE, "libgs_synth.so")
 GS_OK, GS_EINVAL, GS_EHIP, GS_ENOSPC = 0, 1, 2, 3
 GS_W_F32, GS_W_F16, GS_W_U8 = 0, 1, 2
 GS_ROW_DONE, GS_ROW_DENSE = 0, 1
-GS_SEARCH_PHASES = 7
+GS_SEARCH_PHASES = 8
 NOALLOC_SCRATCH_BYTES = 256 << 20   # GS_NOALLOC_SCRATCH_BYTES
-PHASE_NAMES = ("query_prep", "threshold_seed", "scoring", "candidate_select", "fp64_rescore", "final_sort")
+PHASE_NAMES = ("query_prep", "heavy_terms", "threshold_seed", "scoring", "candidate_select", "fp64_rescore",
+               "final_sort")
 ABI_VERSION = 9
 
 WTYPE_OF_DTYPE = {torch.float32: GS_W_F32, torch.float16: GS_W_F16, torch.uint8: GS_W_U8}
@@ -57,7 +58,7 @@ class GsIndex(C.Structure):
     ]
 
 HEAVY_TERMS = 64  # GS_HEAVY_TERMS
-HYBRID_TILE_LOG2 = 9  # GS_HYBRID_TILE_LOG2
+HEAD_BLOCK = 512  # GS_HEAD_BLOCK
 
 
 class GsSearchOpts(C.Structure):

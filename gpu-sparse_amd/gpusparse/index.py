@@ -32,14 +32,10 @@ DEFAULT_TILE_LOG2_PACKED = 13   # 8192 docs per LDS tile: postings read from the
 
 
 def default_tile_log2(index) -> int:
-    """Doc-tile size (log2) of the LDS-add scorer when a search names none: 8192
-    docs (the scorer reads one packed word per posting, and its per-tile set-up
-    weighs more than the 9-query groups of 4096-doc tiles save).  The hybrid
-    scorer always uses 512-doc tiles (HYBRID_TILE_LOG2)."""
+    """Doc-tile size (log2) used when a search names none: 8192 docs (the scorer
+    reads one packed word per posting, and its per-tile set-up weighs more than the
+    9-query groups of 4096-doc tiles save)."""
     return DEFAULT_TILE_LOG2_PACKED
-
-
-HYBRID_TILE_LOG2 = _lib.HYBRID_TILE_LOG2
 
 
 class CSR(NamedTuple):
@@ -370,12 +366,12 @@ def heavy_terms(index) -> torch.Tensor:
 
 
 def hybrid_eligible(index) -> bool:
-    """Whether the hybrid scorer can serve the index: a packed copy exists (finite
-    weights), the heavy lists hold each doc at most once, and slot indexes fit 32
-    bits.  Reads the heavy lists' duplicate counts once (one host sync)."""
+    """Whether the hybrid search can serve the index: float weights with a packed
+    copy (finite weights), and heavy lists that hold each doc at most once.
+    Reads the heavy lists' duplicate counts once (one host sync)."""
     a = index.aux()
     if "hybrid_ok" not in a:
-        ok = int(index.doc_ids.numel()) < (1 << 32) and int(index.num_docs) > 0
+        ok = index.wtype != _lib.GS_W_U8 and int(index.num_docs) > 0
         if ok:
             if "dup" not in a:
                 require_ascending(index)
@@ -390,11 +386,12 @@ def hybrid_eligible(index) -> bool:
 
 def build_head(index):
     """Dense copy of the heavy terms' packed integer weights (gs_head_fill): int8
-    [n_tiles * 512][2][64] limbs, and the [vocab] int8 heavy rank of each term."""
+    [num_docs rounded up to 512][2][64] limbs, and the [vocab] int8 heavy rank of
+    each term."""
     a = index.aux()
     dev = _device_of(index)
     N, V = int(index.num_docs), int(index.vocab_size)
-    n_rows = ((N + (1 << HYBRID_TILE_LOG2) - 1) >> HYBRID_TILE_LOG2) << HYBRID_TILE_LOG2
+    n_rows = (N + _lib.HEAD_BLOCK - 1) // _lib.HEAD_BLOCK * _lib.HEAD_BLOCK
     head = torch.empty((n_rows, 2, _lib.HEAVY_TERMS), dtype=torch.int8, device=dev)
     rank = torch.empty(V, dtype=torch.int8, device=dev)
     _lib.check(_lib.lib().gs_head_fill(_lib.ptr(index.doc_ids), _lib.ptr(index.scores), index.wtype,
@@ -412,9 +409,9 @@ def ensure_search_state(index, tile_log2: int | None = None, forward: bool = Tru
     same results), and for
     float weights the doc-major copy used by the exact rescoring (skipped when
     `forward` is false or the GPU has no room for it: the rescoring then searches
-    the term lists, with the same results).  With `hybrid` (tile_log2 =
-    HYBRID_TILE_LOG2) also the heavy terms' dense copy (skipped when it does not
-    fit: the search then runs the LDS-add scorer, with the same results)."""
+    the term lists, with the same results).  With `hybrid` also the heavy terms'
+    dense copy (skipped when it does not fit: the search then adds every term in
+    LDS, with the same results)."""
     if tile_log2 is None:
         tile_log2 = default_tile_log2(index)
     a = index.aux()
@@ -511,12 +508,10 @@ def build_packed(index, tile_log2: int, arrange: bool = True) -> Packed | None:
 
 
 def gs_index_struct(index, tile_log2: int | None = None, hybrid: bool = False) -> _lib.GsIndex:
-    """The C view of the index for tile_log2; with `hybrid` (tile_log2 must be
-    HYBRID_TILE_LOG2) it carries the heavy terms' dense copy as well."""
+    """The C view of the index for tile_log2; with `hybrid` it carries the heavy
+    terms' dense copy as well."""
     if tile_log2 is None:
         tile_log2 = default_tile_log2(index)
-    if hybrid and tile_log2 != HYBRID_TILE_LOG2:
-        raise ValueError(f"the hybrid scorer uses tile_log2 = {HYBRID_TILE_LOG2}, got {tile_log2}")
     a = ensure_search_state(index, tile_log2, hybrid=hybrid)
     N = int(index.num_docs)
     s = _lib.GsIndex()

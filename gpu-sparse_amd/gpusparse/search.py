@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .index import HYBRID_TILE_LOG2, default_tile_log2, gs_index_struct, hybrid_eligible, _device_of
+from .index import default_tile_log2, gs_index_struct, hybrid_eligible, _device_of
 
 MAX_K = 8192  # largest k of the fused path and of compacted_topk; search answers larger k densely
 MAX_T = 8192  # widest query batch of the fused path (terms per query); search answers wider ones densely
@@ -60,25 +60,21 @@ def query_tensors(index, query_batch):
     return qt.contiguous(), qw.contiguous()
 
 
-HYBRID_DEFAULT = False  # whether searches that name no scorer take the hybrid one
+HYBRID_DEFAULT = True  # whether searches that name no scorer take the hybrid one
 
 
 def scorer_choice(index, tile_log2: int | None = None, hybrid: bool | None = None) -> tuple[int, bool]:
-    """(tile_log2, hybrid) of a search.  hybrid=None: the default scorer
-    (HYBRID_DEFAULT: the hybrid scorer -- heavy terms as int8 matrix products --
-    when no tile size is named and the index allows it), else the LDS-add scorer
-    at tile_log2 (default 8192 docs).  hybrid=True requires an eligible index and
-    no other tile size."""
+    """(tile_log2, hybrid) of a search.  hybrid: whether the index's 64 longest
+    lists are scored as int8 matrix products (the hybrid search) instead of LDS
+    adds; None takes HYBRID_DEFAULT when the index allows it.  hybrid=True
+    requires an eligible index (float weights, heavy lists without repeated
+    docs).  tile_log2 defaults to index.default_tile_log2."""
     if hybrid is None:
-        hybrid = HYBRID_DEFAULT and tile_log2 is None and hybrid_eligible(index)
-    if hybrid:
-        if tile_log2 not in (None, HYBRID_TILE_LOG2):
-            raise ValueError(f"the hybrid scorer uses tile_log2 = {HYBRID_TILE_LOG2}, got {tile_log2}")
-        if not hybrid_eligible(index):
-            raise ValueError("the hybrid scorer needs finite weights, heavy lists without repeated docs "
-                             "and fewer than 2^32 slots")
-        return HYBRID_TILE_LOG2, True
-    return (default_tile_log2(index) if tile_log2 is None else int(tile_log2)), False
+        hybrid = HYBRID_DEFAULT and hybrid_eligible(index)
+    if hybrid and not hybrid_eligible(index):
+        raise ValueError("the hybrid search needs float weights with finite values and heavy lists without "
+                         "repeated docs")
+    return (default_tile_log2(index) if tile_log2 is None else int(tile_log2)), bool(hybrid)
 
 
 def _opts(sample_tiles=0, cand_cap=0, unroll=0, waves=0, tiles_per_wg=0, batch_order=False, hybrid=False):
@@ -167,18 +163,17 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
            batch_order: bool = False, hybrid: bool | None = None):
     """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
 
-    tile_log2, hybrid: the scorer (scorer_choice): by default the hybrid scorer
-    (the index's 64 longest lists as int8 matrix products on 512-doc tiles, the
-    other terms as LDS adds) when the index allows it; a named tile_log2 or
-    hybrid=False selects the LDS-add scorer for every term (default tile:
-    index.default_tile_log2).  Results are the same either way.
+    tile_log2: doc-tile size of the scorer (default: index.default_tile_log2).
+    hybrid: the index's 64 longest lists as int8 matrix products, the other terms
+    as LDS adds (float indexes; scorer_choice); results are the same either way.
     path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense";
     k above MAX_K (8192) or queries wider than MAX_T (8192 terms) always take the
     dense path (any k up to the doc count, any width).
     timing: optional dict; receives event pairs on the launch stream bracketing the
     fused scoring kernel ("score_kernel") and the whole gs_search call ("search"),
     the GS_SEARCH_PHASES events of each call ("phases": start, query prep,
-    threshold seed, scoring, candidate selection, fp64 rescoring, final sort) and
+    heavy-term sums, threshold seed, scoring, candidate selection, fp64
+    rescoring, final sort) and
     the number of rows finished by the dense path ("dense_rows").  Events come
     from timing["event_pool"] while it lasts (see `timing_dict`).
     batch_order: score queries in groups of consecutive queries instead of groups of

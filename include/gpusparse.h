@@ -72,15 +72,14 @@ typedef struct gs_index {
     const int32_t *heavy_d;       /* optional [GS_HEAVY_TERMS] most frequent terms (gs_heavy_terms):
                                      gs_search then groups queries that share them; NULL: batch order */
     const int8_t *head_d;         /* optional dense copy of the heavy terms' weights (gs_head_fill),
-                                     [n_tiles << tile_log2][2][GS_HEAVY_TERMS]: with it (and a packed
-                                     copy for tile_log2 = GS_HYBRID_TILE_LOG2) gs_search runs the hybrid
-                                     scorer -- heavy terms as int8 matrix products, the rest as LDS adds */
+                                     [n_docs rounded up to GS_HEAD_BLOCK][2][GS_HEAVY_TERMS]: with it
+                                     (and the packed copy, float weights) gs_search runs the hybrid
+                                     search -- heavy terms as int8 matrix products, the rest as LDS adds */
     const int8_t *head_rank_d;    /* [vocab] h for term heavy_d[h], -1 for the others (gs_head_fill) */
 } gs_index;
 
-/* Doc tile of the hybrid scorer: 512 docs, slices of 32 queries (16 for batches
- * of at most 16 queries). */
-#define GS_HYBRID_TILE_LOG2 9
+/* Docs per block of the heavy-term products: head_d rows are padded to it. */
+#define GS_HEAD_BLOCK 512
 
 #define GS_HEAVY_TERMS 64
 
@@ -100,14 +99,15 @@ typedef struct gs_search_opts {
                               least 12288, else 1) */
     void **ev_phases;      /* optional array of GS_SEARCH_PHASES hipEvent_t (entries may be NULL)
                               recorded on `stream` at the phase boundaries of gs_search: start,
-                              query prep, threshold seed, scoring, candidate selection, fp64
-                              rescoring, final sort; may be NULL */
+                              query prep, heavy-term sums (hybrid search; empty otherwise),
+                              threshold seed, scoring, candidate selection, fp64 rescoring,
+                              final sort; may be NULL */
     int32_t batch_order;   /* 1: score queries in groups of consecutive queries even when the
                               index has heavy_d (default 0: group by shared frequent terms) */
-    int32_t no_hybrid;     /* 1: the LDS-add scorer for every term even when the index has head_d */
+    int32_t no_hybrid;     /* 1: LDS adds for every term even when the index has head_d */
 } gs_search_opts;
 
-#define GS_SEARCH_PHASES 7
+#define GS_SEARCH_PHASES 8
 
 int gs_query_version(void);
 const char *gs_last_error(void);
@@ -208,10 +208,10 @@ int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wt
  * lists.  lengths_d int32 [vocab] (gs_index.lengths_d), heavy_d int32
  * [GS_HEAVY_TERMS]. */
 int gs_heavy_terms(const int32_t *lengths_d, int32_t vocab, int32_t *heavy_d, void *stream);
-/* Dense copy of the heavy terms' weights for the hybrid scorer (no counterpart in
- * the reference: the B operand of gs_search's int8 matrix products).  head_d
- * int8 [n_rows][2][GS_HEAVY_TERMS], n_rows >= n_docs (the hybrid scorer reads
- * n_tiles << tile_log2 rows): row d holds, for h < GS_HEAVY_TERMS, the packed
+/* Dense copy of the heavy terms' weights for the hybrid search (no counterpart in
+ * the reference: an operand of gs_search's int8 matrix products).  head_d int8
+ * [n_rows][2][GS_HEAVY_TERMS], n_rows >= n_docs rounded up to GS_HEAD_BLOCK
+ * (gs_search reads that many rows): row d holds, for h < GS_HEAVY_TERMS, the packed
  * copy's integer weight wq of (d, heavy_d[h]) -- the uint8 weight, or
  * rint(w * 2^w_shift) clamped to +-32767 -- as two limbs, wq & 127 at [d][0][h]
  * and wq >> 7 (arithmetic) at [d][1][h]; 0 where doc d lacks the term.  The

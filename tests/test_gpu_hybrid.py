@@ -1,19 +1,20 @@
-"""GPU parity of the hybrid scorer: the heavy terms as int8 matrix products
-(MFMA), the other terms as LDS adds, against the CPU oracle.
+"""GPU parity of the hybrid search: the index's 64 longest lists as int8 matrix
+products (MFMA, k_head_scores), whose coarse sums start the LDS slices of the
+other terms' adds, against the CPU oracle.
 
 Same bar as the other search tests: ids and scores bit-identical to the oracle
-(fp64 scatter-add rounded to fp32; exact uint32 sums for uint8 indexes).  The
-cases aim at what the hybrid adds: the dense head copy, the query limbs and
-shift (negative and repeated weights, limbs that do not fit), tail batches and
-their LDS entry stage, groups of 16 and 32 queries with partial groups, tiles
-past the last doc, vocabularies with fewer than 64 terms."""
+(the fp64 scatter-add rounded to fp32).  The cases aim at what the hybrid adds:
+the dense head copy, the query limbs and shift (negative and repeated weights,
+limbs that do not fit), the coarse start and its margin, batches that are not a
+multiple of 16, blocks past the last doc, vocabularies with fewer than 64
+terms, every tile size."""
 import numpy as np
 import pytest
 import torch
 
 import gpusparse as gs
 from gpusparse import synth
-from gpusparse.index import CSR, HYBRID_TILE_LOG2, ensure_search_state
+from gpusparse.index import CSR, ensure_search_state
 from helpers import random_csr, random_queries
 from oracle import oracle as O
 
@@ -81,14 +82,14 @@ def zipf_queries(rng, n, vocab, dtype, max_len=25, s=1.1):
 @pytest.mark.parametrize("dtype,n_docs", [(np.float32, 5000), (np.float16, 1537), (np.uint8, 700)])
 def test_head_copy_matches_oracle(device, dtype, n_docs):
     """gs_head_fill against oracle.head_limbs, byte for byte, rows up to the
-    last 512-doc tile (zero past the docs), and the heavy-rank table."""
+    last 512-doc block (zero past the docs), and the heavy-rank table."""
     from gpusparse.index import build_head
     rng = np.random.default_rng(n_docs)
     csr = zipf_csr(rng, n_docs, 400, dtype)
     if dtype != np.uint8:
         csr.data[::4] *= -1
     ix = gs.build_from_csr(csr, device)
-    ensure_search_state(ix, HYBRID_TILE_LOG2)
+    ensure_search_state(ix)
     head, rank = build_head(ix)
     ref = oracle_index(csr)
     heavy = O.heavy_terms(ref["lengths"])
@@ -103,11 +104,12 @@ def test_head_copy_matches_oracle(device, dtype, n_docs):
 # ------------------------------------------------------------------ search
 
 
-@pytest.mark.parametrize("cfg,n_docs", [("C1", 100_000), ("C3", 120_000), ("C5", 120_000), ("C2", 60_001)])
+@pytest.mark.parametrize("cfg,n_docs", [("C1", 100_000), ("C3", 120_000), ("C4", 100_000), ("C2", 60_001)])
 @pytest.mark.parametrize("B,k", [(1, 10), (16, 1000), (17, 100), (40, 1000)])
 def test_hybrid_synthetic_configs(device, cfg, n_docs, B, k):
-    """The configurations' generators at reduced sizes: batches of 1, 16, 17 and
-    40 queries (groups of 16 and 32, partial last groups), k from 10 to 1000."""
+    """The float configurations' generators at reduced sizes: batches of 1, 16,
+    17 and 40 queries (the products run on blocks of 16 queries, rows past the
+    batch zero), k from 10 to 1000."""
     c = synth.scaled(synth.CONFIGS[cfg], n_docs=n_docs, n_queries=B)
     docs, queries = synth.generate(c)
     ix = gs.build_from_csr(docs, device)
@@ -140,24 +142,36 @@ def test_hybrid_negative_and_repeated_weights(device, dtype):
         check(ix, ref, ti, tw, k)
 
 
-def test_hybrid_u8_limbs_too_large_go_dense(device):
-    """uint8: a heavy term repeated 80 times at weight 255 sums to 20400 > 16383,
-    which two limbs cannot hold: those rows are finished by the dense path and
-    the answers stay exact; the other rows stay on the hybrid path."""
+def test_hybrid_large_repeated_heavy_weights(device):
+    """A heavy term repeated 40 times in some queries, one occurrence weighing
+    3000: the summed limb pair only fits with a large shift r (the heavy terms'
+    weights rounded to a coarse grid, the margin widened to match), and the
+    answers still equal the oracle's."""
     rng = np.random.default_rng(4)
-    csr = zipf_csr(rng, 9000, 300, np.uint8)
+    csr = zipf_csr(rng, 9000, 300, np.float32)
     ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
-    ti, tw = zipf_queries(rng, 20, 300, np.uint8, max_len=10)
+    ti, tw = zipf_queries(rng, 20, 300, np.float32, max_len=10)
     h0 = int(O.heavy_terms(ref["lengths"])[0])
-    extra_t = np.full((20, 80), -1, np.int32)
-    extra_w = np.zeros((20, 80), np.uint8)
+    extra_t = np.full((20, 40), -1, np.int32)
+    extra_w = np.zeros((20, 40), np.float32)
     extra_t[::5] = h0
-    extra_w[::5] = 255
+    extra_w[::5] = rng.uniform(1e-3, 3.0, (4, 40)).astype(np.float32)
+    extra_w[::5, 0] = 3000.0
     ti = np.ascontiguousarray(np.concatenate([ti, extra_t], axis=1))
     tw = np.ascontiguousarray(np.concatenate([tw, extra_w], axis=1))
-    timing = check(ix, ref, ti, tw, 50)
-    assert timing["dense_rows"] == 4
+    check(ix, ref, ti, tw, 50)
+
+
+def test_hybrid_not_for_uint8(device):
+    """uint8 indexes keep exact sums without rescoring, so they always add every
+    term in LDS: hybrid=True raises, the default plan is not hybrid."""
+    rng = np.random.default_rng(14)
+    csr = zipf_csr(rng, 3000, 300, np.uint8)
+    ix = gs.build_from_csr(csr, device)
+    assert not gs.search_plan(ix, 8, 10, 20)["hybrid"]
+    with pytest.raises(ValueError, match="float"):
+        gs.search_plan(ix, 8, 10, 20, hybrid=True)
 
 
 @pytest.mark.parametrize("vocab", [20, 64, 70])
@@ -176,9 +190,7 @@ def test_hybrid_small_vocabularies(device, vocab):
 
 def test_hybrid_many_tail_terms_and_large_entry_lists(device):
     """150 distinct tail terms per query (a group's union spans several LDS
-    batches of 256 terms) and one tail term repeated 30 times in every query
-    (960 (slot, weight) entries per group: more than the LDS stage holds, read
-    from the union instead)."""
+    batches of terms) and one tail term repeated 30 times in every query."""
     rng = np.random.default_rng(6)
     V = 3000
     csr = zipf_csr(rng, 30000, V, np.float32, max_len=60, s=0.9)
@@ -195,31 +207,40 @@ def test_hybrid_many_tail_terms_and_large_entry_lists(device):
     check(ix, ref, ti, tw, 200)
 
 
-@pytest.mark.parametrize("n_docs", [300, 512, 513, 1100])
-def test_hybrid_tiles_past_the_docs(device, n_docs):
-    """Collections of less than one tile to a little over two: the last tile's
-    head rows past the docs are zero and its docs never become candidates."""
+@pytest.mark.parametrize("tile_log2", [None, 8, 9])
+@pytest.mark.parametrize("n_docs", [300, 512, 513, 1100, 2600])
+def test_hybrid_tiles_past_the_docs(device, n_docs, tile_log2):
+    """Collections of less than one 512-doc block to a few: blocks past the head
+    rows write zero sums and the tile's docs past the collection never become
+    candidates.  With 256-doc tiles an odd tile count ends half way through a
+    512-doc block, whose sums must still be computed (a workspace filled with
+    garbage before the call shows sums that were not)."""
     rng = np.random.default_rng(n_docs)
     csr = zipf_csr(rng, n_docs, 200, np.float16, max_len=15)
     ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti, tw = zipf_queries(rng, 18, 200, np.float32, max_len=8)
+    print(f"tiles past the docs: n_docs={n_docs} tile_log2={tile_log2}", flush=True)
     for k in (1, min(100, n_docs), n_docs):
-        check(ix, ref, ti, tw, k)
+        check(ix, ref, ti, tw, k, tile_log2=tile_log2)
+        ix.aux()["workspace"].fill_(0xCD)
 
 
-@pytest.mark.parametrize("tiles_per_wg,sample_tiles", [(1, 0), (2, 1), (7, 3), (64, 0)])
-def test_hybrid_launch_shapes_and_dirty_workspace(device, tiles_per_wg, sample_tiles):
-    """Several tiles per workgroup, seed launches of 1 and 3 tiles, and a
-    workspace filled with garbage before the call."""
+@pytest.mark.parametrize("tile_log2,tiles_per_wg,sample_tiles", [(13, 1, 0), (12, 2, 1), (10, 7, 3), (8, 64, 0),
+                                                                  (9, 0, 0)])
+def test_hybrid_launch_shapes_and_dirty_workspace(device, tile_log2, tiles_per_wg, sample_tiles):
+    """Every tile size (groups of 2 to 32 queries), several tiles per workgroup,
+    seed launches of 1 and 3 tiles, and a workspace filled with garbage before
+    the call."""
     rng = np.random.default_rng(tiles_per_wg)
     csr = zipf_csr(rng, 25000, 800, np.float32)
     ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti, tw = zipf_queries(rng, 48, 800, np.float32)
-    check(ix, ref, ti, tw, 60, tiles_per_wg=tiles_per_wg, sample_tiles=sample_tiles)
+    kw = dict(tile_log2=tile_log2, tiles_per_wg=tiles_per_wg, sample_tiles=sample_tiles)
+    check(ix, ref, ti, tw, 60, **kw)
     ix.aux()["workspace"].fill_(0xCD)
-    check(ix, ref, ti, tw, 60, tiles_per_wg=tiles_per_wg, sample_tiles=sample_tiles)
+    check(ix, ref, ti, tw, 60, **kw)
 
 
 def test_hybrid_not_used_when_heavy_lists_repeat_docs(device):
@@ -237,22 +258,15 @@ def test_hybrid_not_used_when_heavy_lists_repeat_docs(device):
     assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
     with pytest.raises(ValueError, match="hybrid"):
         gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), 20, hybrid=True)
-    with pytest.raises(ValueError, match="tile_log2"):
-        gs.search_plan(ix, 10, ti.shape[1], 20, tile_log2=12, hybrid=True)
 
 
-def test_hybrid_wide_queries_use_groups_that_fit(device):
-    """A group's term entries must fit the LDS sort (8192): 300-term queries
-    run hybrid in groups of 16 (batches of at most 16) and the LDS-add scorer
-    for larger batches, with the same answers."""
+def test_hybrid_wide_queries(device):
+    """300-term queries: every heavy term of the collection in most queries,
+    many tail terms."""
     rng = np.random.default_rng(9)
     csr = zipf_csr(rng, 8000, 2000, np.float32, max_len=40)
     ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti = np.stack([rng.choice(2000, 300, replace=False) for _ in range(24)]).astype(np.int32)
     tw = rng.uniform(0.01, 1.0, ti.shape).astype(np.float32)
-    check(ix, ref, ti[:16], tw[:16], 100)
-    assert not gs.search_plan(ix, 24, 300, 100, hybrid=True)["hybrid"]
-    s, i = gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), 100, path="fused", hybrid=True)
-    vs, _, vi = O.c_search(ref, ti, tw, 100, threads=8)
-    assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+    check(ix, ref, ti, tw, 100)

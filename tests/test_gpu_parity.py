@@ -9,6 +9,7 @@ import torch
 
 import gpusparse as gs
 from gpusparse import synth
+from gpusparse.search import HYBRID_DEFAULT
 from gpusparse.index import CSR, GPUInvertedIndex
 from helpers import random_csr, random_queries
 from oracle import oracle as O
@@ -492,22 +493,19 @@ def test_search_packed_launch_shapes(c3_small, unroll, tile_log2, tiles_per_wg):
 
 
 def test_search_plan_reports_defaults(c1, c3_small):
-    """The plans: the hybrid scorer on 512-doc tiles, 32 queries per group (16 for
-    batches of at most 16), postings from the packed copy; the LDS-add scorer
-    (hybrid=False or a named tile size): the packed copy in 8192-doc tiles, 16
-    postings per lane per chunk, 2 queries per group (64 KiB of LDS)."""
+    """The plan of the fused search: the packed copy in 8192-doc tiles, 16 postings
+    per lane per chunk, 2 queries per group (64 KiB of LDS), with or without the
+    heavy terms as matrix products (hybrid)."""
     ix32, _, ti, _ = c1
     h = gs.search_plan(ix32, 32, ti.shape[1], 100, hybrid=True)
-    assert h["hybrid"] and h["tile_log2"] == 9 and h["packed"] and h["group_size"] == 32
-    assert gs.search_plan(ix32, 16, ti.shape[1], 100, hybrid=True)["group_size"] == 16
-    assert gs.search_plan(ix32, 17, ti.shape[1], 100, hybrid=True)["group_size"] == 32
-    assert gs.search_plan(ix32, 32, ti.shape[1], 100)["hybrid"] == gs.search.HYBRID_DEFAULT
+    assert h["hybrid"] and h["tile_log2"] == 13 and h["packed"] and h["group_size"] == 2
+    assert gs.search_plan(ix32, 32, ti.shape[1], 100)["hybrid"] == HYBRID_DEFAULT
     p32 = gs.search_plan(ix32, 32, ti.shape[1], 100, hybrid=False)
     assert not p32["hybrid"]
     assert p32["tile_log2"] == 13 and p32["packed"] and p32["unroll"] == 16 and p32["group_size"] == 2
     assert p32["seed_tiles"] >= 1 and p32["tiles_per_wg"] in (1, 2, 3)
     p12 = gs.search_plan(ix32, 32, ti.shape[1], 100, tile_log2=12)
-    assert p12["group_size"] == 4 and not p12["hybrid"]
+    assert p12["group_size"] == 4 and p12["hybrid"] == HYBRID_DEFAULT
     ix16, _, ti16, _ = c3_small
     p16 = gs.search_plan(ix16, 24, ti16.shape[1], 1000, hybrid=False)
     assert p16["tile_log2"] == 13 and p16["packed"] and p16["unroll"] == 16 and p16["group_size"] == 2
@@ -589,8 +587,10 @@ def test_packed_scores_exact_under_near_ties(device, dtype, pattern, hybrid):
         assert_search_equal(ix, ref, ti, tw, k, path="fused", hybrid=hybrid)
 
 
-@pytest.mark.parametrize("hybrid", [True, False])
+@pytest.mark.parametrize("hybrid", [None, False])
 def test_search_u8_config_reduced(device, hybrid):
+    """uint8 impacts: exact uint32 sums, always from LDS adds (the hybrid search,
+    whose heavy-term start is rounded, serves float weights only)."""
     cfg = synth.scaled(synth.CONFIGS["C5"], n_docs=300_000, n_queries=64)
     docs, queries = synth.generate(cfg)
     ix = gs.build_from_csr(docs, device)
@@ -599,7 +599,9 @@ def test_search_u8_config_reduced(device, hybrid):
     assert_index_equal(ix, ref)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
     assert tw.dtype == np.uint8
-    assert gs.search_plan(ix, len(ti), ti.shape[1], 1000, hybrid=hybrid)["hybrid"] == hybrid
+    assert not gs.search_plan(ix, len(ti), ti.shape[1], 1000, hybrid=hybrid)["hybrid"]
+    with pytest.raises(ValueError, match="float"):
+        gs.search_plan(ix, len(ti), ti.shape[1], 1000, hybrid=True)
     assert_search_equal(ix, ref, ti, tw, 1000, path="fused", hybrid=hybrid)
 
 

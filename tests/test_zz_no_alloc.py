@@ -11,15 +11,18 @@ import torch
 import gpusparse as gs
 from gpusparse import _lib, synth
 from gpusparse.index import gs_index_struct
+from gpusparse.search import scorer_choice
 
 pytestmark = pytest.mark.gpu
 
 
-def run_both(ix, qt, qw, k, cand_cap=0):
+def run_both(ix, qt, qw, k, cand_cap=0, hybrid=False):
     L = _lib.lib()
     dev = qt.device
     B, T = qt.shape
-    gidx = gs_index_struct(ix)
+    tile, hyb = scorer_choice(ix, None, hybrid)
+    assert hyb == hybrid
+    gidx = gs_index_struct(ix, tile, hybrid=hyb)
     opts = _lib.GsSearchOpts(0, cand_cap, 0, 0, None, None, 0)
     sdt = torch.int32 if ix.scores.dtype == torch.uint8 else torch.float32
     s = _lib.stream_ptr(dev)
@@ -47,19 +50,19 @@ def run_both(ix, qt, qw, k, cand_cap=0):
     return st0
 
 
-@pytest.mark.parametrize("name", ["C1", "C5"])
-def test_noalloc_matches_gs_search(device, name):
+@pytest.mark.parametrize("name,hybrid", [("C1", True), ("C1", False), ("C5", False)])
+def test_noalloc_matches_gs_search(device, name, hybrid):
     cfg = synth.scaled(synth.CONFIGS[name], n_docs=150_000, n_queries=192)
     docs, queries = synth.generate(cfg)
     ix = gs.build_from_csr(docs, device)
     qt, qw, _ = gs.to_query_tensors(queries, device, weight_dtype=None)
-    print(f"noalloc {name}: B=192 k=1000, then B=37 k=100", flush=True)
-    st = run_both(ix, qt, qw, 1000)
+    print(f"noalloc {name} hybrid={hybrid}: B=192 k=1000, then B=37 k=100", flush=True)
+    st = run_both(ix, qt, qw, 1000, hybrid=hybrid)
     assert (st == _lib.GS_ROW_DONE).all()
-    st = run_both(ix, qt[:37].contiguous(), qw[:37].contiguous(), 100)
+    st = run_both(ix, qt[:37].contiguous(), qw[:37].contiguous(), 100, hybrid=hybrid)
     assert (st == _lib.GS_ROW_DONE).all()
     # rows the capped candidate buffer cannot hold are flagged alike
-    st = run_both(ix, qt[:20].contiguous(), qw[:20].contiguous(), 50, cand_cap=100)
+    st = run_both(ix, qt[:20].contiguous(), qw[:20].contiguous(), 50, cand_cap=100, hybrid=hybrid)
     assert (st == _lib.GS_ROW_DENSE).any()
 
 
