@@ -13,6 +13,7 @@ from .search import (MAX_K, MAX_T, PendingSearch, atomic_fused_score, compacted_
 from .chunked import build_chunk_boundaries, triton_chunked_score, triton_chunked_score_fused
 from .engine import determine_dimension, retrieve, run_engine, to_csr, to_query_tensors, write_run
 from .storage import load_index, save_index
+from .verification import compute_recall_exact, prepare_queries_from_meta
 
 __all__ = [
     "BLOCK_SIZE", "CSR", "VOCAB_SIZE", "GPUInvertedIndex", "build_from_csr", "build_gpu_index_from_csr",
@@ -20,5 +21,5 @@ __all__ = [
     "index_memory_stats", "require_ascending", "MAX_K", "MAX_T", "PendingSearch", "atomic_fused_score", "compacted_topk",
     "scatter_add", "search", "search_async", "search_counts", "search_plan", "timing_dict", "topk_rows", "triton_fused_score", "build_chunk_boundaries",
     "triton_chunked_score", "triton_chunked_score_fused", "determine_dimension", "retrieve", "run_engine", "to_csr", "to_query_tensors",
-    "write_run", "load_index", "save_index",
+    "write_run", "load_index", "save_index", "compute_recall_exact", "prepare_queries_from_meta",
 ]
