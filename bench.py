@@ -7,19 +7,26 @@ LDS-tile scoring with threshold selection, candidate selection, fp64 rescoring
 and the status check.  Inputs (index and query batch) are resident in HBM before
 the timed region.
 
-Prints one JSON line.  ``roofline`` is for the dominant kernel (the fused tile
-scoring kernel), timed with HIP events on its launch stream.  Its unit of work
-is one scored posting (a (query, posting of a valid query term) pair), which is
-one LDS atomic add, and its bound is the LDS atomic rate measured on the same
-GPU type (profiles/lds_atomic_rates.json).  Beside it: the physical HBM bytes
-per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated by a copy kernel;
-profiles/traffic_k_score_union_<config>.json) as a fraction of 8 TB/s, and the
-reference kernel's stream (4 B doc id + weight bytes per scored posting) as a
-labelled equivalent.  ``selection`` and ``index_build`` give bytes moved over
-time for candidate selection + fp64 rescoring + final sort, and for the device
-index build.  ``cpu_baseline`` times the reference CPU path
+Prints one JSON line.  ``value`` is queries/s with the results left in HBM (as
+the reference's benchmarks time it); ``queries_per_s_incl_d2h`` adds the
+hand-over of each batch's [B, k] scores and ids to host memory.  ``roofline`` is
+for the dominant kernel (the fused tile scoring kernel), timed with HIP events
+on its launch stream.  Its unit of work is one scored posting of a term added in
+LDS (a (query, posting) pair), which is one LDS atomic add, and its bound is the
+LDS atomic rate measured on the same GPU type (profiles/lds_atomic_rates.json).
+Beside it: the physical HBM bytes per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE,
+calibrated by a copy kernel; profiles/traffic_k_score_union_<config>.json) as a
+fraction of 8 TB/s, and the reference kernel's stream (4 B doc id + weight bytes
+per scored posting) as a labelled equivalent.  With the hybrid search (the 64
+heaviest terms as int8 matrix products) ``heavy_terms_kernel`` gives that
+kernel's HBM and MFMA fractions.  ``selection`` and ``index_build`` give bytes
+moved over time for candidate selection + fp64 rescoring + final sort, and for
+the device index build.  ``cpu_baseline`` times the reference CPU path
 (cpu_sequential_score, restated in C) on a bounded sample of the same batch in
 fresh child processes pinned with taskset and the thread-pool variables.
+``workloads`` holds, from the same run, C3 at B = 16, 64, 256 and 1024, C3 at
+k = 10, and C5 (uint8) at B = 512; with the CPU leg the whole batch of the
+headline, of k = 10 and of C5 is checked against the C oracle.
 """
 from __future__ import annotations
 
@@ -63,7 +70,11 @@ def parse():
                          "affinity up to this cap (the GPU boxes give a process 16 CPUs, one GPU's share of "
                          "the host; the JSON records the affinity beside the cores used)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--parity-queries", type=int, default=4)
+    ap.add_argument("--parity-queries", type=int, default=None,
+                    help="queries of the batch checked against the C oracle (default: the whole batch when the "
+                         "CPU leg runs, else 4)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the extra workloads (batch curve, k = 10, C5) after the headline")
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
     ap.add_argument("--scorer", default="auto", choices=["auto", "hybrid", "lds"],
                     help="fused scorer: hybrid (heavy terms as int8 MFMA products, 512-doc tiles), lds (LDS adds "
@@ -100,18 +111,20 @@ def traffic_file(cfg_name):
     return os.path.join(ROOT, "profiles", f"traffic_k_score_union_{cfg_name}.json")
 
 
-def measured_traffic(cfg_name, n_docs, tile_log2):
-    """HBM bytes per launch of the fused scorer from the committed rocprofv3 PMC
-    measurement (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size),
-    when it was taken on this workload; None otherwise."""
+def measured_traffic(cfg_name, n_docs, tile_log2, hybrid):
+    """The committed rocprofv3 PMC measurement of this workload (HBM bytes per
+    launch of the fused scorer and, for the hybrid search, of the heavy-term
+    kernel: FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), when
+    it was taken on this workload and scorer; None otherwise."""
     try:
         with open(traffic_file(cfg_name)) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    if t.get("config") != cfg_name or t.get("n_docs") != n_docs or t.get("tile_log2") != tile_log2:
+    if t.get("config") != cfg_name or t.get("n_docs") != n_docs or t.get("tile_log2") != tile_log2 or \
+            bool(t.get("hybrid", False)) != bool(hybrid):
         return None
-    return t.get("traffic_bytes_per_launch")
+    return t
 
 
 def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
@@ -123,7 +136,7 @@ def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
     import csv
     import glob
 
-    def last(sub, name):
+    def last(sub, name, required=True):
         rows = {}
         for path in glob.glob(os.path.join(d, sub, "**", "*counter_collection.csv"), recursive=True):
             for r in csv.DictReader(open(path)):
@@ -131,6 +144,8 @@ def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
                     did = int(r["Dispatch_Id"])
                     rows[did] = rows.get(did, 0.0) + float(r["Counter_Value"])
         if not rows:
+            if not required:
+                return None
             raise SystemExit(f"no {name} dispatch under {os.path.join(d, sub)}")
         return rows[max(rows)]
 
@@ -147,22 +162,30 @@ def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
     f, w = last("f", "k_score_union"), last("w", "k_score_union")
     cf, cw = last("cf", "copyBuffer"), last("cw", "copyBuffer")
     fs, ws = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+    # the hybrid search's heavy-term kernel, when the profiled run took it
+    hf, hw = last("f", "k_head_scores", False), last("w", "k_head_scores", False)
+    hybrid = hf is not None and hw is not None
     # the radix passes of the index build (term keys) and of the doc-major copy
     # (doc-id keys), in launch order: a histogram, then a scatter, per pass
     rf, rw = dispatches("f", ("k_rs_hist", "k_rs_scatter")), dispatches("w", ("k_rs_hist", "k_rs_scatter"))
     radix = [{"kernel": a[0], "fetch_bytes": round(a[1] * 1024 * fs), "write_bytes": round(b[1] * 1024 * ws)}
              for a, b in zip(rf, rw) if a[0] == b[0]]
     out = {"config": cfg_name, "n_docs": n_docs, "tile_log2": tile_log2, "kernel": "k_score_union",
+           "hybrid": hybrid,
            "fetch_kib_per_launch": f, "write_kib_per_launch": w, "copy_bytes": copy_bytes,
            "copy_fetch_kib": cf, "copy_write_kib": cw, "fetch_scale": fs, "write_scale": ws,
            "fetch_bytes_per_launch": f * 1024 * fs, "write_bytes_per_launch": w * 1024 * ws,
            "traffic_bytes_per_launch": f * 1024 * fs + w * 1024 * ws,
+           "head_kernel": "k_head_scores" if hybrid else None,
+           "head_fetch_bytes_per_launch": hf * 1024 * fs if hybrid else None,
+           "head_write_bytes_per_launch": hw * 1024 * ws if hybrid else None,
+           "head_traffic_bytes_per_launch": hf * 1024 * fs + hw * 1024 * ws if hybrid else None,
            "radix_dispatches": radix,
            "commands": [
                f"rocprofv3 --pmc FETCH_SIZE -d <out>/f -o f --output-format csv -- python3 bench.py --config {cfg_name} "
-               "--no-cpu --parity-queries 0 --steps 1 --warmup 1",
+               "--no-cpu --no-extra --parity-queries 0 --steps 1 --warmup 1",
                f"rocprofv3 --pmc WRITE_SIZE -d <out>/w -o w --output-format csv -- python3 bench.py --config {cfg_name} "
-               "--no-cpu --parity-queries 0 --steps 1 --warmup 1",
+               "--no-cpu --no-extra --parity-queries 0 --steps 1 --warmup 1",
                f"rocprofv3 --pmc FETCH_SIZE -d <out>/cf -o cf --output-format csv -- python3 bench.py --copy-bytes {copy_bytes}",
                f"rocprofv3 --pmc WRITE_SIZE -d <out>/cw -o cw --output-format csv -- python3 bench.py --copy-bytes {copy_bytes}",
                f"python3 bench.py --config {cfg_name} --summarize-traffic <out>"]}
@@ -230,6 +253,247 @@ def cpu_rows(index_h, ti, tw, k, n1, n_all, cap):
     return rows, len(allowed)
 
 
+
+
+# Published fused-path latencies of the reference at 8.84M docs, k = 1000, on one
+# H100 (final_results/corrected_2026_08/fused_topk_8m.json:3-32): context for the
+# batch curve only (other hardware, other data)
+REFERENCE_FUSED_MS = {16: 26.67, 64: 37.07, 256: 131.82}
+CURVE_BATCHES = (16, 64, 256, 1024)
+HEAD_BLOCK = 512       # docs per block of the heavy-term kernel (GS_HEAD_BLOCK)
+HEAVY_TERMS = 64       # lists taken as int8 matrix products by the hybrid search
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
+
+
+def phase_matrix(timing):
+    """[calls, phases] milliseconds of the library's per-phase events."""
+    import numpy as np
+    return np.array([[ev[i].elapsed_time(ev[i + 1]) for i in range(len(ev) - 1)] for ev in timing["phases"]])
+
+
+def time_search(a, index, qt, qw, k, hyb, depth, n_streams):
+    """Times a.steps searches of one batch resident in HBM, with `depth` batches
+    in flight over n_streams streams, after a.warmup untimed ones; then the same
+    batches one at a time (a batch's own latency), and the hand-over of one
+    batch's [B, k] scores and ids to pinned host memory (what retrieve does after
+    each batch, gpusparse_retrieval.py:166-167), timed on its own."""
+    import torch
+
+    import gpusparse as gs
+
+    def step_async(timing=None):
+        if a.path == "atomic":
+            return gs.PendingSearch(gs.atomic_fused_score(index, qt, qw, k))
+        return gs.search_async(index, (qt, qw), k, tile_log2=a.tile_log2, path=a.path, unroll=a.unroll,
+                               waves=a.waves, tiles_per_wg=a.tiles_per_wg, sample_tiles=a.sample_tiles,
+                               timing=timing, hybrid=hyb)
+
+    # Batch i is queued on stream i mod S once batch i - D has finished (its
+    # status read and any flagged rows completed), so up to D batches are in
+    # flight.  D = 1 runs them one at a time; with S = 1 the batches in flight
+    # share one stream, so only the host's work (the next batch's launches, the
+    # previous one's status read) overlaps the GPU's.
+    streams = [torch.cuda.current_stream()] + [torch.cuda.Stream() for _ in range(max(1, n_streams) - 1)]
+    for st in streams[1:]:
+        st.wait_stream(streams[0])
+
+    def run_steps(n, timing=None):
+        pend, out = [], None
+        for i in range(n):
+            if len(pend) == depth:
+                out = pend.pop(0).result()
+            with torch.cuda.stream(streams[i % len(streams)]):
+                pend.append(step_async(timing))
+        for p in pend:
+            out = p.result()
+        return out
+
+    run_steps(max(a.warmup, depth))
+    # Events are created before the timed region.  Kernel and phase times come
+    # from kernels that do not overlap: from the timed steps on one stream, else
+    # from the second pass with one batch at a time.
+    timing = gs.timing_dict(a.steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = run_steps(a.steps, timing if len(streams) == 1 else None)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    one_ms = None
+    if depth > 1:
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(a.steps):
+            step_async(timing if len(streams) > 1 else None).result()
+        torch.cuda.synchronize()
+        one_ms = 1000.0 * (time.perf_counter() - t1) / a.steps
+    hs = torch.empty(out[0].shape, dtype=out[0].dtype, pin_memory=True)
+    hi = torch.empty(out[1].shape, dtype=out[1].dtype, pin_memory=True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(a.steps):
+        hs.copy_(out[0], non_blocking=True)
+        hi.copy_(out[1], non_blocking=True)
+        torch.cuda.synchronize()
+    d2h_ms = 1000.0 * (time.perf_counter() - t1) / a.steps
+    B = qt.shape[0]
+    return {"B": B, "k": k, "ms_per_step": 1000.0 * wall / a.steps, "qps": B * a.steps / wall, "one_ms": one_ms,
+            "d2h_ms": d2h_ms, "timing": timing, "out": out, "depth": depth, "streams": len(streams)}
+
+
+def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
+    """(roofline of the fused LDS scoring kernel, plan, roofline of the heavy-term
+    kernel or None).
+
+    The LDS scorer's unit of work is one LDS atomic add: one scored posting (a
+    (query, posting) pair of a valid query term; with the hybrid search only the
+    terms outside the 64 heavy ones), so the LDS-atomic issue rate bounds it, not
+    HBM (each posting is fetched once per doc tile and query group and added to
+    every query of the group holding its term).  The heavy-term kernel reads the
+    heavy terms' int8 doc rows (128 B per doc) once and writes one int16 coarse
+    sum per (query slot, doc): HBM-bound; its int8 MFMA work (4 limb products of
+    64 terms per (slot, doc), 512 ops) is given beside it."""
+    import numpy as np
+
+    import gpusparse as gs
+    B = qt.shape[0]
+    kern_ms = [e0.elapsed_time(e1) for e0, e1 in timing["score_kernel"]]
+    call_ms = [e0.elapsed_time(e1) for e0, e1 in timing["search"]]
+    N = int(index.num_docs)
+    n_tiles = (N + (1 << a.tile_log2) - 1) >> a.tile_log2
+    # the main launch scores the tiles after the seed tiles
+    plan = gs.search_plan(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles, unroll=a.unroll,
+                          tiles_per_wg=a.tiles_per_wg, hybrid=hyb)
+    S = min(plan["seed_tiles"], n_tiles)
+    tb = index.aux()[("tile_bounds", a.tile_log2)]
+    cols = tb[:, [S, n_tiles]].cpu().numpy().astype(np.int64)
+    per_term = cols[:, 1] - cols[:, 0]
+    all_term = index.lengths.cpu().numpy().astype(np.int64)
+    qt_h = qt.cpu().numpy()
+    valid = (qt_h >= 0) & (qt_h < index.vocab_size)
+    tq = np.where(valid, qt_h, 0)
+    heavy = np.zeros(int(index.vocab_size), dtype=bool)
+    if plan["hybrid"]:
+        heavy[index.aux()["heavy"].cpu().numpy()] = True
+    in_lds = valid & ~heavy[tq]
+    post_launch = int((per_term[tq] * in_lds).sum())
+    post_tiles = int((per_term[tq] * valid).sum())
+    post_all = int((all_term[tq] * valid).sum())
+    wbytes = index.scores.element_size()
+    per_post = 4 + wbytes
+    avg_ms = float(np.mean(kern_ms))
+    adds_per_s = post_launch / (avg_ms * 1e-3)
+    lds = lds_peak()
+    tr = measured_traffic(cfg_name, N, a.tile_log2, plan["hybrid"])
+    phys = None if tr is None else tr.get("traffic_bytes_per_launch")
+    head = None
+    head_ms = 0.0
+    if plan["hybrid"] and timing.get("phases"):
+        head_ms = float(np.median(phase_matrix(timing)[:, 1]))  # the heavy_terms phase: k_head_scores alone
+        Bpad = (B + 15) // 16 * 16
+        rows = (N + HEAD_BLOCK - 1) // HEAD_BLOCK * HEAD_BLOCK
+        cols_h = ((n_tiles << a.tile_log2) + HEAD_BLOCK - 1) // HEAD_BLOCK * HEAD_BLOCK
+        hbytes = rows * 2 * HEAVY_TERMS + Bpad * cols_h * 2 + Bpad * 2 * HEAVY_TERMS + B * 4
+        ops = 4 * 2 * HEAVY_TERMS * Bpad * rows
+        hphys = None if tr is None else tr.get("head_traffic_bytes_per_launch")
+        head = {"kernel": "k_head_scores (the 64 heavy terms as int8 MFMA limb products; int16 coarse sums "
+                          "written block-major, the LDS slices' start)",
+                "bound": "hbm", "achieved": round(hbytes / (head_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(hbytes / (head_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                "bytes_per_launch": hbytes, "traffic": hphys,
+                "bytes_note": "algorithmic: heavy int8 doc rows read once (128 B per doc) + one int16 coarse sum "
+                              "written per (query slot, doc) + query limbs",
+                "ms": round(head_ms, 3),
+                "mfma_int8": {"ops_per_launch": ops, "achieved": round(ops / (head_ms * 1e-3) / 1e12, 1),
+                              "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                              "frac": round(ops / (head_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}}
+    ref_bytes = post_tiles * per_post
+    ref_ms = avg_ms + head_ms
+    roof = {"bound": "lds_atomic", "achieved": round(adds_per_s / 1e9, 1),
+            "peak": None if lds is None else round(lds["peak"] / 1e9, 1),
+            "unit": "G LDS atomic adds/s (one per scored posting of a term added in LDS)",
+            "frac": None if lds is None else round(adds_per_s / lds["peak"], 4),
+            "traffic": phys,
+            "peak_source": None if lds is None else lds["source"],
+            # the packed copy's bank-aware order brings the adds close to the
+            # conflict-free rate, the higher ceiling
+            "frac_of_conflict_free_rate": None if lds is None else round(adds_per_s / lds["conflict_free"], 4),
+            "hbm_physical": None if phys is None else {
+                "achieved": round(phys / (avg_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(phys / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                "source": os.path.relpath(traffic_file(cfg_name), ROOT)},
+            "reference_stream_equiv": {
+                "bytes_per_launch": ref_bytes, "bytes_per_posting": per_post,
+                "GBs": round(ref_bytes / (ref_ms * 1e-3) / 1e9, 1),
+                "x_hbm_peak": round(ref_bytes / (ref_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
+                "note": "the reference kernel's stream (each posting of the main launch's tiles read once per "
+                        "(query, term): doc id + weight) over the scoring kernels' time (LDS scorer + heavy-term "
+                        "kernel); here each posting is read once per (doc tile, query group), so this is not a "
+                        "fraction of any hardware peak"},
+            "kernel": "k_score_union (fused group-tile LDS scoring + threshold emission"
+                      + (", slices started from the heavy-term sums)" if plan["hybrid"] else ")"),
+            "kernel_ms_avg": round(avg_ms, 3), "kernel_ms_median": round(float(np.median(kern_ms)), 3),
+            "kernel_ms_min": round(float(np.min(kern_ms)), 3),
+            "scored_postings_per_launch": post_launch, "postings_in_launch_tiles": post_tiles,
+            "search_call_ms_avg": round(float(np.mean(call_ms)), 3),
+            "batch_scored_postings": post_all}
+    return roof, plan, head
+
+
+def components_of(timing):
+    """Median per-phase milliseconds of gs_search (HIP events the library records
+    on its launch stream) over the timed steps."""
+    import numpy as np
+
+    from gpusparse import _lib
+    per = phase_matrix(timing)
+    comp = {name: round(float(np.median(per[:, i])), 3) for i, name in enumerate(_lib.PHASE_NAMES)}
+    comp["total_gs_search"] = round(float(np.median(per.sum(axis=1))), 3)
+    return comp
+
+
+def check_parity(index_h, qt, qw, out, k, rows):
+    """The GPU's answers for `rows` queries of the batch against the C oracle's
+    exact top-k (ids, and scores bit for bit)."""
+    import numpy as np
+
+    from oracle import oracle as O
+    t0 = time.perf_counter()
+    ti, tw = qt.cpu().numpy()[:rows], qw.cpu().numpy()[:rows]
+    vs, s64, vi = O.c_search(index_h, ti, tw, k, threads=min(16, os.cpu_count() or 1))
+    got_s, got_i = out[0][:rows].cpu().numpy(), out[1][:rows].cpu().numpy()
+    diff = np.abs(got_s.astype(np.float64) - s64) if s64 is not None else np.zeros(1)
+    return {"queries_checked": rows, "ids_equal": bool(np.array_equal(got_i, vi)),
+            "scores_equal": bool(got_s.dtype == vs.dtype and np.array_equal(got_s, vs)),
+            "max_abs_diff_vs_fp64": float(np.max(diff, initial=0.0)), "s": round(time.perf_counter() - t0, 1)}
+
+
+def workload_entry(a, index, qt, qw, k, hyb, cfg_name, index_h=None):
+    """One extra workload under the same clock: q/s with two batches in flight on
+    one stream, one batch's latency, the scorer's and heavy-term kernel's times
+    and roofline fractions, the phases, and with index_h the whole batch's parity."""
+    m = time_search(a, index, qt, qw, k, hyb, 2, 1)
+    B, T = qt.shape
+    e = {"B": B, "k": k, "queries_per_s": round(m["qps"], 1), "ms_per_batch": round(m["ms_per_step"], 3),
+         "ms_per_batch_one_in_flight": None if m["one_ms"] is None else round(m["one_ms"], 3),
+         "d2h_ms": round(m["d2h_ms"], 3), "dense_rows": m["timing"].get("dense_rows", 0)}
+    if a.path == "fused" and m["timing"].get("score_kernel"):
+        roof, plan, head = scorer_roofline(a, index, qt, T, k, hyb, m["timing"], cfg_name)
+        e.update({"hybrid": plan["hybrid"], "scorer_ms": roof["kernel_ms_avg"], "scorer_lds_frac": roof["frac"],
+                  "scorer_hbm_frac": None if roof["hbm_physical"] is None else roof["hbm_physical"]["frac"],
+                  "heavy_terms_ms": None if head is None else head["ms"],
+                  "heavy_terms_hbm_frac": None if head is None else head["frac"],
+                  "phases_ms": components_of(m["timing"]) if m["timing"].get("phases") else None})
+    if index_h is not None:
+        e["parity"] = check_parity(index_h, qt, qw, m["out"], k, B)
+    ref = REFERENCE_FUSED_MS.get(B) if (cfg_name == "C3" and k == 1000) else None
+    if ref is not None:
+        e["reference_published_ms_h100"] = ref
+    log(f"{cfg_name} B={B} k={k}: {e['ms_per_batch']:.2f} ms/batch, {e['queries_per_s']:.0f} q/s"
+        + (f", scorer {e['scorer_ms']:.2f} ms" if e.get("scorer_ms") is not None else "")
+        + (f", parity {e['parity']['ids_equal'] and e['parity']['scores_equal']}" if "parity" in e else ""))
+    return e
+
+
 def main():
     a = parse()
     if a.summarize_traffic:
@@ -248,6 +512,9 @@ def main():
               "the index would shard by doc range, one shard per GPU, with the per-GPU top-k merged.",
               file=sys.stderr)
         sys.exit(2)
+    import gc
+    from dataclasses import replace
+
     import numpy as np
     import torch
 
@@ -261,6 +528,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     cfg = synth.CONFIGS[a.config]
+    full_size = not a.n_docs and not a.batch
     if a.n_docs:
         cfg = synth.scaled(cfg, n_docs=a.n_docs)
     if a.batch:
@@ -272,139 +540,48 @@ def main():
     log(f"generated {cfg.name}: {docs.shape[0]} docs, {docs.nnz} postings, {queries.shape[0]} queries "
         f"in {t_gen:.1f}s")
 
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    build_ev = {}
-    index = gs.build_from_csr(docs, dev, timing=build_ev)
-    torch.cuda.synchronize()
-    t_build = time.perf_counter() - t0
-    t0 = time.perf_counter()
+    def build(docs):
+        """The index (gs_index_count + gs_index_fill) and its search state."""
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev = {}
+        ix = gs.build_from_csr(docs, dev, timing=ev)
+        torch.cuda.synchronize()
+        t_build = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        tile, hyb = scorer_choice(ix, a.tile_log2 or None, want_hybrid)
+        ensure_search_state(ix, tile, hybrid=hyb)
+        torch.cuda.synchronize()
+        return ix, ev, t_build, time.perf_counter() - t0, tile, hyb
+
     want_hybrid = {"auto": None, "hybrid": True, "lds": False}[a.scorer]
-    a.tile_log2, hyb = scorer_choice(index, a.tile_log2 or None, want_hybrid)
-    ensure_search_state(index, a.tile_log2, hybrid=hyb)
-    torch.cuda.synchronize()
-    t_bounds = time.perf_counter() - t0
-    log(f"index built in {t_build:.2f}s (incl. H2D of the CSR); search state (tile bounds, doc-major copy) "
-        f"{t_bounds:.3f}s")
+    index, build_ev, t_build, t_state, a.tile_log2, hyb = build(docs)
+    log(f"index built in {t_build:.2f}s (incl. H2D of the CSR); first-search state (tile bounds, packed copy, "
+        f"doc-major copy{', heavy-term rows' if hyb else ''}) {t_state:.3f}s")
     qt, qw, T = gs.to_query_tensors(queries, dev, weight_dtype=None)
     B = qt.shape[0]
     k = min(a.k or cfg.k, docs.shape[0])
     del docs
 
-    def step_async(timing=None):
-        if a.path == "atomic":
-            return gs.PendingSearch(gs.atomic_fused_score(index, qt, qw, k))
-        return gs.search_async(index, (qt, qw), k, tile_log2=a.tile_log2, path=a.path, unroll=a.unroll,
-                               waves=a.waves, tiles_per_wg=a.tiles_per_wg, sample_tiles=a.sample_tiles,
-                               timing=timing, hybrid=hyb)
-
-    # Batch i is queued on stream i mod S once batch i - D has finished (its
-    # status read and any flagged rows completed), so up to D batches are in
-    # flight.  D = 1 runs them one at a time; with S = 1 the batches in flight
-    # share one stream, so only the host's work (the next batch's launches, the
-    # previous one's status read) overlaps the GPU's.
-    depth = max(1, a.inflight, a.streams)
-    streams = [torch.cuda.current_stream()] + [torch.cuda.Stream() for _ in range(max(1, a.streams) - 1)]
-    for st in streams[1:]:
-        st.wait_stream(streams[0])
-
-    def run_steps(n, timing=None):
-        pend, out = [], None
-        for i in range(n):
-            if len(pend) == depth:
-                out = pend.pop(0).result()
-            with torch.cuda.stream(streams[i % len(streams)]):
-                pend.append(step_async(timing))
-        for p in pend:
-            out = p.result()
-        return out
-
-    run_steps(max(a.warmup, depth))
-    # Events are created before the timed region.  Kernel and phase times come
-    # from kernels that do not overlap: from the timed steps on one stream, else
-    # from a second pass with one batch at a time.
-    timing = gs.timing_dict(a.steps)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    out = run_steps(a.steps, timing if len(streams) == 1 else None)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_per_step = 1000.0 * wall / a.steps
-    qps = B * a.steps / wall
-    one_ms = None
-    if depth > 1:
-        # the same batches one at a time: a batch's own latency
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(a.steps):
-            step_async(timing if len(streams) > 1 else None).result()
-        torch.cuda.synchronize()
-        one_ms = 1000.0 * (time.perf_counter() - t1) / a.steps
+    m = time_search(a, index, qt, qw, k, hyb, max(1, a.inflight, a.streams), a.streams)
+    timing, out = m["timing"], m["out"]
+    ms_per_step, qps, one_ms = m["ms_per_step"], m["qps"], m["one_ms"]
+    if one_ms is not None:
         log(f"one batch in flight: {one_ms:.2f} ms/batch")
-    log(f"{a.steps} steps: {ms_per_step:.2f} ms/step, {qps:.1f} queries/s, "
-        f"dense rows {timing.get('dense_rows', 0)}")
+    log(f"{a.steps} steps: {ms_per_step:.2f} ms/step, {qps:.1f} queries/s (results resident in HBM), "
+        f"dense rows {timing.get('dense_rows', 0)}; [B, k] hand-over to host {m['d2h_ms']:.3f} ms")
 
-    # ---- roofline of the fused tile-scoring kernel.  Its unit of work is one
-    # scored posting (a (query, posting) pair of a valid query term), which is one
-    # LDS atomic add into the query's tile slice: the LDS-atomic issue rate bounds
-    # it, not HBM (each posting is fetched once per doc tile and query group and
-    # added to every query of the group holding its term).
+    d2h_ms, dense_rows = m["d2h_ms"], timing.get("dense_rows", 0)
     wbytes = index.scores.element_size()
-    S = 0
-    roof = None
-    plan = None
+    roof = plan = head = None
     if a.path == "fused" and timing.get("score_kernel"):
-        kern_ms = [e0.elapsed_time(e1) for e0, e1 in timing["score_kernel"]]
-        call_ms = [e0.elapsed_time(e1) for e0, e1 in timing["search"]]
-        n_tiles = (index.num_docs + (1 << a.tile_log2) - 1) >> a.tile_log2
-        # the main launch scores the tiles after the seed tiles
-        plan = gs.search_plan(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles, unroll=a.unroll,
-                              tiles_per_wg=a.tiles_per_wg, hybrid=hyb)
-        S = min(plan["seed_tiles"], n_tiles)
-        tb = index.aux()[("tile_bounds", a.tile_log2)]
-        cols = tb[:, [S, n_tiles]].cpu().numpy().astype(np.int64)
-        per_term = cols[:, 1] - cols[:, 0]
-        all_term = index.lengths.cpu().numpy().astype(np.int64)
-        qt_h = qt.cpu().numpy()
-        valid = (qt_h >= 0) & (qt_h < index.vocab_size)
-        tq = np.where(valid, qt_h, 0)
-        post_launch = int((per_term[tq] * valid).sum())
-        post_all = int((all_term[tq] * valid).sum())
-        per_post = 4 + wbytes
-        avg_ms = float(np.mean(kern_ms))
-        adds_per_s = post_launch / (avg_ms * 1e-3)
-        lds = lds_peak()
-        phys = measured_traffic(cfg.name, int(index.num_docs), a.tile_log2)
-        ref_bytes = post_launch * per_post
-        roof = {"bound": "lds_atomic", "achieved": round(adds_per_s / 1e9, 1),
-                "peak": None if lds is None else round(lds["peak"] / 1e9, 1),
-                "unit": "G LDS atomic adds/s (one per scored posting)",
-                "frac": None if lds is None else round(adds_per_s / lds["peak"], 4),
-                "traffic": phys,
-                "peak_source": None if lds is None else lds["source"],
-                # the packed copy's bank-aware order brings the adds close to the
-                # conflict-free rate, the higher ceiling
-                "frac_of_conflict_free_rate": None if lds is None else round(adds_per_s / lds["conflict_free"], 4),
-                "hbm_physical": None if phys is None else {
-                    "achieved": round(phys / (avg_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(phys / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                    "source": os.path.relpath(traffic_file(cfg.name), ROOT)},
-                "reference_stream_equiv": {
-                    "bytes_per_launch": ref_bytes, "bytes_per_posting": per_post,
-                    "GBs": round(ref_bytes / (avg_ms * 1e-3) / 1e9, 1),
-                    "x_hbm_peak": round(ref_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
-                    "note": "the reference kernel's stream (each posting read once per (query, term): doc id + "
-                            "weight); here each posting is read once per (doc tile, query group), so this is "
-                            "not a fraction of any hardware peak"},
-                "kernel": "k_score_union (fused group-tile LDS scoring + threshold emission)",
-                "kernel_ms_avg": round(avg_ms, 3), "kernel_ms_median": round(float(np.median(kern_ms)), 3),
-                "kernel_ms_min": round(float(np.min(kern_ms)), 3),
-                "scored_postings_per_launch": post_launch,
-                "search_call_ms_avg": round(float(np.mean(call_ms)), 3),
-                "batch_scored_postings": post_all}
-        log(f"scoring kernel {avg_ms:.2f} ms avg: {adds_per_s / 1e9:.0f} G adds/s"
-            + ("" if lds is None else f" ({100 * adds_per_s / lds['peak']:.1f}% of the measured LDS atomic rate)")
-            + ("" if phys is None else f", HBM {phys / (avg_ms * 1e-3) / 1e9:.0f} GB/s physical"))
+        roof, plan, head = scorer_roofline(a, index, qt, T, k, hyb, timing, cfg.name)
+        log(f"scoring kernel {roof['kernel_ms_avg']:.2f} ms avg: {roof['achieved']:.0f} G adds/s"
+            + ("" if roof["frac"] is None else f" ({100 * roof['frac']:.1f}% of the measured LDS atomic rate)")
+            + ("" if roof["hbm_physical"] is None else f", HBM {roof['hbm_physical']['achieved']:.0f} GB/s physical"))
+        if head is not None:
+            log(f"heavy-term kernel {head['ms']:.3f} ms: {head['achieved']:.0f} GB/s algorithmic "
+                f"({100 * head['frac']:.1f}% of HBM), int8 MFMA {head['mfma_int8']['achieved']:.0f} TOP/s")
 
     # ---- selection after scoring: candidate selection, fp64 rescoring of the
     # candidates near the k-th score (doc-major rows), final sort.  Bytes are those
@@ -415,9 +592,9 @@ def main():
     if a.path == "fused" and timing.get("phases"):
         cand, resc = gs.search_counts(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles,
                                       unroll=a.unroll, tiles_per_wg=a.tiles_per_wg, hybrid=hyb)
-        per = np.array([[ev[i].elapsed_time(ev[i + 1]) for i in range(len(ev) - 1)] for ev in timing["phases"]])
+        per = phase_matrix(timing)
         sel_ms = float(np.median(per[:, 4:7].sum(axis=1)))
-        n_cand = int(np.minimum(cand.astype(np.int64), 65536).sum())
+        n_cand = int(np.minimum(cand.astype(np.int64), plan["cand_cap"] if plan else 65536).sum())
         n_resc = int(resc.astype(np.int64).sum())
         row_bytes = 16 + (int(index.lengths.sum().item()) / max(1, int(index.num_docs))) * (4 + wbytes)
         sel_bytes = n_cand * 8 + n_resc * 4 + int(n_resc * row_bytes) + n_resc * 8 + n_resc * 12 + B * k * 12
@@ -445,64 +622,99 @@ def main():
         index_build = {"kernels": "gs_index_count + gs_index_fill (stable radix transpose)", "ms": round(b_ms, 3),
                        "postings": nnz_b, "bytes": b_bytes,
                        "achieved": round(b_bytes / (b_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                       "frac": round(b_bytes / (b_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+                       "frac": round(b_bytes / (b_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                       "first_search_state_ms": round(1000.0 * t_state, 3),
+                       "first_search_state": "host wall time of ensure_search_state: tile bounds, packed copy "
+                                             "(pack + bank-aware arrange), list checks, doc-major copy"
+                                             + (", heavy-term rows" if hyb else "")}
         log(f"index build on device {b_ms:.2f} ms for {nnz_b} postings ({index_build['achieved']} GB/s algorithmic)")
 
-    # ---- per-phase times of gs_search (HIP events recorded by the library on
-    # its launch stream), medians over the timed steps
     components = None
     if a.path == "fused" and timing.get("phases"):
-        from gpusparse import _lib
-        per = np.array([[ev[i].elapsed_time(ev[i + 1]) for i in range(len(ev) - 1)] for ev in timing["phases"]])
-        components = {name: round(float(np.median(per[:, i])), 3) for i, name in enumerate(_lib.PHASE_NAMES)}
-        components["total_gs_search"] = round(float(np.median(per.sum(axis=1))), 3)
+        components = components_of(timing)
         log(f"phases (median ms): {components}")
 
-    # ---- parity sample at full size, and the CPU baseline
+    # ---- parity at full size (the whole batch when the CPU leg runs), and the CPU baseline
     parity = None
     cpu = None
-    need_host = a.parity_queries > 0 or not a.no_cpu
-    if need_host:
+    n_parity = a.parity_queries if a.parity_queries is not None else (4 if a.no_cpu else B)
+    index_h = None
+    if n_parity > 0 or not a.no_cpu:
         from gpusparse.index import to_host
-        from oracle import oracle as O
         index_h = to_host(index)
-        ti_h, tw_h = qt.cpu().numpy(), qw.cpu().numpy()
-        if a.parity_queries > 0:
-            nq = min(a.parity_queries, B)
-            t0 = time.perf_counter()
-            vs, s64, vi = O.c_search(index_h, ti_h[:nq], tw_h[:nq], k, threads=min(16, os.cpu_count() or 1))
-            got_s, got_i = out[0][:nq].cpu().numpy(), out[1][:nq].cpu().numpy()
-            parity = {"queries_checked": nq, "ids_equal": bool(np.array_equal(got_i, vi)),
-                      "scores_equal": bool(np.array_equal(got_s, vs)),
-                      "max_abs_diff_vs_fp64": float(np.max(np.abs(got_s.astype(np.float64) - s64)))}
-            log(f"parity vs CPU oracle on {nq} queries: {parity} ({time.perf_counter() - t0:.1f}s)")
+        if n_parity > 0:
+            parity = check_parity(index_h, qt, qw, out, k, min(n_parity, B))
+            log(f"parity vs CPU oracle on {parity['queries_checked']} queries: {parity}")
         if not a.no_cpu:
-            rows, n_aff = cpu_rows(index_h, ti_h, tw_h, k, a.cpu_queries_1, a.cpu_queries_all, a.cpu_cores)
+            rows, n_aff = cpu_rows(index_h, qt.cpu().numpy(), qw.cpu().numpy(), k, a.cpu_queries_1,
+                                   a.cpu_queries_all, a.cpu_cores)
             best = rows[-1]
             cpu = {"value": best["qps"], "unit": "queries/s", "cores": best["cores"], "kind": "port",
                    "sample": f"first {best['queries']} queries of the batch over the full index "
                              f"(reference CPU path cpu_sequential_score restated in C, fp32 accumulator)",
                    "cpu_wall_ratio": best["cpu_wall_ratio"], "affinity_cores": n_aff,
-                   "core_cap": a.cpu_cores, "rows": rows}
+                   "core_cap": a.cpu_cores, "rows": rows,
+                   "noise": "the one-core C3 rate has varied by about +-20% between boxes of this pool"}
 
     n_docs = int(index.num_docs)
+    postings = int(index.lengths.sum().item())
+    weights = str(index.scores.dtype).replace("torch.", "")
+
+    # ---- the other workloads under the same clock: the batch curve and k = 10 on
+    # this index, then C5 (uint8) at B = 512
+    extra = None
+    if not a.no_extra and cfg.name == "C3" and full_size and a.path == "fused":
+        extra = {}
+        qbig = synth.generate_rows(replace(cfg.queries, n_rows=max(CURVE_BATCHES)), cfg.seed,
+                                   synth.STREAM_QUERIES)
+        qt_c, qw_c, _ = gs.to_query_tensors(qbig, dev, weight_dtype=None)
+        for Bc in CURVE_BATCHES:
+            extra[f"C3_B{Bc}_k1000"] = workload_entry(a, index, qt_c[:Bc].contiguous(), qw_c[:Bc].contiguous(),
+                                                      1000, hyb, "C3")
+        del qt_c, qw_c
+        extra["C3_B512_k10"] = workload_entry(a, index, qt, qw, 10, hyb, "C3", index_h if not a.no_cpu else None)
+        del index, index_h, out, m, timing
+        gc.collect()
+        torch.cuda.empty_cache()
+        c5 = synth.CONFIGS["C5"]
+        docs5, queries5 = synth.generate(c5)
+        ix5, _, _, t_state5, tile5, hyb5 = build(docs5)
+        del docs5
+        qt5, qw5, _ = gs.to_query_tensors(queries5, dev, weight_dtype=None)
+        tile_keep, a.tile_log2 = a.tile_log2, tile5
+        ix5_h = None
+        if not a.no_cpu:
+            from gpusparse.index import to_host
+            ix5_h = to_host(ix5)
+        extra["C5_B512_k1000"] = workload_entry(a, ix5, qt5, qw5, 1000, hyb5, "C5", ix5_h)
+        extra["C5_B512_k1000"]["first_search_state_ms"] = round(1000.0 * t_state5, 3)
+        a.tile_log2 = tile_keep
+        del ix5, ix5_h
+
     res = {
         "metric": METRIC if (cfg.name == "C3" and k == 1000 and B == 512)
-        else f"queries/s @{n_docs} docs k={k} batch {B} ({cfg.name})", "value": round(qps, 2), "unit": "queries/s", "n_gpus": 1, "steps": a.steps,
+        else f"queries/s @{n_docs} docs k={k} batch {B} ({cfg.name})", "value": round(qps, 2), "unit": "queries/s",
+        "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32" if wbytes != 1 else "u32", "data": "synthetic",
+        "results": "device-resident: a step ends with the [B, k] scores and ids in HBM (as the reference's "
+                   "benchmarks time it); queries_per_s_incl_d2h adds one batch's hand-over to pinned host memory "
+                   "per step, serially",
+        "queries_per_s_incl_d2h": round(B / ((ms_per_step + d2h_ms) * 1e-3), 2),
+        "d2h_ms_per_batch": round(d2h_ms, 3),
         "config": {"workload": f"{cfg.name}: {cfg.description}", "n_docs": n_docs,
-                   "postings": int(index.lengths.sum().item()), "global_batch": B, "k": k, "max_query_terms": T,
-                   "weights": str(index.scores.dtype).replace("torch.", ""), "tile_docs": 1 << a.tile_log2,
-                   "path": a.path, "inflight": depth, "streams": len(streams),
+                   "postings": postings, "global_batch": B, "k": k, "max_query_terms": T,
+                   "weights": weights, "tile_docs": 1 << a.tile_log2,
+                   "path": a.path, "inflight": max(1, a.inflight, a.streams), "streams": a.streams,
                    "scorer": None if plan is None else {key: plan[key] for key in
                                                         ("group_size", "unroll", "tiles_per_wg", "seed_tiles", "packed",
                                                          "hybrid")}},
         "ms_per_batch_one_in_flight": None if one_ms is None else round(one_ms, 3),
-        "roofline": roof, "selection": selection, "index_build": index_build,
+        "roofline": roof, "heavy_terms_kernel": head, "selection": selection, "index_build": index_build,
         "cpu_baseline": cpu, "parity": parity, "components_ms": components,
-        "index_build_s": round(t_build, 3), "search_state_s": round(t_bounds, 3), "generate_s": round(t_gen, 1),
-        "dense_rows": timing.get("dense_rows", 0),
+        "index_build_s": round(t_build, 3), "search_state_s": round(t_state, 3), "generate_s": round(t_gen, 1),
+        "dense_rows": dense_rows,
+        "workloads": extra,
     }
     print(json.dumps(res), flush=True)
 

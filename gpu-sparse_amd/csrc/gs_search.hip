@@ -48,7 +48,11 @@ constexpr int kHeadShift = 16;       // bits of the heavy-term sums dropped in t
 constexpr int kHeadBlock = GS_HEAD_BLOCK;  // docs per workgroup of k_head_scores
 constexpr int64_t kSeedMinDocs = 4096;    // fewest docs of the default first tiles scored with tau = 0
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
-constexpr int kDefaultCandCap = 65536;
+constexpr int kDefaultCandCap = 65536;      // fewest candidate slots per query of the default cap
+constexpr int64_t kCandBudget = 1ll << 24;  // candidate slots of a batch that the default cap spreads over it
+constexpr int kMaxCandCap = 1 << 22;        // most candidate slots per query of the default cap
+constexpr int64_t kSeedFillWgs = 256;       // workgroups (tiles x query groups) a default seed launch aims at
+constexpr int64_t kSeedMaxTiles = 64;       // most tiles of a default seed widened towards that
 constexpr int64_t kPairMinWgs = 12288;    // workgroups (~48 per CU) needed before a workgroup scores two tiles
 constexpr int64_t kTripleMinWgs = 49152;  // and before it scores three
 constexpr size_t kTileLds = 144 * 1024;  // LDS of the fp64 / uint32 row tiles of one dense-path workgroup
@@ -2042,9 +2046,22 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     const int64_t s_max = std::max<int64_t>(s_min, kSeedDocs >> ix->tile_log2);
     int64_t s_def = (4ll * k + TILE - 1) >> ix->tile_log2;
     s_def = std::min<int64_t>(std::max<int64_t>(s_def, s_min), s_max);
+    // A small batch has few query groups, so all of its tiles are scored at once
+    // and tau rises little after the seed: its seed is widened to about
+    // kSeedFillWgs workgroups (one launch's worth), which starts tau from more docs.
+    s_def = std::max<int64_t>(s_def, std::min<int64_t>(kSeedMaxTiles, (kSeedFillWgs + p.n_groups - 1) / p.n_groups));
     p.S = (o && o->sample_tiles > 0) ? o->sample_tiles : (int)s_def;
     if (p.S > ix->n_tiles) p.S = ix->n_tiles;
-    p.cap = (o && o->cand_cap > 0) ? o->cand_cap : kDefaultCandCap;
+    if (o && o->cand_cap > 0) {
+        p.cap = o->cand_cap;
+    } else {
+        // kCandBudget slots spread over the batch, as small batches emit more
+        // candidates per query (the same reason as above); a query cannot emit
+        // more candidates than there are docs
+        int64_t c = std::max<int64_t>(kDefaultCandCap, std::min<int64_t>(kMaxCandCap, kCandBudget / B));
+        c = std::min<int64_t>(c, (ix->n_docs + 255) / 256 * 256);
+        p.cap = (int)c;
+    }
     if (p.cap < 2 * k) p.cap = 2 * k;
     p.rcap = kRescoreCap;
     // default postings per lane per chunk: 16 on packed one-word postings (their
@@ -2348,6 +2365,7 @@ extern "C" int gs_search_plan(const gs_index *index, int32_t B, int32_t T, int32
     out->tiles_per_wg = p.tiles_per_wg > 0 ? p.tiles_per_wg : (rest > 0 ? default_tiles_per_wg(rest, p.n_groups) : 1);
     out->packed = packed_usable(index);
     out->hybrid = p.hyb;
+    out->cand_cap = p.cap;
     return GS_OK;
 }
 

@@ -24,7 +24,7 @@ GS_SEARCH_PHASES = 8
 NOALLOC_SCRATCH_BYTES = 256 << 20   # GS_NOALLOC_SCRATCH_BYTES
 PHASE_NAMES = ("query_prep", "heavy_terms", "threshold_seed", "scoring", "candidate_select", "fp64_rescore",
                "final_sort")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 WTYPE_OF_DTYPE = {torch.float32: GS_W_F32, torch.float16: GS_W_F16, torch.uint8: GS_W_U8}
 
@@ -108,7 +108,8 @@ class GsSearchPlanInfo(C.Structure):
     """Mirror of ``struct gs_search_plan_info`` in include/gpusparse.h."""
 
     _fields_ = [("seed_tiles", C.c_int32), ("group_size", C.c_int32), ("unroll", C.c_int32),
-                ("tiles_per_wg", C.c_int32), ("packed", C.c_int32), ("hybrid", C.c_int32)]
+                ("tiles_per_wg", C.c_int32), ("packed", C.c_int32), ("hybrid", C.c_int32),
+                ("cand_cap", C.c_int32)]
 
 
 SIGNATURES = {

@@ -302,7 +302,7 @@ def search_plan(index, B: int, T: int, k: int, *, tile_log2: int | None = None, 
                                          _lib.C.byref(opts), _lib.C.byref(info)), "gs_search_plan")
     return {"tile_log2": tile_log2, "seed_tiles": info.seed_tiles, "group_size": info.group_size,
             "unroll": info.unroll, "tiles_per_wg": info.tiles_per_wg, "packed": bool(info.packed),
-            "hybrid": bool(info.hybrid)}
+            "hybrid": bool(info.hybrid), "cand_cap": info.cand_cap}
 
 
 def search_counts(index, B: int, T: int, k: int, *, tile_log2: int | None = None, sample_tiles: int = 0,

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 9
+#define GS_ABI_VERSION 10
 
 #define GS_OK 0
 #define GS_EINVAL 1   /* bad argument or layout */
@@ -87,8 +87,10 @@ typedef struct gs_index {
 typedef struct gs_search_opts {
     int32_t sample_tiles;  /* doc tiles scored first with tau = 0 (all their positive docs become
                               candidates) to seed the k-th-score threshold (default: about 4 k
-                              docs, at least 4 Ki and at most 32 Ki docs) */
-    int32_t cand_cap;      /* candidates kept per query before the dense fallback (default 65536) */
+                              docs, at least 4 Ki and at most 32 Ki docs, widened for batches of
+                              few query groups to about 256 workgroups, at most 64 tiles) */
+    int32_t cand_cap;      /* candidates kept per query before the dense fallback (0: 2^24 / B within
+                              [65536, 2^22], at most the docs rounded up to 256) */
     int32_t unroll;        /* postings per lane per chunk of the fused scorer: 1, 2, 4, 8 or 16 (default
                               16 with a packed copy, else 8) */
     int32_t waves;         /* reserved, ignored */
@@ -252,6 +254,8 @@ typedef struct gs_search_plan_info {
     int32_t tiles_per_wg;  /* doc tiles per scoring workgroup after the seed tiles */
     int32_t packed;        /* 1 when the scorer reads the packed copy */
     int32_t hybrid;        /* 1 when heavy terms are scored as int8 matrix products (head_d) */
+    int32_t cand_cap;      /* candidate slots per query (opts->cand_cap, or the default: 2^24 / B
+                              within [65536, 2^22], at most the docs rounded up to 256, at least 2k) */
 } gs_search_plan_info;
 int gs_search_plan(const gs_index *index, int32_t B, int32_t T, int32_t k, const gs_search_opts *opts,
                    gs_search_plan_info *out);
@@ -269,7 +273,8 @@ int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_wei
  * results and status as gs_search; the caller still passes inputs and outputs.
  * GS_ENOSPC, with a message, when the search needs more scratch than that
  * (gs_search_workspace reports the need): e.g. B = 512, T = 107, k = 1000 fits
- * with cand_cap <= 32768, and B <= 256 fits at the default caps.  The scratch
+ * with cand_cap <= 32768, and B <= 256 fits at the default caps (the hybrid search
+ * needs 2 bytes more per query slot and doc, for its coarse heavy-term sums).  The scratch
  * keeps the last call's contents; every call clears what it needs cleared.
  * Calls that overlap on one GPU (other threads, other streams) share that GPU's
  * array and race: serialise them.  Allocates nothing and does not synchronise. */

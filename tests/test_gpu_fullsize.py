@@ -8,7 +8,8 @@ At these sizes the oracle does not rebuild the index on the host.  Instead:
   offsets, every list ascending (gs_check_lists), and the same multiset of
   (doc, term, weight) postings (the oracle's order-independent checksum);
 - the oracle then scores the host copy of that index (as bench.py does), and
-  the GPU answers must equal its exact top-k bit for bit: ids, and scores equal
+  the GPU answers to every query of the batch must equal its exact top-k bit
+  for bit: ids, and scores equal
   to the fp64 scatter-add rounded to fp32 (|diff| <= 1e-5 follows) or the
   exact uint32 sums.
 One configuration is held at a time (the previous one is freed first)."""
@@ -63,11 +64,17 @@ def check_index(name, device):
     assert O.checksum_index(h, threads=16) == (want, 0)
 
 
-def check_search(name, device, k, rows):
+def check_search(name, device, k, rows=None, batch=None, **opts):
+    """The GPU's top-k of the whole batch (or of its first `batch` queries); `rows`
+    of it (all by default) checked against the oracle."""
     cfg, ix, h, qt, qw, *_ = full(name, device)
-    print(f"{name}: search B={qt.shape[0]} k={k}, {len(rows)} rows checked", flush=True)
+    if batch is not None:
+        qt, qw = qt[:batch].contiguous(), qw[:batch].contiguous()
+    if rows is None:
+        rows = np.arange(qt.shape[0])
+    print(f"{name}: search B={qt.shape[0]} k={k} {opts}, {len(rows)} rows checked", flush=True)
     timing = {}
-    s, i = gs.search(ix, (qt, qw), k, timing=timing)
+    s, i = gs.search(ix, (qt, qw), k, timing=timing, path="fused", **opts)
     assert s.shape == (qt.shape[0], k)
     ti, tw = qt.cpu().numpy()[rows], qw.cpu().numpy()[rows]
     vs, s64, vi = O.c_search(h, ti, tw, k, threads=16)
@@ -79,14 +86,6 @@ def check_search(name, device, k, rows):
     return timing
 
 
-def sample_rows(B, n, seed):
-    """n rows of a B-query batch: the first n/2 and n/2 more spread at random."""
-    rng = np.random.default_rng(seed)
-    head = np.arange(n // 2)
-    rest = rng.choice(np.arange(n // 2, B), size=n - n // 2, replace=False)
-    return np.sort(np.concatenate([head, rest]))
-
-
 def test_c2_full_index(device):
     check_index("C2", device)
 
@@ -94,28 +93,41 @@ def test_c2_full_index(device):
 def test_c2_full_search_whole_batch(device):
     """1M docs, B=1024 (the groups of a whole 1024-query ordering block), fp32,
     k=1000: every query of the batch checked."""
-    check_search("C2", device, 1000, np.arange(1024))
+    check_search("C2", device, 1000)
 
 
 def test_c4_full_index(device):
     check_index("C4", device)
 
 
-def test_c4_full_search(device):
+@pytest.mark.parametrize("tile_log2,hybrid", [(None, None), (None, False), (8, True), (8, False), (10, None),
+                                              (12, None)])
+def test_c4_full_search(device, tile_log2, hybrid):
     """1M docs whose top-50 terms each hold > 200K postings (dense in every tile):
-    the head-heavy case of the scorer, 96 rows of the 512-query batch."""
-    rows = sample_rows(512, 96, seed=4)
-    check_search("C4", device, 1000, rows)
+    the head-heavy case of the scorer, every row of the 512-query batch, over the
+    tile sweep (256, 1K, 4K and the default 8K docs); at 256-doc tiles 32 queries
+    share a workgroup, with and without the heavy terms as matrix products."""
+    check_search("C4", device, 1000, tile_log2=tile_log2, hybrid=hybrid)
 
 
 def test_c3_full_index(device):
     check_index("C3", device)
 
 
-@pytest.mark.parametrize("k", [1000, 10])
-def test_c3_full_search(device, k):
-    rows = sample_rows(512, 48, seed=k)
-    timing = check_search("C3", device, k, rows)
+@pytest.mark.parametrize("k,hybrid", [(1000, None), (1000, False), (10, None)])
+def test_c3_full_search(device, k, hybrid):
+    """Every row of the 512-query batch, by the default search (the hybrid one
+    for these fp16 weights) and by the LDS-only one."""
+    timing = check_search("C3", device, k, hybrid=hybrid)
+    assert timing["dense_rows"] == 0
+
+
+@pytest.mark.parametrize("B", [1, 8, 16, 64])
+def test_c3_full_small_batches(device, B):
+    """Few query groups score all their tiles at once, so tau rises little after
+    the seed; the seed widened for them and the default candidate cap spread over
+    the batch keep every row on the fused path, exact."""
+    timing = check_search("C3", device, 1000, batch=B)
     assert timing["dense_rows"] == 0
 
 
@@ -126,8 +138,7 @@ def test_c5_full_index(device):
 def test_c5_full_search_bit_exact(device):
     """The integer configuration: uint8 x uint8 products summed in uint32,
     bit-exact with the CPU integer reference, ties by ascending doc id."""
-    rows = sample_rows(512, 48, seed=5)
-    check_search("C5", device, 1000, rows)
+    check_search("C5", device, 1000)
 
 
 def test_zz_release_full_size(device):

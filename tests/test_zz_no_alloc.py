@@ -73,6 +73,7 @@ def test_noalloc_refuses_searches_beyond_its_scratch(device):
     gidx = gs_index_struct(ix)
     B, T, k = 600, 8, 1000  # 600 queries x (64K candidates + 16K rescored) exceed 256 MiB
     opts = _lib.GsSearchOpts()
+    opts.cand_cap = 65536  # the default would be held to the 20K docs
     need = C.c_size_t()
     L = _lib.lib()
     _lib.check(L.gs_search_workspace(C.byref(gidx), B, T, k, C.byref(opts), C.byref(need)), "gs_search_workspace")
