@@ -261,7 +261,6 @@ def cpu_rows(index_h, ti, tw, k, n1, n_all, cap):
 REFERENCE_FUSED_MS = {16: 26.67, 64: 37.07, 256: 131.82}
 CURVE_BATCHES = (16, 64, 256, 1024)
 HEAD_BLOCK = 512       # docs per block of the heavy-term kernel (GS_HEAD_BLOCK)
-HEAVY_TERMS = 64       # lists taken as int8 matrix products by the hybrid search
 PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
 
 
@@ -346,7 +345,7 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
 
     The LDS scorer's unit of work is one LDS atomic add: one scored posting (a
     (query, posting) pair of a valid query term; with the hybrid search only the
-    terms outside the 64 heavy ones), so the LDS-atomic issue rate bounds it, not
+    terms outside the heavy ones), so the LDS-atomic issue rate bounds it, not
     HBM (each posting is fetched once per doc tile and query group and added to
     every query of the group holding its term).  The heavy-term kernel reads the
     heavy terms' int8 doc rows (128 B per doc) once and writes one int16 coarse
@@ -355,6 +354,7 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
     import numpy as np
 
     import gpusparse as gs
+    from gpusparse import _lib
     B = qt.shape[0]
     kern_ms = [e0.elapsed_time(e1) for e0, e1 in timing["score_kernel"]]
     call_ms = [e0.elapsed_time(e1) for e0, e1 in timing["search"]]
@@ -392,10 +392,11 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
         Bpad = (B + 15) // 16 * 16
         rows = (N + HEAD_BLOCK - 1) // HEAD_BLOCK * HEAD_BLOCK
         cols_h = ((n_tiles << a.tile_log2) + HEAD_BLOCK - 1) // HEAD_BLOCK * HEAD_BLOCK
-        hbytes = rows * 2 * HEAVY_TERMS + Bpad * cols_h * 2 + Bpad * 2 * HEAVY_TERMS + B * 4
-        ops = 4 * 2 * HEAVY_TERMS * Bpad * rows
+        n_heavy = _lib.heavy_term_count()  # lists taken as int8 matrix products
+        hbytes = rows * 2 * n_heavy + Bpad * cols_h * 2 + Bpad * 2 * n_heavy + B * 4
+        ops = 4 * 2 * n_heavy * Bpad * rows
         hphys = None if tr is None else tr.get("head_traffic_bytes_per_launch")
-        head = {"kernel": "k_head_scores (the 64 heavy terms as int8 MFMA limb products; int16 coarse sums "
+        head = {"kernel": f"k_head_scores (the {n_heavy} heavy terms as int8 MFMA limb products; int16 coarse sums "
                           "written block-major, the LDS slices' start)",
                 "bound": "hbm", "achieved": round(hbytes / (head_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(hbytes / (head_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),

@@ -28,6 +28,7 @@ void gs_set_error(const char *fmt, ...) {
 }
 
 extern "C" int gs_query_version(void) { return GS_ABI_VERSION; }
+extern "C" int gs_heavy_term_count(void) { return kHeavyTerms; }
 extern "C" const char *gs_last_error(void) { return g_err; }
 
 namespace {
@@ -915,58 +916,109 @@ __global__ void __launch_bounds__(1024) k_heavy_terms(const int32_t *__restrict_
         }
     }
     __syncthreads();
-    if (tid < 64) {  // bitonic sort of the 64 picks by (length desc, term asc); -1 last
-        const int32_t t = s_sel[lane];
-        uint64_t key = t < 0 ? 0ull : ((uint64_t)(uint32_t)len[t] << 32) | (uint32_t)(0x7FFFFFFF - t);
-        for (int size = 2; size <= 64; size <<= 1)
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                const uint64_t o = __shfl_xor(key, stride, 64);
-                const bool desc = (lane & size) == 0;
-                const bool lower = (lane & stride) == 0;
-                key = (lower == desc) ? (key > o ? key : o) : (key < o ? key : o);
+    // bitonic sort of the picks by (length desc, term asc), -1 last: key =
+    // length << 32 | (2^31 - 1 - term), 0 for no pick, sorted descending
+    __shared__ uint64_t s_key[kHeavyTerms];
+    if (tid < kHeavyTerms) {
+        const int32_t t = s_sel[tid];
+        s_key[tid] = t < 0 ? 0ull : ((uint64_t)(uint32_t)len[t] << 32) | (uint32_t)(0x7FFFFFFF - t);
+    }
+    for (int size = 2; size <= kHeavyTerms; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            const int j = tid ^ stride;
+            if (tid < kHeavyTerms && j > tid) {
+                const uint64_t x = s_key[tid], y = s_key[j];
+                if (((tid & size) == 0) ? x < y : x > y) {
+                    s_key[tid] = y;
+                    s_key[j] = x;
+                }
             }
-        heavy[lane] = key ? (int32_t)(0x7FFFFFFF - (uint32_t)key) : -1;
+        }
+    __syncthreads();
+    (void)lane;
+    if (tid < kHeavyTerms) {
+        const uint64_t key = s_key[tid];
+        heavy[tid] = key ? (int32_t)(0x7FFFFFFF - (uint32_t)key) : -1;
     }
 }
 
-// Dense copy of the heavy terms' packed integer weights, the B operand of the
-// hybrid scorer's int8 matrix products: row d holds two limb vectors of
-// GS_HEAVY_TERMS bytes, low = wq & 127 and high = wq >> 7 (arithmetic), for wq
-// the packed copy's integer weight of (d, heavy[h]) (pack_word_of) and 0 where
-// doc d lacks term h.  Every |wq| <= 16383 fits: low in [0, 127], high in
-// [-128, 127].  One thread per posting of one heavy list (blockIdx.y = h); the
-// lists hold each doc at most once (checked by the caller).
-template <int WT>
-__global__ void k_head_fill(const int32_t *__restrict__ doc, const void *__restrict__ w,
-                            const int64_t *__restrict__ offsets, const int32_t *__restrict__ lengths,
-                            const int32_t *__restrict__ heavy, int32_t shift, int64_t n_docs, int8_t *__restrict__ head) {
-    const int h = blockIdx.y;
-    const int32_t t = heavy[h];
-    if (t < 0) return;
-    const int64_t o = offsets[t];
-    const int32_t n = lengths[t];
-    const auto *wall = reinterpret_cast<const typename gs_weight<WT>::store_t *>(w);
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const int32_t d = doc[o + i];
-        if (d < 0 || d >= n_docs) continue;
-        // the packed word's weight half: uint8 0..255, or int16 rint(w 2^shift)
-        const int32_t wq = (int32_t)(int16_t)(pack_word_of<WT>(d, wall[o + i], 0u, shift) >> 16);
-        int8_t *row = head + (int64_t)d * (2 * kHeavyTerms);
-        row[h] = (int8_t)(wq & 127);
-        row[kHeavyTerms + h] = (int8_t)(wq >> 7);
+// Dense copy of the heavy terms' packed integer weights, an operand of the
+// hybrid search's int8 matrix products: row d holds two limb vectors of
+// kHeavyTerms bytes, low = wq & 127 and high = wq >> 7 (arithmetic), for wq the
+// packed copy's integer weight of (d, heavy[h]) (pack_word_of) and 0 where doc d
+// lacks term h.  Every |wq| <= 16383 fits: low in [0, 127], high in [-128, 127].
+// One workgroup per kHeadFillDocs docs: per heavy term, a lane finds the term's
+// postings of those docs (binary search of the ascending list), the wave writes
+// their limbs into the block's rows staged in LDS, and the workgroup writes the
+// rows out whole (a byte scatter straight into the rows would cost a write
+// transaction per byte).  The lists hold each doc at most once (checked by the
+// caller); rows past n_docs stay zero.
+constexpr int kHeadFillDocs = 256;
+constexpr int kHeadRow = 2 * kHeavyTerms;  // bytes per row
+static_assert(kHeadFillDocs * kHeadRow <= 64 * 1024, "head fill stage fits 64 KiB of LDS");
+
+// the first position in doc[lo, hi) (ascending) holding a doc >= d
+__device__ __forceinline__ int64_t lower_doc(const int32_t *__restrict__ doc, int64_t lo, int64_t hi, int64_t d) {
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((int64_t)doc[mid] < d) lo = mid + 1;
+        else hi = mid;
     }
+    return lo;
+}
+
+template <int WT>
+__global__ void __launch_bounds__(256)
+    k_head_fill(const int32_t *__restrict__ doc, const void *__restrict__ w, const int64_t *__restrict__ offsets,
+                const int32_t *__restrict__ lengths, const int32_t *__restrict__ heavy, int32_t shift, int64_t n_docs,
+                int64_t n_rows, int8_t *__restrict__ head) {
+    __shared__ __align__(16) int8_t stage[kHeadFillDocs * kHeadRow];
+    __shared__ int64_t s_lo[kHeavyTerms], s_hi[kHeavyTerms];
+    const int tid = threadIdx.x, lane = gs_lane(), wave = tid >> 6;
+    const int64_t d0 = (int64_t)blockIdx.x * kHeadFillDocs;
+    const int64_t d1 = min(d0 + kHeadFillDocs, n_docs);
+    for (int i = tid; i < kHeadFillDocs * kHeadRow / 16; i += blockDim.x)
+        reinterpret_cast<uint4 *>(stage)[i] = make_uint4(0, 0, 0, 0);
+    for (int h = tid; h < kHeavyTerms; h += blockDim.x) {
+        const int32_t t = heavy[h];
+        int64_t lo = 0, hi = 0;
+        if (t >= 0 && d0 < d1) {
+            const int64_t o = offsets[t], e = o + lengths[t];
+            lo = lower_doc(doc, o, e, d0);
+            hi = lower_doc(doc, lo, e, d1);
+        }
+        s_lo[h] = lo;
+        s_hi[h] = hi;
+    }
+    __syncthreads();
+    const auto *wall = reinterpret_cast<const typename gs_weight<WT>::store_t *>(w);
+    for (int h = wave; h < kHeavyTerms; h += blockDim.x / 64) {
+        for (int64_t i = s_lo[h] + lane; i < s_hi[h]; i += 64) {
+            const int32_t d = doc[i];  // in [d0, d1): the range above
+            // the packed word's weight half: uint8 0..255, or int16 rint(w 2^shift)
+            const int32_t wq = (int32_t)(int16_t)(pack_word_of<WT>(d, wall[i], 0u, shift) >> 16);
+            int8_t *row = stage + (int64_t)(d - d0) * kHeadRow;
+            row[h] = (int8_t)(wq & 127);
+            row[kHeavyTerms + h] = (int8_t)(wq >> 7);
+        }
+    }
+    __syncthreads();
+    const int64_t rows = min<int64_t>(kHeadFillDocs, n_rows - d0);
+    uint4 *out = reinterpret_cast<uint4 *>(head + d0 * kHeadRow);
+    for (int64_t i = tid; i < rows * kHeadRow / 16; i += blockDim.x) out[i] = reinterpret_cast<const uint4 *>(stage)[i];
 }
 
 // rank[t] = h for t = heavy[h], -1 for every other term
-__global__ void k_head_rank(int32_t V, int8_t *__restrict__ rank) {
+__global__ void k_head_rank(int32_t V, int16_t *__restrict__ rank) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < V; i += (int64_t)gridDim.x * blockDim.x)
         rank[i] = -1;
 }
-__global__ void k_head_rank_set(const int32_t *__restrict__ heavy, int32_t V, int8_t *__restrict__ rank) {
+__global__ void k_head_rank_set(const int32_t *__restrict__ heavy, int32_t V, int16_t *__restrict__ rank) {
     const int h = threadIdx.x;
     if (h < kHeavyTerms) {
         const int32_t t = heavy[h];
-        if (t >= 0 && t < V) rank[t] = (int8_t)h;
+        if (t >= 0 && t < V) rank[t] = (int16_t)h;
     }
 }
 
@@ -1388,33 +1440,34 @@ extern "C" int gs_heavy_terms(const int32_t *lengths_d, int32_t vocab, int32_t *
 
 extern "C" int gs_head_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, const int64_t *offsets_d,
                             const int32_t *lengths_d, int32_t vocab, const int32_t *heavy_d, int32_t w_shift,
-                            int64_t n_docs, int64_t n_rows, int8_t *head_d, int8_t *head_rank_d, void *stream) {
+                            int64_t n_docs, int64_t n_rows, int8_t *head_d, int16_t *head_rank_d, void *stream) {
     GS_REQUIRE(vocab > 0, "vocab must be positive, got %d", vocab);
     GS_REQUIRE(n_docs >= 0 && n_rows >= n_docs, "head rows %lld fewer than the %lld docs", (long long)n_rows,
                (long long)n_docs);
+    GS_REQUIRE(n_rows % 16 == 0, "head rows %lld not a multiple of 16", (long long)n_rows);
     GS_REQUIRE(wtype >= GS_W_F32 && wtype <= GS_W_U8, "unknown weight type %d", wtype);
     GS_REQUIRE(wtype == GS_W_U8 || (w_shift >= -200 && w_shift <= 200), "w_shift %d outside [-200, 200]", w_shift);
     GS_REQUIRE(doc_ids_d && weights_d && offsets_d && lengths_d && heavy_d && head_d && head_rank_d,
                "null pointer");
     hipStream_t s = gs_stream(stream);
-    const int64_t bytes = n_rows * 2 * kHeavyTerms;
-    k_fill<uint32_t><<<gs_blocks(bytes / 4, 256, 1 << 16), 256, 0, s>>>(reinterpret_cast<uint32_t *>(head_d),
-                                                                         bytes / 4, 0u);
     k_head_rank<<<gs_blocks(vocab, 256), 256, 0, s>>>(vocab, head_rank_d);
     k_head_rank_set<<<1, kHeavyTerms, 0, s>>>(heavy_d, vocab, head_rank_d);
-    const dim3 g(gs_blocks(n_docs, 256, 4096), kHeavyTerms);
+    GS_CHECK_LAUNCH();
+    const int64_t nb = (n_rows + kHeadFillDocs - 1) / kHeadFillDocs;  // every row written, zero past n_docs
+    if (nb == 0) return GS_OK;
+    GS_REQUIRE(nb < (1ll << 31), "too many head rows");
     switch (wtype) {
         case GS_W_F32:
-            k_head_fill<GS_W_F32><<<g, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d, w_shift,
-                                                    n_docs, head_d);
+            k_head_fill<GS_W_F32><<<(unsigned)nb, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d,
+                                                               w_shift, n_docs, n_rows, head_d);
             break;
         case GS_W_F16:
-            k_head_fill<GS_W_F16><<<g, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d, w_shift,
-                                                    n_docs, head_d);
+            k_head_fill<GS_W_F16><<<(unsigned)nb, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d,
+                                                               w_shift, n_docs, n_rows, head_d);
             break;
         default:
-            k_head_fill<GS_W_U8><<<g, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d, 0, n_docs,
-                                                   head_d);
+            k_head_fill<GS_W_U8><<<(unsigned)nb, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, lengths_d, heavy_d, 0,
+                                                              n_docs, n_rows, head_d);
             break;
     }
     GS_CHECK_LAUNCH();

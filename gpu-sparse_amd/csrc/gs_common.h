@@ -58,7 +58,9 @@ struct gs_arena {
 // ------------------------------------------------------------------ device helpers
 
 constexpr int GS_WAVE = 64;
-constexpr int kHeavyTerms = GS_HEAVY_TERMS;  // most frequent terms that sign a query for grouping
+constexpr int kHeavyTerms = GS_HEAVY_TERMS;  // most frequent terms: the hybrid search's matrix-product terms
+constexpr int kSignTerms = 64;               // the first of them sign a query for grouping (a 64-bit mask)
+static_assert(kHeavyTerms == 64 || kHeavyTerms == 128 || kHeavyTerms == 256, "heavy terms: 64, 128 or 256");
 
 __device__ __forceinline__ int gs_lane() { return (int)(threadIdx.x & (GS_WAVE - 1)); }
 

@@ -353,7 +353,7 @@ template <int WT>
 __global__ void __launch_bounds__(1024)
     k_group_terms(const int32_t *__restrict__ qt, const void *__restrict__ qw, const float *__restrict__ scale,
                   int32_t pk, int32_t B, int32_t T, int32_t V, int32_t G, int32_t ecap,
-                  const int8_t *__restrict__ hrank, int32_t *__restrict__ u_term, int32_t *__restrict__ u_ebeg,
+                  const int16_t *__restrict__ hrank, int32_t *__restrict__ u_term, int32_t *__restrict__ u_ebeg,
                   int32_t *__restrict__ u_count, uint2 *__restrict__ e_sw) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     __shared__ int32_t s_sh[17];
@@ -492,8 +492,8 @@ __global__ void __launch_bounds__(1024)
 
 // Each posting is loaded once per (doc tile, query group) and added to every slot
 // of the group holding its term, so groups whose queries share long lists load
-// fewer postings.  A query's signature is the set of the index's kHeavyTerms most
-// frequent terms it holds: a 64-bit mask, bit 63 = the most frequent term.  Per
+// fewer postings.  A query's signature is the set of the index's kSignTerms (64)
+// most frequent terms it holds: a 64-bit mask, bit 63 = the most frequent term.  Per
 // block of NB = G floor(1024 / G) queries: masks from all (query, term) entries
 // at once (LDS atomic or), then the queries sorted by mask (descending, then
 // query index), so that queries holding the same most frequent terms become
@@ -516,7 +516,7 @@ __global__ void __launch_bounds__(1024)
     s_mask[tid] = 0;
     s_idx[tid] = (uint32_t)tid;  // entries past n sort last: mask 0, larger index
     __syncthreads();
-    if (tid < kHeavyTerms) {
+    if (tid < kSignTerms) {
         const int32_t t = heavy[tid];
         if (t >= 0) {
             uint32_t h = ((uint32_t)t * 2654435761u) >> 24;
@@ -1241,8 +1241,8 @@ __global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const
 // ---------------------------------------------------------------------- heavy terms on the MFMA units
 
 // The heavy terms (the index's GS_HEAVY_TERMS longest lists) hold most of the
-// postings a batch scores: at C3 the 64 of them carry 91% of the scored
-// postings, 32 of them 83%.  The hybrid search computes their part of every
+// postings a batch scores: at C3 the 64 longest lists carry 91% of the scored
+// postings, the 128 longest 96%.  The hybrid search computes their part of every
 // (query, doc) sum with int8 matrix products (k_head_scores) and starts each
 // LDS slice of k_score_union from it; the slices then take the other ("tail")
 // terms' postings as LDS adds.
@@ -1254,8 +1254,9 @@ __global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const
 // query's shift r and bounds the error).  With a_h = 128 ah + al and wq = 128 wh
 // + wl (al, wl in [0, 127], ah, wh signed bytes):
 //   sum_h a_h wq_h = sum al wl + 2^7 (sum al wh + sum ah wl) + 2^14 sum ah wh,
-// four v_mfma_i32_16x16x64_i8 per 16 docs x 16 queries over the 64 heavy terms,
-// each an exact int32 sum (|.| <= 64 * 128 * 128); the combination H is exact in
+// four chains of v_mfma_i32_16x16x64_i8 per 16 docs x 16 queries, one product
+// per 64 heavy terms in each, every one an exact int32 sum (|.| <= 2 * 256 * 128
+// * 128 = 2^23 for the middle one over 256 terms); the combination H is exact in
 // wrapping 32-bit arithmetic because it fits int32.  The slices start from
 // floor(H / 2^16) * 2^16, which is below H by less than 2^16: the margin grows
 // by 2^16 (k_query_prep_hybrid), so every doc that can reach the top k is still
@@ -1269,14 +1270,15 @@ typedef int32_t gs_v4i __attribute__((ext_vector_type(4)));
 // of 512-doc block b -- so that each workgroup writes one contiguous run, slots
 // 0..Bpad-1 (slots past B hold zero limbs); blocks past the head rows (docs
 // past the collection) hold zeros.  Eight waves, each holding its 4 blocks of
-// 16 docs as the A operand (lane: doc lane % 16, terms 16 (lane / 16) .. + 15,
-// two limbs) for every block of 16 slots (B operand: the query limbs, same lane
-// layout, loaded one block ahead).  A lane's 4 outputs are 4 consecutive docs
-// of one slot (rows 4 (lane / 16) + i, column lane % 16 of the 16x16 product);
-// they go to an LDS stage of the 16 slots' rows (double-buffered, rows padded
-// so that the 16 rows of a store fall in different banks), which the
-// workgroup then writes out as 16-byte pieces, one contiguous 16 KiB run per
-// block of slots.
+// 16 docs as the A operands (per 64 heavy terms: lane = doc lane % 16, terms
+// 16 (lane / 16) .. + 15, two limbs) for every block of 16 slots (B operands:
+// the query limbs, same lane layout, loaded one block ahead).  A lane's 4
+// outputs are 4 consecutive docs of one slot (rows 4 (lane / 16) + i, column
+// lane % 16 of the 16x16 product); they go to an LDS stage of the 16 slots'
+// rows (double-buffered, rows padded so that the 16 rows of a store fall in
+// different banks), which the workgroup then writes out as 16-byte pieces, one
+// contiguous 16 KiB run per block of slots.  (Each wave writing its own 64 docs
+// of the rows, with no workgroup barrier, measured slower.)
 constexpr int kHeadStageRow = kHeadBlock + 16;  // int16 per staged row (bank padding)
 
 __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ head, int64_t head_rows,
@@ -1284,6 +1286,7 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
                                                      const int32_t *__restrict__ hshift, int32_t B, int32_t Bpad,
                                                      int16_t *__restrict__ out) {
     constexpr int HT = kHeavyTerms;
+    constexpr int KB = HT / 64;               // 64-term blocks of the products
     constexpr int CPW = kHeadBlock / 16 / 8;  // blocks of 16 docs per wave
     __shared__ __align__(16) int16_t stage[2][16 * kHeadStageRow];
     const int lane = gs_lane(), tid = threadIdx.x;
@@ -1295,35 +1298,49 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
             reinterpret_cast<uint4 *>(ob)[i] = make_uint4(0, 0, 0, 0);
         return;
     }
-    gs_v4i dl[CPW], dh[CPW];
+    gs_v4i dl[CPW][KB], dh[CPW][KB];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
         const int8_t *hp = head + (doc0 + (wave * CPW + c) * 16 + (lane & 15)) * (2 * HT) + (lane >> 4) * 16;
-        dl[c] = *reinterpret_cast<const gs_v4i *>(hp);
-        dh[c] = *reinterpret_cast<const gs_v4i *>(hp + HT);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            dl[c][kb] = *reinterpret_cast<const gs_v4i *>(hp + kb * 64);
+            dh[c][kb] = *reinterpret_cast<const gs_v4i *>(hp + HT + kb * 64);
+        }
     }
-    auto load_q = [&](int rb, gs_v4i &ql, gs_v4i &qh, int &r) {
+    auto load_q = [&](int rb, gs_v4i (&ql)[KB], gs_v4i (&qh)[KB], int &r) {
         const int s = rb + (lane & 15);
         const int8_t *ap = alimb + (int64_t)s * (2 * HT) + (lane >> 4) * 16;
-        ql = *reinterpret_cast<const gs_v4i *>(ap);
-        qh = *reinterpret_cast<const gs_v4i *>(ap + HT);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            ql[kb] = *reinterpret_cast<const gs_v4i *>(ap + kb * 64);
+            qh[kb] = *reinterpret_cast<const gs_v4i *>(ap + HT + kb * 64);
+        }
         r = s < B ? hshift[s] : 0;
     };
-    gs_v4i ql, qh;
+    gs_v4i ql[KB], qh[KB];
     int r;
     load_q(0, ql, qh, r);
     for (int rb = 0, buf = 0; rb < Bpad; rb += 16, buf ^= 1) {
-        gs_v4i nl = ql, nh = qh;
+        gs_v4i nl[KB], nh[KB];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            nl[kb] = ql[kb];
+            nh[kb] = qh[kb];
+        }
         int nr = r;
         if (rb + 16 < Bpad) load_q(rb + 16, nl, nh, nr);
         int16_t *st = stage[buf];
 #pragma unroll
         for (int c = 0; c < CPW; ++c) {
-            const gs_v4i z = {0, 0, 0, 0};
-            const gs_v4i c00 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dl[c], ql, z, 0, 0, 0);
-            gs_v4i cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(dh[c], ql, z, 0, 0, 0);
-            cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(dl[c], qh, cm, 0, 0, 0);
-            const gs_v4i c11 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dh[c], qh, z, 0, 0, 0);
+            gs_v4i c00 = {0, 0, 0, 0}, cm = {0, 0, 0, 0}, c11 = {0, 0, 0, 0};
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                c00 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dl[c][kb], ql[kb], c00, 0, 0, 0);
+                cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(dh[c][kb], ql[kb], cm, 0, 0, 0);
+                cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(dl[c][kb], qh[kb], cm, 0, 0, 0);
+                c11 = __builtin_amdgcn_mfma_i32_16x16x64_i8(dh[c][kb], qh[kb], c11, 0, 0, 0);
+            }
             uint32_t w[2];
 #pragma unroll
             for (int i = 0; i < 4; i += 2) {
@@ -1344,8 +1361,11 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
             reinterpret_cast<uint4 *>(ob + (int64_t)(rb + row) * kHeadBlock)[col / 8] =
                 *reinterpret_cast<const uint4 *>(st + row * kHeadStageRow + col);
         }
-        ql = nl;
-        qh = nh;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            ql[kb] = nl[kb];
+            qh[kb] = nh[kb];
+        }
         r = nr;
     }
 }
@@ -1373,7 +1393,7 @@ template <int WT>
 __global__ void __launch_bounds__(256)
     k_query_prep_hybrid(const int32_t *__restrict__ qt, const void *__restrict__ qw, int32_t B, int32_t Bpad, int32_t T,
                         int32_t V, const float *__restrict__ max_abs, const int32_t *__restrict__ dup,
-                        const int8_t *__restrict__ hrank, int32_t pk_shift, float *__restrict__ scale,
+                        const int16_t *__restrict__ hrank, int32_t pk_shift, float *__restrict__ scale,
                         uint32_t *__restrict__ mfix, uint32_t *__restrict__ tau, uint32_t *__restrict__ cnt,
                         uint32_t *__restrict__ maxbin, int32_t *__restrict__ hshift, int8_t *__restrict__ alimb) {
     constexpr int HT = kHeavyTerms;
@@ -1383,14 +1403,15 @@ __global__ void __launch_bounds__(256)
     const int q = (int)((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6);
     const int lane = gs_lane();
     if (q >= Bpad) return;
-    s_hs[wv][lane] = 0.0f;
-    s_hn[wv][lane] = 0;
-    s_ha[wv][lane] = 0;
+    for (int h = lane; h < HT; h += 64) {
+        s_hs[wv][h] = 0.0f;
+        s_hn[wv][h] = 0;
+        s_ha[wv][h] = 0;
+    }
     gs_wave_sync();
     int8_t *lim = alimb + (int64_t)q * (2 * HT);
     if (q >= B) {
-        lim[lane] = 0;
-        lim[HT + lane] = 0;
+        for (int h = lane; h < 2 * HT; h += 64) lim[h] = 0;
         return;
     }
     if (lane == 0) {
@@ -1442,8 +1463,12 @@ __global__ void __launch_bounds__(256)
     // the largest |q| sum and occurrence count over the heavy terms; the fp32
     // sums are lifted by 1e-5 to cover their rounding (the limbs are checked
     // exactly below in any case)
-    double smax = (double)s_hs[wv][lane] * (1.0 + 1e-5);
-    int nmax = s_hn[wv][lane];
+    double smax = 0.0;
+    int nmax = 0;
+    for (int h = lane; h < HT; h += 64) {
+        smax = fmax(smax, (double)s_hs[wv][h] * (1.0 + 1e-5));
+        nmax = max(nmax, s_hn[wv][h]);
+    }
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
         smax = fmax(smax, __shfl_xor(smax, d, 64));
@@ -1483,10 +1508,17 @@ __global__ void __launch_bounds__(256)
         if (h >= 0) atomicAdd(&s_ha[wv][h], (int32_t)rintf(wrow[j] * hsc));
     }
     gs_wave_sync();
-    const int32_t av = s_ha[wv][lane];
-    ok = ok && __ballot(av > 16383 || av < -16384) == 0;
-    lim[lane] = ok ? (int8_t)(av & 127) : 0;
-    lim[HT + lane] = ok ? (int8_t)(av >> 7) : 0;
+    bool out_of_range = false;
+    for (int h = lane; h < HT; h += 64) {
+        const int32_t av = s_ha[wv][h];
+        out_of_range = out_of_range || av > 16383 || av < -16384;
+    }
+    ok = ok && __ballot(out_of_range) == 0;
+    for (int h = lane; h < HT; h += 64) {
+        const int32_t av = s_ha[wv][h];
+        lim[h] = ok ? (int8_t)(av & 127) : 0;
+        lim[HT + h] = ok ? (int8_t)(av >> 7) : 0;
+    }
     if (lane != 0) return;
     const double Ef = 0.5 * Bt + ldexp(Bh, r - 1) + 0.5 * Q * ldexp(1.0, f);  // fixed-point units
     // + 2^kHeadShift: the slices start from the heavy-term sums rounded down to a

@@ -57,7 +57,10 @@ class GsIndex(C.Structure):
         ("head_rank_d", C.c_void_p),
     ]
 
-HEAVY_TERMS = 64  # GS_HEAVY_TERMS
+def heavy_term_count() -> int:
+    """GS_HEAVY_TERMS of the loaded library (gs_heavy_term_count): the heavy
+    lists per index, and the hybrid search's matrix-product terms."""
+    return int(lib().gs_heavy_term_count())
 HEAD_BLOCK = 512  # GS_HEAD_BLOCK
 
 
@@ -114,6 +117,7 @@ class GsSearchPlanInfo(C.Structure):
 
 SIGNATURES = {
     "gs_query_version": (C.c_int, []),
+    "gs_heavy_term_count": (C.c_int, []),
     "gs_last_error": (C.c_char_p, []),
     "gs_index_count": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P]),
     "gs_index_fill_workspace": (_SZ, [_I64, _I32]),

@@ -355,11 +355,12 @@ def list_max_abs(index) -> torch.Tensor:
 
 
 def heavy_terms(index) -> torch.Tensor:
-    """The index's 64 longest posting lists (gs_heavy_terms), int32 term ids by
-    (length desc, term asc), -1 past the non-empty lists; gs_search groups the
-    queries of a batch by which of these terms they hold."""
+    """The index's heavy lists, its _lib.heavy_term_count() (64) longest posting
+    lists (gs_heavy_terms), int32 term ids by (length desc, term asc), -1 past the
+    non-empty lists; gs_search groups the queries of a batch by which of the first
+    64 they hold, and the hybrid search scores all of them as matrix products."""
     dev = _device_of(index)
-    out = torch.empty(_lib.HEAVY_TERMS, dtype=torch.int32, device=dev)
+    out = torch.empty(_lib.heavy_term_count(), dtype=torch.int32, device=dev)
     _lib.check(_lib.lib().gs_heavy_terms(_lib.ptr(index.lengths), int(index.vocab_size), _lib.ptr(out),
                                          _lib.stream_ptr(dev)), "gs_heavy_terms")
     return out
@@ -386,14 +387,14 @@ def hybrid_eligible(index) -> bool:
 
 def build_head(index):
     """Dense copy of the heavy terms' packed integer weights (gs_head_fill): int8
-    [num_docs rounded up to 512][2][64] limbs, and the [vocab] int8 heavy rank of
-    each term."""
+    [num_docs rounded up to 512][2][heavy terms] limbs, and the [vocab] int16 heavy
+    rank of each term (-1 for the others)."""
     a = index.aux()
     dev = _device_of(index)
     N, V = int(index.num_docs), int(index.vocab_size)
     n_rows = (N + _lib.HEAD_BLOCK - 1) // _lib.HEAD_BLOCK * _lib.HEAD_BLOCK
-    head = torch.empty((n_rows, 2, _lib.HEAVY_TERMS), dtype=torch.int8, device=dev)
-    rank = torch.empty(V, dtype=torch.int8, device=dev)
+    head = torch.empty((n_rows, 2, _lib.heavy_term_count()), dtype=torch.int8, device=dev)
+    rank = torch.empty(V, dtype=torch.int16, device=dev)
     _lib.check(_lib.lib().gs_head_fill(_lib.ptr(index.doc_ids), _lib.ptr(index.scores), index.wtype,
                                        _lib.ptr(index.offsets), _lib.ptr(index.lengths), V, _lib.ptr(a["heavy"]),
                                        pack_shift(index), N, n_rows, _lib.ptr(head), _lib.ptr(rank),

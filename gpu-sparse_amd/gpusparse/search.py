@@ -64,7 +64,7 @@ HYBRID_DEFAULT = True  # whether searches that name no scorer take the hybrid on
 
 
 def scorer_choice(index, tile_log2: int | None = None, hybrid: bool | None = None) -> tuple[int, bool]:
-    """(tile_log2, hybrid) of a search.  hybrid: whether the index's 64 longest
+    """(tile_log2, hybrid) of a search.  hybrid: whether the index's heavy (64 longest)
     lists are scored as int8 matrix products (the hybrid search) instead of LDS
     adds; None takes HYBRID_DEFAULT when the index allows it.  hybrid=True
     requires an eligible index (float weights, heavy lists without repeated
@@ -164,7 +164,7 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
     """Exact top-k of a query batch.  Returns ``(scores [B, k], ids [B, k] int64)``.
 
     tile_log2: doc-tile size of the scorer (default: index.default_tile_log2).
-    hybrid: the index's 64 longest lists as int8 matrix products, the other terms
+    hybrid: the index's heavy (64 longest) lists as int8 matrix products, the other terms
     as LDS adds (float indexes; scorer_choice); results are the same either way.
     path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense";
     k above MAX_K (8192) or queries wider than MAX_T (8192 terms) always take the

@@ -75,13 +75,20 @@ typedef struct gs_index {
                                      [n_docs rounded up to GS_HEAD_BLOCK][2][GS_HEAVY_TERMS]: with it
                                      (and the packed copy, float weights) gs_search runs the hybrid
                                      search -- heavy terms as int8 matrix products, the rest as LDS adds */
-    const int8_t *head_rank_d;    /* [vocab] h for term heavy_d[h], -1 for the others (gs_head_fill) */
+    const int16_t *head_rank_d;   /* [vocab] h for term heavy_d[h], -1 for the others (gs_head_fill) */
 } gs_index;
 
 /* Docs per block of the heavy-term products: head_d rows are padded to it. */
 #define GS_HEAD_BLOCK 512
 
+/* The heavy terms: the index's GS_HEAVY_TERMS longest lists (gs_heavy_terms).
+ * gs_search groups queries by the 64 most frequent of them; the hybrid search
+ * takes all of them as int8 matrix products.  64, 128 or 256;
+ * gs_heavy_term_count reports the value the library was built with. */
+#ifndef GS_HEAVY_TERMS
 #define GS_HEAVY_TERMS 64
+#endif
+int gs_heavy_term_count(void);
 
 /* Tuning knobs of gs_search; zero selects the default. */
 typedef struct gs_search_opts {
@@ -219,10 +226,10 @@ int gs_heavy_terms(const int32_t *lengths_d, int32_t vocab, int32_t *heavy_d, vo
  * and wq >> 7 (arithmetic) at [d][1][h]; 0 where doc d lacks the term.  The
  * heavy lists must hold each doc at most once (gs_check_lists dup = 0) and their
  * |wq| <= 16383 (w_shift from gs_pack_shift keeps every |wq| <= 8191).
- * head_rank_d int8 [vocab] <- h for heavy_d[h], -1 for other terms. */
+ * head_rank_d int16 [vocab] <- h for heavy_d[h], -1 for other terms. */
 int gs_head_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, const int64_t *offsets_d,
                  const int32_t *lengths_d, int32_t vocab, const int32_t *heavy_d, int32_t w_shift,
-                 int64_t n_docs, int64_t n_rows, int8_t *head_d, int8_t *head_rank_d, void *stream);
+                 int64_t n_docs, int64_t n_rows, int8_t *head_d, int16_t *head_rank_d, void *stream);
 /* Weight scale of a packed copy of float weights: the largest `shift` with
  * max_abs * 2^shift <= 8191, for max_abs = the largest |weight| of the index (0 for
  * max_abs == 0).  GS_EINVAL for a negative or non-finite max_abs. */

@@ -1,19 +1,19 @@
-"""GPU parity of the hybrid search: the index's 64 longest lists as int8 matrix
-products (MFMA, k_head_scores), whose coarse sums start the LDS slices of the
+"""GPU parity of the hybrid search: the index's heavy lists (its 64 longest) as
+int8 matrix products (MFMA, k_head_scores), whose coarse sums start the LDS slices of the
 other terms' adds, against the CPU oracle.
 
 Same bar as the other search tests: ids and scores bit-identical to the oracle
 (the fp64 scatter-add rounded to fp32).  The cases aim at what the hybrid adds:
 the dense head copy, the query limbs and shift (negative and repeated weights,
 limbs that do not fit), the coarse start and its margin, batches that are not a
-multiple of 16, blocks past the last doc, vocabularies with fewer than 64
-terms, every tile size."""
+multiple of 16, blocks past the last doc, vocabularies with fewer terms than
+the heavy set, every tile size."""
 import numpy as np
 import pytest
 import torch
 
 import gpusparse as gs
-from gpusparse import synth
+from gpusparse import _lib, synth
 from gpusparse.index import CSR, ensure_search_state
 from helpers import random_csr, random_queries
 from oracle import oracle as O
@@ -92,11 +92,11 @@ def test_head_copy_matches_oracle(device, dtype, n_docs):
     ensure_search_state(ix)
     head, rank = build_head(ix)
     ref = oracle_index(csr)
-    heavy = O.heavy_terms(ref["lengths"])
+    heavy = O.heavy_terms(ref["lengths"], _lib.heavy_term_count())
     n_rows = ((n_docs + 511) // 512) * 512
-    assert head.shape == (n_rows, 2, 64)
+    assert head.shape == (n_rows, 2, _lib.heavy_term_count()) and len(heavy) == _lib.heavy_term_count()
     assert np.array_equal(head.cpu().numpy(), O.head_limbs(ref, heavy, n_rows))
-    want_rank = np.full(400, -1, np.int8)
+    want_rank = np.full(400, -1, np.int16)
     want_rank[heavy[heavy >= 0]] = np.arange((heavy >= 0).sum())
     assert np.array_equal(rank.cpu().numpy(), want_rank)
 
@@ -131,7 +131,7 @@ def test_hybrid_negative_and_repeated_weights(device, dtype):
     ref = oracle_index(csr)
     ti, tw = zipf_queries(rng, 37, 500, np.float32, max_len=12)
     tw[::2, :4] *= -1
-    heavy = O.heavy_terms(ref["lengths"])
+    heavy = O.heavy_terms(ref["lengths"], _lib.heavy_term_count())
     ti = np.ascontiguousarray(np.concatenate([ti, np.tile(heavy[:3], (37, 1)), np.tile(heavy[:2], (37, 1))], axis=1))
     tw = np.ascontiguousarray(np.concatenate([tw, rng.uniform(-1, 2, (37, 5)).astype(np.float32)], axis=1))
     ti[5, :] = -1
@@ -152,7 +152,7 @@ def test_hybrid_large_repeated_heavy_weights(device):
     ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
     ti, tw = zipf_queries(rng, 20, 300, np.float32, max_len=10)
-    h0 = int(O.heavy_terms(ref["lengths"])[0])
+    h0 = int(O.heavy_terms(ref["lengths"], _lib.heavy_term_count())[0])
     extra_t = np.full((20, 40), -1, np.int32)
     extra_w = np.zeros((20, 40), np.float32)
     extra_t[::5] = h0
@@ -174,10 +174,11 @@ def test_hybrid_not_for_uint8(device):
         gs.search_plan(ix, 8, 10, 20, hybrid=True)
 
 
-@pytest.mark.parametrize("vocab", [20, 64, 70])
+@pytest.mark.parametrize("vocab", [20, 64, 70, 128, 134])
 def test_hybrid_small_vocabularies(device, vocab):
-    """Vocabularies of 20 and 64 terms: every term is heavy (no tail term at all;
-    unused heavy slots hold -1); 70: six tail terms."""
+    """Vocabularies of at most as many terms as the heavy set (64): every term is
+    heavy (no tail term at all; unused heavy slots hold -1); larger ones have
+    tail terms."""
     rng = np.random.default_rng(vocab)
     csr = zipf_csr(rng, 7000, vocab, np.float32, max_len=min(12, vocab))
     ix = gs.build_from_csr(csr, device)
@@ -196,7 +197,7 @@ def test_hybrid_many_tail_terms_and_large_entry_lists(device):
     csr = zipf_csr(rng, 30000, V, np.float32, max_len=60, s=0.9)
     ix = gs.build_from_csr(csr, device)
     ref = oracle_index(csr)
-    heavy = set(O.heavy_terms(ref["lengths"]).tolist())
+    heavy = set(O.heavy_terms(ref["lengths"], _lib.heavy_term_count()).tolist())
     tail = np.array([t for t in range(V) if t not in heavy], np.int32)
     B = 40
     ti = np.stack([rng.choice(tail, 150, replace=False) for _ in range(B)]).astype(np.int32)

@@ -512,14 +512,16 @@ def test_search_plan_reports_defaults(c1, c3_small):
     assert gs.search_plan(ix16, 24, ti16.shape[1], 1000, sample_tiles=3, unroll=4)["seed_tiles"] == 3
 
 
-@pytest.mark.parametrize("vocab,seed", [(20, 0), (65, 1), (3000, 2), (30522, 3)])
+@pytest.mark.parametrize("vocab,seed", [(20, 0), (65, 1), (129, 4), (200, 5), (3000, 2), (30522, 3)])
 def test_heavy_terms_matches_oracle(device, vocab, seed):
     from gpusparse.index import heavy_terms
     rng = np.random.default_rng(seed)
     print(f"heavy terms vocab={vocab}", flush=True)
     csr = random_csr(rng, 4000, vocab, max_len=12, dtype=np.float32)
     ix = gs.build_from_csr(csr, device)
-    assert np.array_equal(heavy_terms(ix).cpu().numpy(), O.heavy_terms(ix.lengths.cpu().numpy()))
+    from gpusparse import _lib
+    assert np.array_equal(heavy_terms(ix).cpu().numpy(), O.heavy_terms(ix.lengths.cpu().numpy(),
+                                                                        _lib.heavy_term_count()))
 
 
 @pytest.mark.parametrize("B,k", [(24, 1000), (7, 10)])

@@ -104,16 +104,17 @@ def test_tile_bounds_match_linear_scan(tile_log2):
             assert tb[t, j] == next((i for i, d in enumerate(seg) if d >= edge), n)
 
 
-@pytest.mark.parametrize("vocab,seed", [(20, 0), (64, 1), (65, 2), (3000, 3), (30522, 4)])
-def test_heavy_terms_matches_sorted(vocab, seed):
+@pytest.mark.parametrize("n", [64, 128])
+@pytest.mark.parametrize("vocab,seed", [(20, 0), (64, 1), (65, 2), (128, 5), (129, 6), (3000, 3), (30522, 4)])
+def test_heavy_terms_matches_sorted(vocab, seed, n):
     """Ties of equal length (lengths drawn from a few values) and empty lists."""
     rng = np.random.default_rng(seed)
     lengths = rng.choice([0, 0, 1, 2, 3, 7, 7, 50], size=vocab).astype(np.int32)
     if vocab > 100:
         lengths[rng.choice(vocab, 90, replace=False)] = rng.integers(100, 130, 90)
-    want = [t for t in sorted(range(vocab), key=lambda t: (-int(lengths[t]), t)) if lengths[t] > 0][:64]
-    got = O.heavy_terms(lengths)
-    assert got.tolist() == want + [-1] * (64 - len(want))
+    want = [t for t in sorted(range(vocab), key=lambda t: (-int(lengths[t]), t)) if lengths[t] > 0][:n]
+    got = O.heavy_terms(lengths, n)
+    assert got.tolist() == want + [-1] * (n - len(want))
 
 
 @pytest.mark.parametrize("max_abs,want", [(1.0, 12), (3.0, 11), (8191.0, 0), (8192.0, -1), (0.5, 13),
@@ -169,7 +170,7 @@ def test_head_limbs_recombine_to_packed_weights(dtype):
     rec = 128 * hi + lo
     w64 = csr.data.astype(np.float64)
     shift = 0 if dtype == np.uint8 else O.pack_shift(float(np.abs(w64).max()))
-    want = np.zeros((3072, 64), np.int64)
+    want = np.zeros((3072, len(heavy)), np.int64)
     rows = np.repeat(np.arange(3000), np.diff(csr.indptr))
     col_of = {int(t): h for h, t in enumerate(heavy) if t >= 0}
     for r, t, w in zip(rows, csr.indices, w64):
