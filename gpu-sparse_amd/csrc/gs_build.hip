@@ -709,11 +709,15 @@ __global__ void k_pack_postings(const int32_t *__restrict__ doc, const void *__r
 // groups only.  The postings of one residue land in different groups while
 // they last, so a group holds a residue ceil(count / G) times at most (2 for
 // random docs), where docs in ascending order pile 3-5 lanes onto one bank.
-// One thread per (term, tile); its wave rewrites the wave's sub-ranges of more
-// than 64 postings one after the other: a pass counting residues, then a pass
-// that ranks each posting among its residue (64-lane ballot match plus the
-// wave's running counts) and writes its word to its place.
+// One wave per kArrangeTiles tiles of one term (lane j < kArrangeTiles holds
+// tile j's sub-range); the wave rewrites its sub-ranges of more than 64
+// postings one after the other: a pass counting residues, then a pass that
+// ranks each posting among its residue (64-lane ballot match plus the wave's
+// running counts) and writes its word to its place.  Few tiles per wave keep
+// a long list's work spread over many waves (with 64 tiles per wave a head
+// term's waves ran long after the rest had finished).
 constexpr int kArrangeUnroll = 4;  // 64-posting groups loaded together per lane
+constexpr int kArrangeTiles = 8;   // tiles of one term per wave
 
 template <int WT>
 __global__ void __launch_bounds__(256)
@@ -723,14 +727,17 @@ __global__ void __launch_bounds__(256)
     __shared__ uint32_t s_cnt[4][64], s_run[4][64], s_below[4][64];
     const int lane = gs_lane(), wave = threadIdx.x >> 6;
     const uint32_t mask = (1u << tile_log2) - 1u;
-    const int64_t g = blockIdx.x * 256ll + threadIdx.x;
+    const int64_t per_term = (n_tiles + kArrangeTiles - 1) / kArrangeTiles;  // waves per term
+    const int64_t gw = blockIdx.x * 4ll + wave;                               // this wave
     int64_t s = 0;
     int n = 0;
-    if (g < (int64_t)V * n_tiles) {
-        const int64_t t = g / n_tiles, j = g - t * n_tiles;
-        const int32_t *b = tb + t * (n_tiles + 1) + j;
-        n = b[1] - b[0];
-        s = offsets[t] + b[0];
+    if (gw < (int64_t)V * per_term && lane < kArrangeTiles) {
+        const int64_t t = gw / per_term, j = (gw - t * per_term) * kArrangeTiles + lane;
+        if (j < n_tiles) {
+            const int32_t *b = tb + t * (n_tiles + 1) + j;
+            n = b[1] - b[0];
+            s = offsets[t] + b[0];
+        }
     }
     uint64_t todo = __ballot(n > 64);
     while (todo) {
@@ -1404,8 +1411,9 @@ extern "C" int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d,
     uint32_t *out = reinterpret_cast<uint32_t *>(out_d);
     const int64_t n_tiles = (n_docs + (1ll << tile_log2) - 1) >> tile_log2;
     const int64_t pairs = (int64_t)vocab * n_tiles;
-    GS_REQUIRE(!tile_bounds_d || pairs <= (int64_t)256 * 0x7FFFFFFF, "too many (term, tile) pairs");
-    const unsigned ga = (unsigned)((pairs + 255) / 256);
+    const int64_t arrange_waves = (int64_t)vocab * ((n_tiles + kArrangeTiles - 1) / kArrangeTiles);
+    GS_REQUIRE(!tile_bounds_d || arrange_waves <= (int64_t)4 * 0x7FFFFFFF, "too many (term, tile) pairs");
+    const unsigned ga = (unsigned)((arrange_waves + 3) / 4);
     switch (wtype) {
         case GS_W_F32:
             k_pack_postings<GS_W_F32><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, w_shift, out);

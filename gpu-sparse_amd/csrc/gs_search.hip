@@ -1278,7 +1278,9 @@ typedef int32_t gs_v4i __attribute__((ext_vector_type(4)));
 // rows (double-buffered, rows padded so that the 16 rows of a store fall in
 // different banks), which the workgroup then writes out as 16-byte pieces, one
 // contiguous 16 KiB run per block of slots.  (Each wave writing its own 64 docs
-// of the rows, with no workgroup barrier, measured slower.)
+// of the rows, with no workgroup barrier, measured slower; so did int8 coarse
+// sums with a per-query shift: half the bytes, but their wider margin costs the
+// scorer and the rescoring more than the writes save.)
 constexpr int kHeadStageRow = kHeadBlock + 16;  // int16 per staged row (bank padding)
 
 __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ head, int64_t head_rows,
