@@ -57,10 +57,13 @@ class GsIndex(C.Structure):
         ("head_rank_d", C.c_void_p),
     ]
 
+
 def heavy_term_count() -> int:
     """GS_HEAVY_TERMS of the loaded library (gs_heavy_term_count): the heavy
     lists per index, and the hybrid search's matrix-product terms."""
     return int(lib().gs_heavy_term_count())
+
+
 HEAD_BLOCK = 512  # GS_HEAD_BLOCK
 
 

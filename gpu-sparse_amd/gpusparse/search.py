@@ -13,6 +13,8 @@ float32; uint8 indexes return the exact uint32 sums as int32.
 """
 from __future__ import annotations
 
+from collections import OrderedDict
+
 import numpy as np
 import torch
 
@@ -30,33 +32,56 @@ def _check_pow2(block_pl: int) -> None:
         f"block_pl must be a positive power of 2, got {block_pl}"
 
 
-def query_tensors(index, query_batch):
+_U8_WEIGHTS_MSG = "a uint8 index takes uint8 query weights: float weights must be integers in [0, 255]"
+
+
+def query_tensors(index, query_batch, defer_check: bool = False):
     """(term ids int32 [B, T], weights [B, T]) on the index device, from a tuple of
-    tensors/arrays or from a query CSR (no truncation, as to_query_tensors)."""
+    tensors/arrays or from a query CSR (no truncation, as to_query_tensors; a
+    uint8 CSR stays uint8).
+
+    A uint8 index takes float query weights (the reference's query tensors are
+    float32, gpusparse_retrieval.py:124) when every one is an integer in
+    [0, 255]: the uint8 impacts they carry.  Weights in host memory are checked
+    on the host before the upload.  Weights already on the GPU are checked there;
+    reading that check waits for the GPU, so with `defer_check` it is returned
+    instead, as a third item (a device bool, True when a weight fails; None when
+    nothing was checked on the GPU), for the caller to read with its results."""
     dev = _device_of(index)
     if isinstance(query_batch, tuple) and len(query_batch) in (2, 3) and not hasattr(query_batch, "indptr"):
         qt, qw = query_batch[0], query_batch[1]
     else:
         from .engine import to_query_tensors
-        qt, qw, _ = to_query_tensors(query_batch, dev)
-    qt = torch.as_tensor(qt).to(dev)
-    qw = torch.as_tensor(qw).to(dev)
+        qt, qw, _ = to_query_tensors(query_batch, dev, weight_dtype=None)
+    qt = torch.as_tensor(qt)
+    qw = torch.as_tensor(qw)
     if qt.dim() != 2 or qw.shape != qt.shape:
         raise ValueError(f"query term ids {tuple(qt.shape)} and weights {tuple(qw.shape)} must be the same [B, T]")
+    want = torch.uint8 if index.scores.dtype == torch.uint8 else torch.float32
+    bad = None
+    if qw.dtype != want and want == torch.uint8:
+        if not (qw.dtype.is_floating_point or qw.dtype in (torch.int16, torch.int32, torch.int64)):
+            raise ValueError(f"a uint8 index takes uint8 query weights, got {qw.dtype}")
+        if qw.numel():
+            if qw.device.type == "cpu":
+                h = qw.double().numpy()
+                if not bool(np.all((h >= 0) & (h <= 255) & (h == np.round(h)))):
+                    raise ValueError(_U8_WEIGHTS_MSG)
+            else:
+                qd = qw.to(dev)
+                bad = ~((qd >= 0) & (qd <= 255) & (qd == torch.round(qd.double()))).all()
+                if not defer_check:
+                    if bool(bad):
+                        raise ValueError(_U8_WEIGHTS_MSG)
+                    bad = None
+    qt = qt.to(dev)
+    qw = qw.to(dev)
     if qt.dtype != torch.int32:
         qt = qt.to(torch.int32)
-    want = torch.uint8 if index.scores.dtype == torch.uint8 else torch.float32
     if qw.dtype != want:
-        if want == torch.uint8:
-            # float query weights (the reference's query tensors are float32,
-            # gpusparse_retrieval.py:124) are taken when every one is an integer
-            # in [0, 255]: the uint8 impacts they carry
-            if not (qw.dtype.is_floating_point or qw.dtype in (torch.int16, torch.int32, torch.int64)):
-                raise ValueError(f"a uint8 index takes uint8 query weights, got {qw.dtype}")
-            ok = bool(((qw >= 0) & (qw <= 255) & (qw == torch.round(qw.double()))).all()) if qw.numel() else True
-            if not ok:
-                raise ValueError("a uint8 index takes uint8 query weights: float weights must be integers in [0, 255]")
         qw = qw.to(want)
+    if defer_check:
+        return qt.contiguous(), qw.contiguous(), bad
     return qt.contiguous(), qw.contiguous()
 
 
@@ -84,19 +109,26 @@ def _opts(sample_tiles=0, cand_cap=0, unroll=0, waves=0, tiles_per_wg=0, batch_o
     return o
 
 
+WORKSPACE_STREAMS = 4  # streams whose fused-search workspaces an index keeps
+
+
 def _workspace(index, nbytes: int, stream_key: int = 0) -> torch.Tensor:
     """The index's fused-search workspace for one stream (searches in flight on
     different streams must not share one; on one stream they run in order).  The
-    one last handed out is also aux()["workspace"], which search_counts reads."""
+    index keeps those of its WORKSPACE_STREAMS most recently used streams (a
+    dropped one is freed once the searches queued with it are done: the
+    allocator orders its reuse on its stream).  The one last handed out is also
+    aux()["workspace"], which search_counts reads."""
     a = index.aux()
-    pool = a.setdefault("workspaces", {})
+    pool = a.setdefault("workspaces", OrderedDict())
     ws = pool.get(stream_key)
     if ws is None or ws.numel() < nbytes:
-        pool.pop(stream_key, None)
-        if a.get("workspace") is ws:
-            a.pop("workspace", None)
+        pool.pop(stream_key, None)  # a smaller one is replaced, not kept beside it
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=_device_of(index))
         pool[stream_key] = ws
+    pool.move_to_end(stream_key)
+    while len(pool) > WORKSPACE_STREAMS:
+        pool.popitem(last=False)
     a["workspace"] = ws
     return ws
 
@@ -198,7 +230,7 @@ def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = Non
     kk = min(int(k), N)
     if kk < 1:
         raise ValueError(f"k must be >= 1, got {k}")
-    qt, qw = query_tensors(index, query_batch)
+    qt, qw, bad_w = query_tensors(index, query_batch, defer_check=True)
     B, T = qt.shape
     out_dtype = torch.int32 if index.scores.dtype == torch.uint8 else torch.float32
     out_s = torch.empty((B, kk), dtype=out_dtype, device=dev)
@@ -221,6 +253,8 @@ def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = Non
     # selection takes any k (rounds of MAX_K) and whose scorer any width
     use_dense = path == "dense" or kk > MAX_K or T > MAX_T or (path == "auto" and dense_bytes <= dense_budget)
     if use_dense:
+        if bad_w is not None and bool(bad_w):
+            raise ValueError(_U8_WEIGHTS_MSG)
         _dense_rows(index, gidx, qt, qw, kk, None, out_s, out_i, max(dense_budget, 1))
         return PendingSearch((out_s, out_i), stream)
     opts = _opts(sample_tiles, cand_cap, unroll, waves, tiles_per_wg, batch_order, hyb)
@@ -249,10 +283,16 @@ def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = Non
             timing.setdefault("phases", []).append(ph)
     status_h = torch.empty(B, dtype=torch.int32, pin_memory=True)
     status_h.copy_(status, non_blocking=True)
+    bad_h = None
+    if bad_w is not None:  # the weights' check, read with the status
+        bad_h = torch.empty((), dtype=torch.bool, pin_memory=True)
+        bad_h.copy_(bad_w, non_blocking=True)
     done = torch.cuda.Event()
     done.record(stream)
 
     def finish(bad):
+        if bad_h is not None and bool(bad_h):
+            raise ValueError(_U8_WEIGHTS_MSG)
         if timing is not None:
             timing["dense_rows"] = timing.get("dense_rows", 0) + int(bad.size)
         if bad.size:

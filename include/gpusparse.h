@@ -283,6 +283,10 @@ int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_wei
  * with cand_cap <= 32768, and B <= 256 fits at the default caps (the hybrid search
  * needs 2 bytes more per query slot and doc, for its coarse heavy-term sums).  The scratch
  * keeps the last call's contents; every call clears what it needs cleared.
+ * The first call on each device looks up the array's device address
+ * (hipGetSymbolAddress): make it outside stream capture.  Later calls record
+ * no memset and no allocation or synchronisation, so they can be captured into
+ * a HIP graph and replayed (tests/test_zz_no_alloc.py replays one).
  * Calls that overlap on one GPU (other threads, other streams) share that GPU's
  * array and race: serialise them.  Allocates nothing and does not synchronise. */
 #define GS_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)

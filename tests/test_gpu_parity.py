@@ -843,6 +843,16 @@ def test_reference_builders_store_float32(device, dtype):
         assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
         with pytest.raises(ValueError, match="integers"):
             gs.search(native, (torch.from_numpy(ti), torch.from_numpy(tw + 0.5)), 20)
+        # weights already on the GPU: the same answer, and the same error, which
+        # search_async defers to result() (its launches do not wait for the check)
+        s2, i2 = gs.search(native, (torch.from_numpy(ti).cuda(), torch.from_numpy(tw).cuda()), 20, path="fused")
+        assert np.array_equal(i2.cpu().numpy(), vi) and np.array_equal(s2.cpu().numpy(), vs)
+        pend = gs.search_async(native, (torch.from_numpy(ti).cuda(), torch.from_numpy(tw + 0.5).cuda()), 20,
+                               path="fused")
+        with pytest.raises(ValueError, match="integers"):
+            pend.result()
+        with pytest.raises(ValueError, match="integers"):
+            gs.search(native, (torch.from_numpy(ti).cuda(), torch.from_numpy(tw - 300).cuda()), 20, path="dense")
 
 
 def test_retrieve_and_run_engine(device, tmp_path):

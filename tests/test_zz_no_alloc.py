@@ -87,3 +87,66 @@ def test_noalloc_refuses_searches_beyond_its_scratch(device):
                              oi.data_ptr(), st.data_ptr(), _lib.stream_ptr(device))
     assert rc == _lib.GS_ENOSPC
     assert b"allocation-free" in L.gs_last_error()
+
+
+def test_noalloc_replays_from_a_hip_graph(device):
+    """After one eager call on the device (which looks up the scratch array's
+    address), a gs_search_noalloc call captured into a HIP graph replays to
+    gs_search's answer, replay after replay, with eager searches (one of them
+    allocation-free, sharing the scratch) and synchronisations in between."""
+    cfg = synth.scaled(synth.CONFIGS["C1"], n_docs=150_000, n_queries=48)
+    docs, queries = synth.generate(cfg)
+    ix = gs.build_from_csr(docs, device)
+    qt, qw, _ = gs.to_query_tensors(queries, device, weight_dtype=None)
+    B, T = qt.shape
+    k = 100
+    L = _lib.lib()
+    tile, hyb = scorer_choice(ix, None, None)
+    gidx = gs_index_struct(ix, tile, hybrid=hyb)
+    opts = _lib.GsSearchOpts()
+    print(f"graph replay: B={B} k={k} hybrid={hyb}", flush=True)
+    need = C.c_size_t()
+    _lib.check(L.gs_search_workspace(C.byref(gidx), B, T, k, C.byref(opts), C.byref(need)), "gs_search_workspace")
+    ws = torch.empty(int(need.value), dtype=torch.uint8, device=device)
+    rs = torch.empty((B, k), dtype=torch.float32, device=device)
+    ri = torch.empty((B, k), dtype=torch.int64, device=device)
+    rst = torch.empty(B, dtype=torch.int32, device=device)
+    _lib.check(L.gs_search(C.byref(gidx), qt.data_ptr(), qw.data_ptr(), B, T, k, C.byref(opts), rs.data_ptr(),
+                           ri.data_ptr(), rst.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(device)),
+               "gs_search")
+    torch.cuda.synchronize(device)
+    want = (rs.cpu().numpy(), ri.cpu().numpy(), rst.cpu().numpy())
+    assert (want[2] == _lib.GS_ROW_DONE).all()
+    os_ = torch.empty((B, k), dtype=torch.float32, device=device)
+    oi = torch.empty((B, k), dtype=torch.int64, device=device)
+    st = torch.empty(B, dtype=torch.int32, device=device)
+
+    def call(stream_ptr, b=B):
+        return L.gs_search_noalloc(C.byref(gidx), qt.data_ptr(), qw.data_ptr(), b, T, k, C.byref(opts),
+                                   os_.data_ptr(), oi.data_ptr(), st.data_ptr(), stream_ptr)
+
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        _lib.check(call(side.cuda_stream), "gs_search_noalloc")  # eager: scratch address looked up here
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side, capture_error_mode="relaxed"):
+        rc = call(torch.cuda.current_stream(device).cuda_stream)
+    _lib.check(rc, "gs_search_noalloc under capture")
+    for rep in range(3):
+        os_.fill_(-7.0)
+        oi.fill_(-7)
+        st.fill_(-7)
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        got = (os_.cpu().numpy(), oi.cpu().numpy(), st.cpu().numpy())
+        assert np.array_equal(got[2], want[2]), rep
+        assert np.array_equal(got[1], want[1]), rep
+        assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32)), rep
+        # eager work between the replays: a smaller allocation-free search (same
+        # scratch, same outputs' first rows) and a regular one
+        _lib.check(call(_lib.stream_ptr(device), b=B // 3), "gs_search_noalloc")
+        gs.search(ix, (qt[:7], qw[:7]), 20)
+        torch.cuda.synchronize(device)
