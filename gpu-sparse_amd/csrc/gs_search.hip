@@ -2014,7 +2014,7 @@ int check_index(const gs_index *ix) {
     GS_REQUIRE(ix, "null index");
     GS_REQUIRE(ix->wtype >= GS_W_F32 && ix->wtype <= GS_W_U8, "unknown weight type %d", ix->wtype);
     GS_REQUIRE(ix->vocab > 0 && ix->n_docs > 0 && ix->n_docs < 0x7FFFFFFFll, "bad index sizes");
-    GS_REQUIRE(ix->tile_log2 >= 8 && ix->tile_log2 <= 13, "tile_log2 %d outside [8, 13]", ix->tile_log2);
+    GS_REQUIRE(ix->tile_log2 >= 8 && ix->tile_log2 <= 14, "tile_log2 %d outside [8, 14]", ix->tile_log2);
     GS_REQUIRE(ix->n_tiles == (int32_t)((ix->n_docs + (1ll << ix->tile_log2) - 1) >> ix->tile_log2),
                "n_tiles %d inconsistent with n_docs and tile_log2", ix->n_tiles);
     GS_REQUIRE(ix->doc_ids_d && ix->weights_d && ix->offsets_d && ix->max_abs_d && ix->dup_d && ix->tile_bounds_d,

@@ -29,6 +29,7 @@ BLOCK_SIZE = 32          # posting lists are padded to a multiple of this (gpu_i
 VOCAB_SIZE = 30522       # fixed vocabulary of the harness builder (run_correctness_verification.py:28)
 DEFAULT_TILE_LOG2 = 12          # 4096 docs per LDS tile: postings read from the index arrays
 DEFAULT_TILE_LOG2_PACKED = 13   # 8192 docs per LDS tile: postings read from the packed copy
+DEFAULT_TILE_LOG2_HYBRID = 14   # 16384 docs per LDS tile, one query each: the hybrid search
 
 
 def default_tile_log2(index) -> int:

@@ -19,7 +19,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .index import default_tile_log2, gs_index_struct, hybrid_eligible, _device_of
+from .index import DEFAULT_TILE_LOG2_HYBRID, default_tile_log2, gs_index_struct, hybrid_eligible, _device_of
 
 MAX_K = 8192  # largest k of the fused path and of compacted_topk; search answers larger k densely
 MAX_T = 8192  # widest query batch of the fused path (terms per query); search answers wider ones densely
@@ -93,13 +93,19 @@ def scorer_choice(index, tile_log2: int | None = None, hybrid: bool | None = Non
     lists are scored as int8 matrix products (the hybrid search) instead of LDS
     adds; None takes HYBRID_DEFAULT when the index allows it.  hybrid=True
     requires an eligible index (float weights, heavy lists without repeated
-    docs).  tile_log2 defaults to index.default_tile_log2."""
+    docs).  tile_log2 defaults to DEFAULT_TILE_LOG2_HYBRID (16384 docs, one query
+    per workgroup) for the hybrid search and to index.default_tile_log2 (8192
+    docs, two queries) otherwise: the terms left to the LDS adds of the hybrid
+    search are rarely shared by the queries of a group, while longer runs per
+    (term, tile) halve the per-run work (C3 scoring 5.68 vs 6.24 ms)."""
     if hybrid is None:
         hybrid = HYBRID_DEFAULT and hybrid_eligible(index)
     if hybrid and not hybrid_eligible(index):
         raise ValueError("the hybrid search needs float weights with finite values and heavy lists without "
                          "repeated docs")
-    return (default_tile_log2(index) if tile_log2 is None else int(tile_log2)), bool(hybrid)
+    if tile_log2 is None:
+        tile_log2 = DEFAULT_TILE_LOG2_HYBRID if hybrid else default_tile_log2(index)
+    return int(tile_log2), bool(hybrid)
 
 
 def _opts(sample_tiles=0, cand_cap=0, unroll=0, waves=0, tiles_per_wg=0, batch_order=False, hybrid=False):

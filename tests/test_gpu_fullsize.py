@@ -101,12 +101,13 @@ def test_c4_full_index(device):
 
 
 @pytest.mark.parametrize("tile_log2,hybrid", [(None, None), (None, False), (8, True), (8, False), (10, None),
-                                              (12, None)])
+                                              (12, None), (13, True)])
 def test_c4_full_search(device, tile_log2, hybrid):
     """1M docs whose top-50 terms each hold > 200K postings (dense in every tile):
     the head-heavy case of the scorer, every row of the 512-query batch, over the
-    tile sweep (256, 1K, 4K and the default 8K docs); at 256-doc tiles 32 queries
-    share a workgroup, with and without the heavy terms as matrix products."""
+    tile sweep (256, 1K, 4K, 8K docs and the defaults: 16K for the hybrid search,
+    8K for the LDS-only one); at 256-doc tiles 32 queries share a workgroup, with
+    and without the heavy terms as matrix products."""
     check_search("C4", device, 1000, tile_log2=tile_log2, hybrid=hybrid)
 
 

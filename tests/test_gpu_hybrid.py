@@ -208,7 +208,7 @@ def test_hybrid_many_tail_terms_and_large_entry_lists(device):
     check(ix, ref, ti, tw, 200)
 
 
-@pytest.mark.parametrize("tile_log2", [None, 8, 9])
+@pytest.mark.parametrize("tile_log2", [None, 8, 9, 13])
 @pytest.mark.parametrize("n_docs", [300, 512, 513, 1100, 2600])
 def test_hybrid_tiles_past_the_docs(device, n_docs, tile_log2):
     """Collections of less than one 512-doc block to a few: blocks past the head
@@ -227,8 +227,8 @@ def test_hybrid_tiles_past_the_docs(device, n_docs, tile_log2):
         ix.aux()["workspace"].fill_(0xCD)
 
 
-@pytest.mark.parametrize("tile_log2,tiles_per_wg,sample_tiles", [(13, 1, 0), (12, 2, 1), (10, 7, 3), (8, 64, 0),
-                                                                  (9, 0, 0)])
+@pytest.mark.parametrize("tile_log2,tiles_per_wg,sample_tiles", [(14, 3, 0), (14, 1, 2), (13, 1, 0), (12, 2, 1),
+                                                                  (10, 7, 3), (8, 64, 0), (9, 0, 0)])
 def test_hybrid_launch_shapes_and_dirty_workspace(device, tile_log2, tiles_per_wg, sample_tiles):
     """Every tile size (groups of 2 to 32 queries), several tiles per workgroup,
     seed launches of 1 and 3 tiles, and a workspace filled with garbage before

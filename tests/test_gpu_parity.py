@@ -311,7 +311,7 @@ def test_search_c1(c1, path, hybrid, k):
     assert_search_equal(ix, ref, ti, tw, k, path=path, hybrid=hybrid)
 
 
-@pytest.mark.parametrize("tile_log2", [8, 10, 13])
+@pytest.mark.parametrize("tile_log2", [8, 10, 13, 14])
 def test_search_c1_tile_sizes(c1, tile_log2):
     ix, ref, ti, tw = c1
     print(f"search C1 tile_log2={tile_log2}", flush=True)
@@ -493,12 +493,13 @@ def test_search_packed_launch_shapes(c3_small, unroll, tile_log2, tiles_per_wg):
 
 
 def test_search_plan_reports_defaults(c1, c3_small):
-    """The plan of the fused search: the packed copy in 8192-doc tiles, 16 postings
-    per lane per chunk, 2 queries per group (64 KiB of LDS), with or without the
-    heavy terms as matrix products (hybrid)."""
+    """The plan of the fused search: the packed copy, 16 postings per lane per
+    chunk, 64 KiB of LDS slices: 8192-doc tiles and 2 queries per group for the
+    LDS-only search, 16384-doc tiles and one query for the hybrid one (heavy terms
+    as matrix products)."""
     ix32, _, ti, _ = c1
     h = gs.search_plan(ix32, 32, ti.shape[1], 100, hybrid=True)
-    assert h["hybrid"] and h["tile_log2"] == 13 and h["packed"] and h["group_size"] == 2
+    assert h["hybrid"] and h["tile_log2"] == 14 and h["packed"] and h["group_size"] == 1
     assert gs.search_plan(ix32, 32, ti.shape[1], 100)["hybrid"] == HYBRID_DEFAULT
     p32 = gs.search_plan(ix32, 32, ti.shape[1], 100, hybrid=False)
     assert not p32["hybrid"]
