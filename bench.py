@@ -25,8 +25,9 @@ the device index build.  ``cpu_baseline`` times the reference CPU path
 (cpu_sequential_score, restated in C) on a bounded sample of the same batch in
 fresh child processes pinned with taskset and the thread-pool variables.
 ``workloads`` holds, from the same run, C3 at B = 16, 64, 256 and 1024, C3 at
-k = 10, and C5 (uint8) at B = 512; with the CPU leg the whole batch of the
-headline, of k = 10 and of C5 is checked against the C oracle.
+k = 10, and C5 (uint8) at B = 512 (measured by a child bench.py process); with
+the CPU leg the whole batch of the headline, of k = 10 and of C5 is checked
+against the C oracle.
 """
 from __future__ import annotations
 
@@ -162,9 +163,13 @@ def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
     f, w = last("f", "k_score_union"), last("w", "k_score_union")
     cf, cw = last("cf", "copyBuffer"), last("cw", "copyBuffer")
     fs, ws = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
-    # the hybrid search's heavy-term kernel, when the profiled run took it
+    # the hybrid search's heavy-term kernel, when the profiled run took it (then
+    # at the hybrid search's default tile, unless one was named)
     hf, hw = last("f", "k_head_scores", False), last("w", "k_head_scores", False)
     hybrid = hf is not None and hw is not None
+    if tile_log2 is None:
+        from gpusparse.index import DEFAULT_TILE_LOG2_HYBRID, DEFAULT_TILE_LOG2_PACKED
+        tile_log2 = DEFAULT_TILE_LOG2_HYBRID if hybrid else DEFAULT_TILE_LOG2_PACKED
     # the radix passes of the index build (term keys) and of the doc-major copy
     # (doc-id keys), in launch order: a histogram, then a scatter, per pass
     rf, rw = dispatches("f", ("k_rs_hist", "k_rs_scatter")), dispatches("w", ("k_rs_hist", "k_rs_scatter"))
@@ -343,14 +348,21 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
     """(roofline of the fused LDS scoring kernel, plan, roofline of the heavy-term
     kernel or None).
 
-    The LDS scorer's unit of work is one LDS atomic add: one scored posting (a
-    (query, posting) pair of a valid query term; with the hybrid search only the
-    terms outside the heavy ones), so the LDS-atomic issue rate bounds it, not
-    HBM (each posting is fetched once per doc tile and query group and added to
-    every query of the group holding its term).  The heavy-term kernel reads the
-    heavy terms' int8 doc rows (128 B per doc) once and writes one int16 coarse
-    sum per (query slot, doc): HBM-bound; its int8 MFMA work (4 limb products of
-    64 terms per (slot, doc), 512 ops) is given beside it."""
+    LDS-only search: the scorer's unit of work is one LDS atomic add, one scored
+    posting (a (query, posting) pair of a valid query term), so the LDS-atomic
+    issue rate bounds it, not HBM (each posting is fetched once per doc tile and
+    query group and added to every query of the group holding its term).
+    Hybrid search: the heavy terms' part of every (query, doc) sum arrives as an
+    int16 coarse sum, and the other ("tail") terms are added in LDS, about a
+    tenth of the scored postings.  The scorer then streams its inputs: per
+    launch it reads the coarse sums of its tiles (2 B per (query, doc)) and, per
+    query group and tile, the packed words of the group's tail terms (4 B per
+    posting and group holding the term); those algorithmic bytes over its time,
+    against the HBM peak, are its roofline, with the LDS-atomic rate of its adds
+    beside it.  The heavy-term kernel reads the heavy terms' int8 doc rows (128 B
+    per doc) once and writes one int16 coarse sum per (query slot, doc):
+    HBM-bound; its int8 MFMA work (4 limb products of the heavy terms per (slot,
+    doc)) is given beside it."""
     import numpy as np
 
     import gpusparse as gs
@@ -385,6 +397,15 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
     lds = lds_peak()
     tr = measured_traffic(cfg_name, N, a.tile_log2, plan["hybrid"])
     phys = None if tr is None else tr.get("traffic_bytes_per_launch")
+    # the hybrid scorer's algorithmic bytes: coarse sums of the main launch's
+    # tiles, and the tail words once per (group of consecutive queries, term)
+    docs_main = max(0, min(N, n_tiles << a.tile_log2) - (S << a.tile_log2))
+    G = plan["group_size"]
+    word_reads = 0
+    for g0 in range(0, B, G):
+        t = qt_h[g0:g0 + G][in_lds[g0:g0 + G]]
+        word_reads += int(per_term[np.unique(t)].sum())
+    hd_bytes = 2 * B * docs_main + 4 * word_reads
     head = None
     head_ms = 0.0
     if plan["hybrid"] and timing.get("phases"):
@@ -409,15 +430,25 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
                               "frac": round(ops / (head_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}}
     ref_bytes = post_tiles * per_post
     ref_ms = avg_ms + head_ms
-    roof = {"bound": "lds_atomic", "achieved": round(adds_per_s / 1e9, 1),
-            "peak": None if lds is None else round(lds["peak"] / 1e9, 1),
-            "unit": "G LDS atomic adds/s (one per scored posting of a term added in LDS)",
-            "frac": None if lds is None else round(adds_per_s / lds["peak"], 4),
-            "traffic": phys,
-            "peak_source": None if lds is None else lds["source"],
-            # the packed copy's bank-aware order brings the adds close to the
-            # conflict-free rate, the higher ceiling
-            "frac_of_conflict_free_rate": None if lds is None else round(adds_per_s / lds["conflict_free"], 4),
+    lds_roof = {"bound": "lds_atomic", "achieved": round(adds_per_s / 1e9, 1),
+                "peak": None if lds is None else round(lds["peak"] / 1e9, 1),
+                "unit": "G LDS atomic adds/s (one per scored posting of a term added in LDS)",
+                "frac": None if lds is None else round(adds_per_s / lds["peak"], 4),
+                "peak_source": None if lds is None else lds["source"],
+                # the packed copy's bank-aware order brings the adds close to the
+                # conflict-free rate, the higher ceiling
+                "frac_of_conflict_free_rate": None if lds is None else round(adds_per_s / lds["conflict_free"], 4)}
+    if plan["hybrid"]:
+        roof = {"bound": "hbm", "achieved": round(hd_bytes / (avg_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(hd_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                "traffic": phys, "bytes_per_launch": hd_bytes,
+                "bytes_note": "algorithmic: int16 coarse heavy-term sum per (query, doc) of the launch's tiles "
+                              f"({2 * B * docs_main} B) + 4 B packed word per tail posting and group holding its "
+                              f"term ({4 * word_reads} B)",
+                "lds_atomic": lds_roof}
+    else:
+        roof = dict(lds_roof, traffic=phys)
+    roof.update({
             "hbm_physical": None if phys is None else {
                 "achieved": round(phys / (avg_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(phys / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -436,7 +467,7 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
             "kernel_ms_min": round(float(np.min(kern_ms)), 3),
             "scored_postings_per_launch": post_launch, "postings_in_launch_tiles": post_tiles,
             "search_call_ms_avg": round(float(np.mean(call_ms)), 3),
-            "batch_scored_postings": post_all}
+            "batch_scored_postings": post_all})
     return roof, plan, head
 
 
@@ -479,7 +510,8 @@ def workload_entry(a, index, qt, qw, k, hyb, cfg_name, index_h=None):
          "d2h_ms": round(m["d2h_ms"], 3), "dense_rows": m["timing"].get("dense_rows", 0)}
     if a.path == "fused" and m["timing"].get("score_kernel"):
         roof, plan, head = scorer_roofline(a, index, qt, T, k, hyb, m["timing"], cfg_name)
-        e.update({"hybrid": plan["hybrid"], "scorer_ms": roof["kernel_ms_avg"], "scorer_lds_frac": roof["frac"],
+        e.update({"hybrid": plan["hybrid"], "scorer_ms": roof["kernel_ms_avg"], "scorer_bound": roof["bound"],
+                  "scorer_frac": roof["frac"], "scorer_lds_frac": roof.get("lds_atomic", roof)["frac"],
                   "scorer_hbm_frac": None if roof["hbm_physical"] is None else roof["hbm_physical"]["frac"],
                   "heavy_terms_ms": None if head is None else head["ms"],
                   "heavy_terms_hbm_frac": None if head is None else head["frac"],
@@ -495,15 +527,47 @@ def workload_entry(a, index, qt, qw, k, hyb, cfg_name, index_h=None):
     return e
 
 
+def child_workload(a, cfg_name):
+    """A configuration measured by a fresh bench.py process (its own GPU context
+    and allocations: the same C5 search measured after the C3 workloads in this
+    process, whose buffers have come and gone, ran ~10% slower), with the same
+    steps, and the whole batch's parity when the CPU leg runs."""
+    import subprocess
+    cmd = [sys.executable, os.path.join(ROOT, "bench.py"), "--config", cfg_name, "--no-extra", "--no-cpu",
+           "--steps", str(a.steps), "--warmup", str(a.warmup), "--parity-queries", "0" if a.no_cpu else "100000"]
+    t0 = time.perf_counter()
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"{cfg_name} child bench failed ({r.returncode}): {r.stderr[-2000:]}")
+    c = json.loads(r.stdout.strip().splitlines()[-1])
+    roof = c.get("roofline") or {}
+    head = c.get("heavy_terms_kernel")
+    e = {"B": c["config"]["global_batch"], "k": c["config"]["k"], "queries_per_s": c["value"],
+         "ms_per_batch": c["ms_per_step"], "ms_per_batch_one_in_flight": c["ms_per_batch_one_in_flight"],
+         "d2h_ms": c["d2h_ms_per_batch"], "dense_rows": c["dense_rows"],
+         "hybrid": (c["config"].get("scorer") or {}).get("hybrid"), "scorer_ms": roof.get("kernel_ms_avg"),
+         "scorer_bound": roof.get("bound"), "scorer_frac": roof.get("frac"),
+         "scorer_lds_frac": (roof.get("lds_atomic") or roof).get("frac"),
+         "scorer_hbm_frac": (roof.get("hbm_physical") or {}).get("frac"),
+         "heavy_terms_ms": None if head is None else head["ms"],
+         "heavy_terms_hbm_frac": None if head is None else head["frac"],
+         "phases_ms": c.get("components_ms"), "parity": c.get("parity"),
+         "first_search_state_ms": (c.get("index_build") or {}).get("first_search_state_ms"),
+         "measured_in": "a child bench.py process: " + " ".join(["python3", "bench.py"] + cmd[2:]),
+         "child_wall_s": round(time.perf_counter() - t0, 1)}
+    log(f"{cfg_name} B={e['B']} k={e['k']}: {e['ms_per_batch']:.2f} ms/batch, {e['queries_per_s']:.0f} q/s"
+        + (f", scorer {e['scorer_ms']:.2f} ms" if e["scorer_ms"] is not None else "")
+        + ("" if not e["parity"] else f", parity {e['parity']['ids_equal'] and e['parity']['scores_equal']}"))
+    return e
+
+
 def main():
     a = parse()
     if a.summarize_traffic:
         from gpusparse import synth
         cfg = synth.CONFIGS[a.config]
         n_docs = a.n_docs or cfg.docs.n_rows
-        from gpusparse.index import DEFAULT_TILE_LOG2_PACKED
-        tile = a.tile_log2 or DEFAULT_TILE_LOG2_PACKED
-        summarize_traffic(a.summarize_traffic, cfg.name, n_docs, tile, a.copy_bytes or (1 << 30))
+        summarize_traffic(a.summarize_traffic, cfg.name, n_docs, a.tile_log2 or None, a.copy_bytes or (1 << 30))
         return
     if a.copy_bytes:
         copy_only(a.copy_bytes)
@@ -577,8 +641,12 @@ def main():
     roof = plan = head = None
     if a.path == "fused" and timing.get("score_kernel"):
         roof, plan, head = scorer_roofline(a, index, qt, T, k, hyb, timing, cfg.name)
-        log(f"scoring kernel {roof['kernel_ms_avg']:.2f} ms avg: {roof['achieved']:.0f} G adds/s"
-            + ("" if roof["frac"] is None else f" ({100 * roof['frac']:.1f}% of the measured LDS atomic rate)")
+        lr = roof.get("lds_atomic", roof)
+        log(f"scoring kernel {roof['kernel_ms_avg']:.2f} ms avg"
+            + (f": {roof['achieved']:.0f} GB/s algorithmic ({100 * roof['frac']:.1f}% of HBM)"
+               if roof["bound"] == "hbm" else "")
+            + f", {lr['achieved']:.0f} G LDS adds/s"
+            + ("" if lr["frac"] is None else f" ({100 * lr['frac']:.1f}% of the measured LDS atomic rate)")
             + ("" if roof["hbm_physical"] is None else f", HBM {roof['hbm_physical']['achieved']:.0f} GB/s physical"))
         if head is not None:
             log(f"heavy-term kernel {head['ms']:.3f} ms: {head['achieved']:.0f} GB/s algorithmic "
@@ -677,20 +745,7 @@ def main():
         del index, index_h, out, m, timing
         gc.collect()
         torch.cuda.empty_cache()
-        c5 = synth.CONFIGS["C5"]
-        docs5, queries5 = synth.generate(c5)
-        ix5, _, _, t_state5, tile5, hyb5 = build(docs5)
-        del docs5
-        qt5, qw5, _ = gs.to_query_tensors(queries5, dev, weight_dtype=None)
-        tile_keep, a.tile_log2 = a.tile_log2, tile5
-        ix5_h = None
-        if not a.no_cpu:
-            from gpusparse.index import to_host
-            ix5_h = to_host(ix5)
-        extra["C5_B512_k1000"] = workload_entry(a, ix5, qt5, qw5, 1000, hyb5, "C5", ix5_h)
-        extra["C5_B512_k1000"]["first_search_state_ms"] = round(1000.0 * t_state5, 3)
-        a.tile_log2 = tile_keep
-        del ix5, ix5_h
+        extra["C5_B512_k1000"] = child_workload(a, "C5")
 
     res = {
         "metric": METRIC if (cfg.name == "C3" and k == 1000 and B == 512)
