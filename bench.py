@@ -15,7 +15,7 @@ on its launch stream.  Its unit of work is one scored posting of a term added in
 LDS (a (query, posting) pair), which is one LDS atomic add, and its bound is the
 LDS atomic rate measured on the same GPU type (profiles/lds_atomic_rates.json).
 Beside it: the physical HBM bytes per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE,
-calibrated by a copy kernel; profiles/traffic_k_score_union_<config>.json) as a
+calibrated by a copy kernel; profiles/traffic_k_score_union_[hybrid_]<config>.json) as a
 fraction of 8 TB/s, and the reference kernel's stream (4 B doc id + weight bytes
 per scored posting) as a labelled equivalent.  With the hybrid search (the 64
 heaviest terms as int8 matrix products) ``heavy_terms_kernel`` gives that
@@ -86,7 +86,8 @@ def parse():
                     help="streams the batches in flight take in turn (at most --inflight; 1: all on one stream, "
                          "so their kernels run one after another)")
     ap.add_argument("--summarize-traffic", default=None, metavar="DIR",
-                    help="write profiles/traffic_k_score_union_<config>.json from rocprofv3 --pmc runs under DIR")
+                    help="write profiles/traffic_k_score_union_[hybrid_]<config>.json from rocprofv3 --pmc "
+                         "runs under DIR")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run a plain device-to-device copy of this many bytes (PMC counter calibration)")
     return ap.parse_args()
@@ -108,8 +109,9 @@ def lds_peak():
             "source": os.path.relpath(path, ROOT) + ": ds_add_u32, random addresses"}
 
 
-def traffic_file(cfg_name):
-    return os.path.join(ROOT, "profiles", f"traffic_k_score_union_{cfg_name}.json")
+def traffic_file(cfg_name, hybrid=False):
+    """The committed traffic measurement of one configuration and scorer."""
+    return os.path.join(ROOT, "profiles", f"traffic_k_score_union_{'hybrid_' if hybrid else ''}{cfg_name}.json")
 
 
 def measured_traffic(cfg_name, n_docs, tile_log2, hybrid):
@@ -118,7 +120,7 @@ def measured_traffic(cfg_name, n_docs, tile_log2, hybrid):
     kernel: FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), when
     it was taken on this workload and scorer; None otherwise."""
     try:
-        with open(traffic_file(cfg_name)) as f:
+        with open(traffic_file(cfg_name, hybrid)) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
@@ -194,7 +196,7 @@ def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
                f"rocprofv3 --pmc FETCH_SIZE -d <out>/cf -o cf --output-format csv -- python3 bench.py --copy-bytes {copy_bytes}",
                f"rocprofv3 --pmc WRITE_SIZE -d <out>/cw -o cw --output-format csv -- python3 bench.py --copy-bytes {copy_bytes}",
                f"python3 bench.py --config {cfg_name} --summarize-traffic <out>"]}
-    with open(traffic_file(cfg_name), "w") as fh:
+    with open(traffic_file(cfg_name, hybrid), "w") as fh:
         json.dump(out, fh, indent=1)
     print(json.dumps(out), flush=True)
 
@@ -452,7 +454,7 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
             "hbm_physical": None if phys is None else {
                 "achieved": round(phys / (avg_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(phys / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                "source": os.path.relpath(traffic_file(cfg_name), ROOT)},
+                "source": os.path.relpath(traffic_file(cfg_name, plan["hybrid"]), ROOT)},
             "reference_stream_equiv": {
                 "bytes_per_launch": ref_bytes, "bytes_per_posting": per_post,
                 "GBs": round(ref_bytes / (ref_ms * 1e-3) / 1e9, 1),
