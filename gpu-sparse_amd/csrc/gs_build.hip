@@ -734,11 +734,12 @@ __global__ void k_pack_postings(const int32_t *__restrict__ doc, const void *__r
 // ranks each posting among its residue (64-lane ballot match plus the wave's
 // running counts) and writes its word to its place.  Few tiles per wave keep
 // a long list's work spread over many waves (with 64 tiles per wave a head
-// term's waves ran long after the rest had finished).  The placement's 4-byte
-// stores, 64 words apart, take most of the time (C3: 5.5 of 8.5 ms); staging a
-// sub-range in LDS to write it out contiguously was slower, though: with four
-// waves sharing a 64 KiB copy (two workgroups per CU) and barriers between
-// the phases, 20 ms.
+// term's waves ran long after the rest had finished).  The placement pass
+// takes most of the time (C3: 5.5 of 8.5 ms with the elementwise pass), in its
+// ranking rather than its scattered 4-byte stores: staging the sub-ranges of up
+// to 2048 postings in 8 KiB of LDS per wave, written out in order, changed
+// nothing (8.66 ms), and four waves sharing one sub-range in a 64 KiB copy (two
+// workgroups per CU, barriers between the phases) took 20 ms.
 constexpr int kArrangeUnroll = 4;  // 64-posting groups loaded together per lane
 constexpr int kArrangeTiles = 8;   // tiles of one term per wave
 
