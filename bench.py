@@ -369,6 +369,7 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
 
     import gpusparse as gs
     from gpusparse import _lib
+    from gpusparse.search import search_index
     B = qt.shape[0]
     kern_ms = [e0.elapsed_time(e1) for e0, e1 in timing["score_kernel"]]
     call_ms = [e0.elapsed_time(e1) for e0, e1 in timing["search"]]
@@ -378,7 +379,8 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
     plan = gs.search_plan(index, B, T, k, tile_log2=a.tile_log2, sample_tiles=a.sample_tiles, unroll=a.unroll,
                           tiles_per_wg=a.tiles_per_wg, hybrid=hyb)
     S = min(plan["seed_tiles"], n_tiles)
-    tb = index.aux()[("tile_bounds", a.tile_log2)]
+    sidx = search_index(index, plan["hybrid"])  # a uint8 index's hybrid search runs on its float16 copy
+    tb = sidx.aux()[("tile_bounds", a.tile_log2)]
     cols = tb[:, [S, n_tiles]].cpu().numpy().astype(np.int64)
     per_term = cols[:, 1] - cols[:, 0]
     all_term = index.lengths.cpu().numpy().astype(np.int64)
@@ -387,7 +389,7 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
     tq = np.where(valid, qt_h, 0)
     heavy = np.zeros(int(index.vocab_size), dtype=bool)
     if plan["hybrid"]:
-        heavy[index.aux()["heavy"].cpu().numpy()] = True
+        heavy[sidx.aux()["heavy"].cpu().numpy()] = True
     in_lds = valid & ~heavy[tq]
     post_launch = int((per_term[tq] * in_lds).sum())
     post_tiles = int((per_term[tq] * valid).sum())
@@ -588,7 +590,7 @@ def main():
     import gpusparse as gs
     from gpusparse import synth
     from gpusparse.index import ensure_search_state
-    from gpusparse.search import scorer_choice
+    from gpusparse.search import scorer_choice, search_index
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -617,7 +619,7 @@ def main():
         t_build = time.perf_counter() - t0
         t0 = time.perf_counter()
         tile, hyb = scorer_choice(ix, a.tile_log2 or None, want_hybrid)
-        ensure_search_state(ix, tile, hybrid=hyb)
+        ensure_search_state(search_index(ix, hyb), tile, hybrid=hyb)
         torch.cuda.synchronize()
         return ix, ev, t_build, time.perf_counter() - t0, tile, hyb
 

@@ -88,7 +88,53 @@ def query_tensors(index, query_batch, defer_check: bool = False):
 HYBRID_DEFAULT = True  # whether searches that name no scorer take the hybrid one
 
 
-def scorer_choice(index, tile_log2: int | None = None, hybrid: bool | None = None) -> tuple[int, bool]:
+U8_HYBRID_MAX_T = 258  # widest uint8 batch the float16 copy serves: 258 * 255 * 255 < 2^24
+
+
+def u8_float_copy(index):
+    """For a uint8 index: the same postings with the weights as float16 (exact
+    for 0..255), which the hybrid search runs on; built once, kept in aux()
+    (2 bytes per slot more HBM, plus that copy's own search state).  Its answers
+    are the exact integer sums: the fp64 rescoring sums integer products, and
+    the fp32 result of a sum below 2^24 is that sum."""
+    from .index import GPUInvertedIndex
+    a = index.aux()
+    f = a.get("f16_copy")
+    if f is None:
+        f = GPUInvertedIndex(doc_ids=index.doc_ids, scores=index.scores.to(torch.float16), offsets=index.offsets,
+                             lengths=index.lengths, padded_lengths=index.padded_lengths,
+                             max_scores=index.max_scores, num_docs=index.num_docs, vocab_size=index.vocab_size,
+                             device=_device_of(index))
+        a["f16_copy"] = f
+    return f
+
+
+def u8_hybrid_ok(index, T: int | None = None) -> bool:
+    """Whether a uint8 index can take the hybrid search through its float16 copy
+    for batches T terms wide: no list repeats a doc (so a doc's sum holds at
+    most T products of at most 255 * 255, below 2^24 for T <= 258, exact in
+    fp32) and the copy is eligible.  Reads the lists' duplicate counts once."""
+    if index.wtype != _lib.GS_W_U8 or int(index.num_docs) == 0:
+        return False
+    if T is not None and int(T) > U8_HYBRID_MAX_T:
+        return False
+    a = index.aux()
+    if "u8_hybrid_ok" not in a:
+        if "dup" not in a:
+            from .index import require_ascending
+            require_ascending(index)
+        a["u8_hybrid_ok"] = int(a["dup"].max().item()) == 0 and hybrid_eligible(u8_float_copy(index))
+    return a["u8_hybrid_ok"]
+
+
+def search_index(index, hybrid: bool):
+    """The index a search with this scorer runs on: a uint8 index's float16 copy
+    for the hybrid search, else the index itself."""
+    return u8_float_copy(index) if hybrid and index.wtype == _lib.GS_W_U8 else index
+
+
+def scorer_choice(index, tile_log2: int | None = None, hybrid: bool | None = None,
+                  T: int | None = None) -> tuple[int, bool]:
     """(tile_log2, hybrid) of a search.  hybrid: whether the index's heavy (64 longest)
     lists are scored as int8 matrix products (the hybrid search) instead of LDS
     adds; None takes HYBRID_DEFAULT when the index allows it.  hybrid=True
@@ -97,12 +143,15 @@ def scorer_choice(index, tile_log2: int | None = None, hybrid: bool | None = Non
     per workgroup) for the hybrid search and to index.default_tile_log2 (8192
     docs, two queries) otherwise: the terms left to the LDS adds of the hybrid
     search are rarely shared by the queries of a group, while longer runs per
-    (term, tile) halve the per-run work (C3 scoring 5.68 vs 6.24 ms)."""
+    (term, tile) halve the per-run work (C3 scoring 5.68 vs 6.24 ms).  A uint8
+    index takes the hybrid search through its float16 copy (u8_hybrid_ok; T =
+    the batch width, when known)."""
+    ok = u8_hybrid_ok(index, T) if index.wtype == _lib.GS_W_U8 else hybrid_eligible(index)
     if hybrid is None:
-        hybrid = HYBRID_DEFAULT and hybrid_eligible(index)
-    if hybrid and not hybrid_eligible(index):
-        raise ValueError("the hybrid search needs float weights with finite values and heavy lists without "
-                         "repeated docs")
+        hybrid = HYBRID_DEFAULT and ok
+    if hybrid and not ok:
+        raise ValueError("the hybrid search needs finite weights, heavy lists without repeated docs, and for "
+                         f"uint8 weights no repeated docs at all and batches of at most {U8_HYBRID_MAX_T} terms")
     if tile_log2 is None:
         tile_log2 = DEFAULT_TILE_LOG2_HYBRID if hybrid else default_tile_log2(index)
     return int(tile_log2), bool(hybrid)
@@ -166,14 +215,15 @@ class PendingSearch:
     The returned tensors are ordered on the search's stream: the stream current
     at the `result()` call is made to wait for it."""
 
-    __slots__ = ("_out", "_stream", "_event", "_status_h", "_finish")
+    __slots__ = ("_out", "_stream", "_event", "_status_h", "_finish", "_post")
 
-    def __init__(self, out, stream=None, event=None, status_h=None, finish=None):
+    def __init__(self, out, stream=None, event=None, status_h=None, finish=None, post=None):
         self._out = out
         self._stream = stream
         self._event = event
         self._status_h = status_h
         self._finish = finish
+        self._post = post  # applied to the results once, on the stream current at result()
 
     def done(self) -> bool:
         """True when result() would not wait for the GPU."""
@@ -192,6 +242,9 @@ class PendingSearch:
                 cur.wait_stream(self._stream)
                 for t in self._out:
                     t.record_stream(cur)  # freed only after the current stream's uses
+        if self._post is not None:
+            post, self._post = self._post, None
+            self._out = post(self._out)
         return self._out
 
 
@@ -203,7 +256,8 @@ def search(index, query_batch, k: int = 10, *, tile_log2: int | None = None, pat
 
     tile_log2: doc-tile size of the scorer (default: index.default_tile_log2).
     hybrid: the index's heavy (64 longest) lists as int8 matrix products, the other terms
-    as LDS adds (float indexes; scorer_choice); results are the same either way.
+    as LDS adds (scorer_choice; a uint8 index through its float16 copy); results
+    are the same either way.
     path: "auto" (dense when the [B, N] rows fit `dense_budget`), "fused" or "dense";
     k above MAX_K (8192) or queries wider than MAX_T (8192 terms) always take the
     dense path (any k up to the doc count, any width).
@@ -247,7 +301,27 @@ def search_async(index, query_batch, k: int = 10, *, tile_log2: int | None = Non
         qt = torch.full((B, 1), -1, dtype=torch.int32, device=dev)
         qw = torch.zeros((B, 1), dtype=qw.dtype, device=dev)
         T = 1
-    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid)
+    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid, T)
+    if hyb and index.wtype == _lib.GS_W_U8:
+        # the float16 copy's hybrid search; its fp32 scores are the exact sums.
+        # The weights' check (device weights) is copied out ahead of the search,
+        # so it has landed when result() has the search's status.
+        bad_h = None
+        if bad_w is not None:
+            bad_h = torch.empty((), dtype=torch.bool, pin_memory=True)
+            bad_h.copy_(bad_w, non_blocking=True)
+        inner = search_async(u8_float_copy(index), (qt, qw.to(torch.float32)), k, tile_log2=tile_log2, path=path,
+                             sample_tiles=sample_tiles, cand_cap=cand_cap, unroll=unroll, waves=waves,
+                             tiles_per_wg=tiles_per_wg, dense_budget=dense_budget, timing=timing,
+                             batch_order=batch_order, hybrid=True)
+
+        def to_int(out):
+            if bad_h is not None and bool(bad_h):
+                raise ValueError(_U8_WEIGHTS_MSG)
+            return out[0].to(torch.int32), out[1]
+
+        inner._post = to_int
+        return inner
     gidx = gs_index_struct(index, tile_log2, hyb)
     L = _lib.lib()
     acc_bytes = 4 if index.scores.dtype == torch.uint8 else 8
@@ -340,7 +414,8 @@ def search_plan(index, B: int, T: int, k: int, *, tile_log2: int | None = None, 
     (gs_search_plan): seed tiles, queries per group, postings per lane per chunk,
     tiles per scoring workgroup, whether the packed copy is read and whether the
     hybrid scorer runs."""
-    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid)
+    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid, T)
+    index = search_index(index, hyb)
     gidx = gs_index_struct(index, tile_log2, hyb)
     opts = _opts(sample_tiles, cand_cap, unroll, 0, tiles_per_wg, batch_order, hyb)
     info = _lib.GsSearchPlanInfo()
@@ -357,7 +432,8 @@ def search_counts(index, B: int, T: int, k: int, *, tile_log2: int | None = None
     """Per scoring slot of the fused search that last ran with these arguments:
     (docs the scorer emitted as candidates, candidates rescored in fp64), two
     numpy uint32 [B] arrays (gs_search_counts on the index's cached workspace)."""
-    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid)
+    tile_log2, hyb = scorer_choice(index, tile_log2, hybrid, T)
+    index = search_index(index, hyb)
     ws = index.aux().get("workspace")
     if ws is None:
         raise ValueError("no fused search has run on this index")

@@ -136,10 +136,12 @@ def test_c5_full_index(device):
     check_index("C5", device)
 
 
-def test_c5_full_search_bit_exact(device):
+@pytest.mark.parametrize("hybrid", [None, False])
+def test_c5_full_search_bit_exact(device, hybrid):
     """The integer configuration: uint8 x uint8 products summed in uint32,
-    bit-exact with the CPU integer reference, ties by ascending doc id."""
-    check_search("C5", device, 1000)
+    bit-exact with the CPU integer reference, ties by ascending doc id; by the
+    hybrid search on the index's float16 copy (the default) and by LDS adds."""
+    check_search("C5", device, 1000, hybrid=hybrid)
 
 
 def test_zz_release_full_size(device):

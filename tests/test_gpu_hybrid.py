@@ -163,15 +163,41 @@ def test_hybrid_large_repeated_heavy_weights(device):
     check(ix, ref, ti, tw, 50)
 
 
-def test_hybrid_not_for_uint8(device):
-    """uint8 indexes keep exact sums without rescoring, so they always add every
-    term in LDS: hybrid=True raises, the default plan is not hybrid."""
+def test_hybrid_uint8_through_float16_copy(device):
+    """A uint8 index takes the hybrid search on its float16 copy: int32 scores
+    equal to the exact uint32 sums, for uint8 and for integer float query
+    weights, equal to the LDS-only search's.  Batches wider than 258 terms (sums
+    could pass 2^24) and indexes whose lists repeat a doc fall back to LDS adds
+    (hybrid=True raises there); weights that are not integers in [0, 255] raise,
+    from device memory too."""
+    from gpusparse.search import U8_HYBRID_MAX_T
     rng = np.random.default_rng(14)
-    csr = zipf_csr(rng, 3000, 300, np.uint8)
+    csr = zipf_csr(rng, 6000, 300, np.uint8)
     ix = gs.build_from_csr(csr, device)
-    assert not gs.search_plan(ix, 8, 10, 20)["hybrid"]
-    with pytest.raises(ValueError, match="float"):
-        gs.search_plan(ix, 8, 10, 20, hybrid=True)
+    ref = oracle_index(csr)
+    ti, tw = zipf_queries(rng, 21, 300, np.uint8)
+    print("uint8 hybrid", flush=True)
+    for k in (1, 100, 6000):
+        check(ix, ref, ti, tw, k)
+        s, i = gs.search(ix, (torch.from_numpy(ti), torch.from_numpy(tw)), k, hybrid=False)
+        s2, i2 = gs.search(ix, (torch.from_numpy(ti).cuda(), torch.from_numpy(tw.astype(np.float32)).cuda()), k)
+        assert s.dtype == s2.dtype == torch.int32
+        assert torch.equal(s, s2) and torch.equal(i, i2)
+    with pytest.raises(ValueError, match="integers"):
+        gs.search(ix, (torch.from_numpy(ti).cuda(), torch.from_numpy(tw.astype(np.float32) + 0.5).cuda()), 10)
+    wide = np.full((3, U8_HYBRID_MAX_T + 1), -1, np.int32)
+    wide[:, :20] = ti[:3, :20]
+    ww = np.zeros(wide.shape, np.uint8)
+    ww[:, :20] = tw[:3, :20]
+    assert not gs.search_plan(ix, 3, wide.shape[1], 50)["hybrid"]
+    with pytest.raises(ValueError, match="258"):
+        gs.search_plan(ix, 3, wide.shape[1], 50, hybrid=True)
+    vs, _, vi = O.c_search(ref, wide, ww, 50, threads=8)
+    s, i = gs.search(ix, (torch.from_numpy(wide), torch.from_numpy(ww)), 50)
+    assert np.array_equal(i.cpu().numpy(), vi) and np.array_equal(s.cpu().numpy(), vs)
+    dup = random_csr(rng, 2000, 50, dtype=np.uint8, dup_rate=0.2)
+    ixd = gs.build_from_csr(dup, device)
+    assert not gs.search_plan(ixd, 4, 6, 20)["hybrid"]
 
 
 @pytest.mark.parametrize("vocab", [20, 64, 70, 128, 134])

@@ -590,10 +590,10 @@ def test_packed_scores_exact_under_near_ties(device, dtype, pattern, hybrid):
         assert_search_equal(ix, ref, ti, tw, k, path="fused", hybrid=hybrid)
 
 
-@pytest.mark.parametrize("hybrid", [None, False])
+@pytest.mark.parametrize("hybrid", [None, True, False])
 def test_search_u8_config_reduced(device, hybrid):
-    """uint8 impacts: exact uint32 sums, always from LDS adds (the hybrid search,
-    whose heavy-term start is rounded, serves float weights only)."""
+    """uint8 impacts: exact uint32 sums (int32 scores), by the hybrid search on
+    the index's float16 copy (the default) or by LDS adds of every term."""
     cfg = synth.scaled(synth.CONFIGS["C5"], n_docs=300_000, n_queries=64)
     docs, queries = synth.generate(cfg)
     ix = gs.build_from_csr(docs, device)
@@ -602,10 +602,10 @@ def test_search_u8_config_reduced(device, hybrid):
     assert_index_equal(ix, ref)
     ti, tw, _ = O.to_query_tensors(queries.indptr, queries.indices, queries.data)
     assert tw.dtype == np.uint8
-    assert not gs.search_plan(ix, len(ti), ti.shape[1], 1000, hybrid=hybrid)["hybrid"]
-    with pytest.raises(ValueError, match="float"):
-        gs.search_plan(ix, len(ti), ti.shape[1], 1000, hybrid=True)
-    assert_search_equal(ix, ref, ti, tw, 1000, path="fused", hybrid=hybrid)
+    want = HYBRID_DEFAULT if hybrid is None else hybrid
+    assert gs.search_plan(ix, len(ti), ti.shape[1], 1000, hybrid=hybrid)["hybrid"] == want
+    s, _ = assert_search_equal(ix, ref, ti, tw, 1000, path="fused", hybrid=hybrid)
+    assert s.dtype == np.int32
 
 
 @pytest.mark.parametrize("tile_log2", [10, 12, 13])
