@@ -720,39 +720,44 @@ __global__ void k_pack_postings(const int32_t *__restrict__ doc, const void *__r
 // scorer adds a sub-range's postings 64 at a time -- one ds_add_u32 per lane,
 // groups aligned to the sub-range's start -- into the words of their docs, and
 // postings whose docs agree mod 64 fall in one LDS bank.  Any order inside a
-// sub-range gives the same sums, so a sub-range of n > 64 postings (G groups,
-// the last one holding n_last = n - 64 (G - 1)) is rewritten "column-major by
-// residue": its postings sorted by (doc mod 64, doc) are dealt to the groups
-// in turn -- the k-th of them to group k mod G, position k / G, while every
-// group has room at that position (k < n_last * G), then to the first G - 1
-// groups only.  The postings of one residue land in different groups while
-// they last, so a group holds a residue ceil(count / G) times at most (2 for
-// random docs), where docs in ascending order pile 3-5 lanes onto one bank.
+// sub-range gives the same sums.  The sub-range is cut into blocks of
+// kArrangeBlock = 1024 postings from its start, and each block of n > 64
+// postings (G groups, the last one holding n_last = n - 64 (G - 1)) is
+// rewritten "column-major by residue": its postings sorted by (doc mod 64, doc)
+// are dealt to the groups in turn -- the k-th of them to group k mod G, position
+// k / G, while every group has room at that position (k < n_last * G), then to
+// the first G - 1 groups only.  The postings of one residue land in different
+// groups while they last, so a group holds a residue ceil(count / G) times at
+// most (2 for random docs), where docs in ascending order pile 3-5 lanes onto
+// one bank.
 // One wave per kArrangeTiles tiles of one term (lane j < kArrangeTiles holds
-// tile j's sub-range); the wave rewrites its sub-ranges of more than 64
-// postings one after the other: a pass counting residues, then a pass that
-// ranks each posting among its residue (64-lane ballot match plus the wave's
-// running counts) and writes its word to its place.  Few tiles per wave keep
-// a long list's work spread over many waves (with 64 tiles per wave a head
-// term's waves ran long after the rest had finished).  The placement pass
-// takes most of the time (C3: 5.5 of 8.5 ms with the elementwise pass), in its
-// ranking rather than its scattered 4-byte stores: staging the sub-ranges of up
-// to 2048 postings in 8 KiB of LDS per wave, written out in order, changed
-// nothing (8.66 ms), and four waves sharing one sub-range in a 64 KiB copy (two
-// workgroups per CU, barriers between the phases) took 20 ms.
-constexpr int kArrangeUnroll = 4;  // 64-posting groups loaded together per lane
-constexpr int kArrangeTiles = 8;   // tiles of one term per wave
+// tile j's sub-range); the wave takes the blocks of its sub-ranges one after the
+// other, in place in the packed copy that k_pack_postings has written in slot
+// order: every lane loads its words of the block (all loads in flight; a word's
+// offset bits give its doc's residue: (doc mod tile) mod 64, the scorer's bank,
+// which orders a sub-range's docs as doc mod 64 does), the residues are counted
+// in LDS, each posting is ranked among its residue (the lanes of its 64-posting
+// group with that residue OR their bits into an LDS mask; its rank is the count
+// of lower lanes in it, after the running count of the residue), its word goes
+// to its place in an LDS copy of the block, and the wave writes the copy back.
+// Dealing whole sub-ranges (up to 16384 postings at 16384-doc tiles) instead of
+// blocks puts each 64-posting group's words on 64 different cache lines: those
+// stores took 5.3 of that kernel's 7.4 ms at C3 (tile 14), where the blocked
+// pass takes 4.5 ms with the same scorer times.
+constexpr int kArrangeGroups = 16;                  // 64-posting groups per block
+constexpr int kArrangeBlock = 64 * kArrangeGroups;  // postings per block
+constexpr int kArrangeTiles = 8;                    // tiles of one term per wave
 
-template <int WT>
 __global__ void __launch_bounds__(256)
-    k_pack_arrange(const int32_t *__restrict__ doc, const void *__restrict__ w, const int64_t *__restrict__ offsets,
-                   const int32_t *__restrict__ tb, int32_t V, int64_t n_tiles, int32_t tile_log2, int32_t shift,
+    k_pack_arrange(const int64_t *__restrict__ offsets, const int32_t *__restrict__ tb, int32_t V, int64_t n_tiles,
                    uint32_t *__restrict__ out) {
-    __shared__ uint32_t s_cnt[4][64], s_run[4][64], s_below[4][64];
+    __shared__ uint32_t s_cnt[4][64], s_run[4][64];
+    __shared__ uint64_t s_peers[4][64];
+    __shared__ uint32_t s_block[4][kArrangeBlock];
     const int lane = gs_lane(), wave = threadIdx.x >> 6;
-    const uint32_t mask = (1u << tile_log2) - 1u;
     const int64_t per_term = (n_tiles + kArrangeTiles - 1) / kArrangeTiles;  // waves per term
     const int64_t gw = blockIdx.x * 4ll + wave;                               // this wave
+    s_peers[wave][lane] = 0;
     int64_t s = 0;
     int n = 0;
     if (gw < (int64_t)V * per_term && lane < kArrangeTiles) {
@@ -770,83 +775,73 @@ __global__ void __launch_bounds__(256)
         const int64_t ss = ((int64_t)__builtin_amdgcn_readlane((int)(s >> 32), src) << 32) |
                            (uint32_t)__builtin_amdgcn_readlane((int)s, src);
         const int nn = __builtin_amdgcn_readlane(n, src);
-        const int G = (nn + 63) >> 6, nl = nn - 64 * (G - 1);
-        s_cnt[wave][lane] = 0;
-        gs_wave_sync();
-        for (int c = 0; c < nn; c += 64 * kArrangeUnroll) {  // kArrangeUnroll loads in flight per lane
-            int32_t dv[kArrangeUnroll];
+        for (int b0 = 0; nn - b0 > 64; b0 += kArrangeBlock) {  // the blocks of more than 64 postings
+            const int nb = min(kArrangeBlock, nn - b0);
+            uint32_t *blk = out + ss + b0;
+            const int G = (nb + 63) >> 6, nl = nb - 64 * (G - 1);
+            // quotients below 1024 from a float reciprocal: within one, corrected below
+            const float rcp_g = 1.0f / (float)G, rcp_g1 = 1.0f / (float)(G - 1);
+            uint32_t wd[kArrangeGroups];
 #pragma unroll
-            for (int u = 0; u < kArrangeUnroll; ++u) {
-                const int i = c + u * 64 + lane;
-                dv[u] = i < nn ? doc[ss + i] : -1;
+            for (int u = 0; u < kArrangeGroups; ++u) {
+                const int i = u * 64 + lane;
+                wd[u] = i < nb ? blk[i] : 0u;
             }
-#pragma unroll
-            for (int u = 0; u < kArrangeUnroll; ++u)
-                if (dv[u] >= 0) atomicAdd(&s_cnt[wave][dv[u] & 63], 1u);
-        }
-        gs_wave_sync();
-        const uint32_t cnt = s_cnt[wave][lane];
-        uint32_t x = cnt;  // inclusive scan of the residue counts over the lanes
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const uint32_t o = __shfl_up(x, d, 64);
-            if (lane >= d) x += o;
-        }
-        s_below[wave][lane] = x - cnt;
-        s_run[wave][lane] = 0;
-        gs_wave_sync();
-        using store_t = typename gs_weight<WT>::store_t;
-        const store_t *wall = reinterpret_cast<const store_t *>(w);
-        for (int c = 0; c < nn; c += 64 * kArrangeUnroll) {
-            int32_t dv[kArrangeUnroll];
-            store_t wv[kArrangeUnroll];
-#pragma unroll
-            for (int u = 0; u < kArrangeUnroll; ++u) {
-                const int i = c + u * 64 + lane;
-                dv[u] = 0;
-                wv[u] = store_t(0);
-                if (i < nn) {
-                    dv[u] = doc[ss + i];
-                    wv[u] = wall[ss + i];
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kArrangeUnroll; ++u) {
-            const int i = c + u * 64 + lane;
-            const bool valid = i < nn;
-            const int32_t d = dv[u];
-            const uint32_t r = (uint32_t)d & 63u;
-            uint64_t peers = __ballot(valid);
-#pragma unroll
-            for (int bit = 0; bit < 6; ++bit) {
-                const bool on = (r >> bit) & 1u;
-                const uint64_t m = __ballot(on);
-                peers &= on ? m : ~m;
-            }
-            const uint32_t rank = __popcll(peers & gs_lanemask_lt());
-            uint32_t seen = 0, below = 0;
-            if (valid) {
-                seen = s_run[wave][r];
-                below = s_below[wave][r];
-            }
+            s_cnt[wave][lane] = 0;
             gs_wave_sync();
-            if (valid && rank == 0) s_run[wave][r] = seen + (uint32_t)__popcll(peers);
+#pragma unroll
+            for (int u = 0; u < kArrangeGroups; ++u)
+                if (u * 64 + lane < nb) atomicAdd(&s_cnt[wave][(wd[u] >> 2) & 63u], 1u);
             gs_wave_sync();
-            if (valid) {
-                const uint32_t k = below + seen + rank;  // place in (residue, doc) order
-                uint32_t grp, pos;
-                if (k < (uint32_t)(nl * G)) {
-                    pos = k / (uint32_t)G;
-                    grp = k - pos * (uint32_t)G;
-                } else {
-                    const uint32_t k2 = k - (uint32_t)(nl * G);
-                    const uint32_t q = k2 / (uint32_t)(G - 1);
-                    grp = k2 - q * (uint32_t)(G - 1);
-                    pos = (uint32_t)nl + q;
+            const uint32_t cnt = s_cnt[wave][lane];
+            uint32_t x = cnt;  // inclusive scan of the residue counts over the lanes
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t o = __shfl_up(x, d, 64);
+                if (lane >= d) x += o;
+            }
+            s_run[wave][lane] = x - cnt;  // next place of residue `lane` in (residue, doc) order
+            gs_wave_sync();
+#pragma unroll
+            for (int u = 0; u < kArrangeGroups; ++u) {
+                if (u >= G) continue;  // uniform: the block's groups only
+                const bool valid = u * 64 + lane < nb;
+                const uint32_t r = (wd[u] >> 2) & 63u;
+                if (valid) atomicOr(&s_peers[wave][r], 1ull << lane);
+                gs_wave_sync();
+                uint64_t peers = 0;
+                uint32_t seen = 0;
+                if (valid) {
+                    peers = s_peers[wave][r];
+                    seen = s_run[wave][r];
                 }
-                out[ss + (int64_t)grp * 64 + pos] = pack_word_of<WT>(d, wv[u], mask, shift);
+                gs_wave_sync();
+                const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(peers >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)peers, 0u));
+                if (valid && rank == 0) {  // the residue's first lane advances its place and clears its mask
+                    s_run[wave][r] = seen + (uint32_t)__popcll(peers);
+                    s_peers[wave][r] = 0;
+                }
+                if (valid) {
+                    // k < nb: group and position, k divided by G (k < nl G) or, past that, k - nl G by G - 1
+                    const uint32_t k = seen + rank;
+                    const bool all = k < (uint32_t)(nl * G);
+                    const uint32_t num = all ? k : k - (uint32_t)(nl * G);
+                    const uint32_t den = all ? (uint32_t)G : (uint32_t)(G - 1);
+                    uint32_t q = (uint32_t)((float)num * (all ? rcp_g : rcp_g1));
+                    const int32_t rem = (int32_t)(num - q * den);
+                    q = rem < 0 ? q - 1u : (rem >= (int32_t)den ? q + 1u : q);
+                    const uint32_t grp = num - q * den, pos = all ? q : (uint32_t)nl + q;
+                    s_block[wave][grp * 64 + pos] = wd[u];
+                }
+                gs_wave_sync();
             }
+#pragma unroll
+            for (int u = 0; u < kArrangeGroups; ++u) {
+                const int i = u * 64 + lane;
+                if (i < nb) blk[i] = s_block[wave][i];
             }
+            gs_wave_sync();  // the next block reuses the LDS copy and counts
         }
     }
 }
@@ -1449,8 +1444,7 @@ extern "C" int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d,
         if (vec) k_pack_postings<WT, true><<<gv, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, w_shift, out);
         else k_pack_postings<WT, false><<<g, 256, 0, s>>>(doc_ids_d, weights_d, n_slots, tile_log2, w_shift, out);
         if (tile_bounds_d && pairs > 0)
-            k_pack_arrange<WT><<<ga, 256, 0, s>>>(doc_ids_d, weights_d, offsets_d, tile_bounds_d, vocab, n_tiles,
-                                                  tile_log2, w_shift, out);
+            k_pack_arrange<<<ga, 256, 0, s>>>(offsets_d, tile_bounds_d, vocab, n_tiles, out);
     };
     switch (wtype) {
         case GS_W_F32: pack(std::integral_constant<int, GS_W_F32>{}); break;

@@ -379,9 +379,11 @@ def hybrid_eligible(index) -> bool:
                 require_ascending(index)
             if "heavy" not in a:
                 a["heavy"] = heavy_terms(index)
-            h = a["heavy"]
-            h = h[h >= 0].long()
-            ok = h.numel() > 0 and int(a["dup"][h].max().item()) == 0 and pack_shift(index) is not None
+            # small host copies (the heavy ids, the [vocab] counts): no device
+            # reduction on the way to the first search
+            h = a["heavy"].cpu().numpy()
+            h = h[h >= 0]
+            ok = h.size > 0 and int(a["dup"].cpu().numpy()[h].max()) == 0 and pack_shift(index) is not None
         a["hybrid_ok"] = bool(ok)
     return a["hybrid_ok"]
 
@@ -466,7 +468,10 @@ def pack_shift(index) -> int | None:
     of the index; 0 for uint8), or None when a weight is not finite."""
     if index.wtype == _lib.GS_W_U8:
         return 0
-    m = float(list_max_abs(index).max().item())
+    a = index.aux()
+    if "max_abs_all" not in a:
+        a["max_abs_all"] = float(np.max(list_max_abs(index).cpu().numpy()))  # NaN when a weight is NaN
+    m = a["max_abs_all"]
     if not math.isfinite(m):
         return None
     sh = C.c_int32(0)

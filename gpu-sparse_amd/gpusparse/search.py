@@ -123,7 +123,7 @@ def u8_hybrid_ok(index, T: int | None = None) -> bool:
         if "dup" not in a:
             from .index import require_ascending
             require_ascending(index)
-        a["u8_hybrid_ok"] = int(a["dup"].max().item()) == 0 and hybrid_eligible(u8_float_copy(index))
+        a["u8_hybrid_ok"] = int(a["dup"].cpu().numpy().max()) == 0 and hybrid_eligible(u8_float_copy(index))
     return a["u8_hybrid_ok"]
 
 

@@ -144,13 +144,17 @@ def pack_shift(max_abs: float) -> int:
     return s
 
 
+ARRANGE_BLOCK = 1024  # postings per block of the packed copy's bank-aware order
+
+
 def pack_postings(index: dict, tile_log2: int, shift: int | None = None, arrange: bool = True) -> np.ndarray:
     """Packed scoring copy (gs_pack_postings; no reference counterpart: a layout of
     its posting arrays), int32 [n]: per slot (doc mod 2^tile_log2) * 4 in bits 0-15
     and the weight in bits 16-31 -- the uint8 weight, or for float weights the
     int16 rint(w * 2^shift) (half to even, clamped to +-32767), shift defaulting to
     pack_shift of the largest |w|; padding slots (doc < 0) are 0.
-    arrange: each (term, tile) sub-range of n > 64 postings is rewritten in the
+    arrange: each (term, tile) sub-range is cut into blocks of ARRANGE_BLOCK
+    postings from its start, and each block of n > 64 postings is rewritten in the
     order arrange_order gives (the sums over a sub-range do not depend on it)."""
     doc = index["doc_ids"].astype(np.int64)
     w = index["scores"]
@@ -175,9 +179,10 @@ def pack_postings(index: dict, tile_log2: int, shift: int | None = None, arrange
         lst = doc[o:o + L]
         b = np.searchsorted(lst, edges, side="left")
         for lo, hi in zip(b[:-1], b[1:]):
-            if hi - lo > 64:
-                src = o + lo + arrange_order(lst[lo:hi])
-                out[o + lo: o + hi] = words[src]
+            for a in range(int(lo), int(hi), ARRANGE_BLOCK):
+                z = min(a + ARRANGE_BLOCK, int(hi))
+                if z - a > 64:
+                    out[o + a: o + z] = words[o + a + arrange_order(lst[a:z])]
     return out
 
 
@@ -203,8 +208,8 @@ def head_limbs(index: dict, heavy, n_rows: int, shift: int | None = None) -> np.
 
 
 def arrange_order(docs: np.ndarray) -> np.ndarray:
-    """Bank-aware order of one (term, tile) sub-range of n > 64 postings (docs
-    ascending): element i of the result is the sub-range index of the posting
+    """Bank-aware order of one block of n > 64 postings of a (term, tile) sub-range
+    (docs ascending): element i of the result is the block index of the posting
     placed at position i.  G = ceil(n / 64) groups of 64 positions, the last one
     n_last = n - 64 (G - 1) long.  The postings sorted by (doc mod 64, doc) are
     dealt out in turn: the k-th to group k mod G, position k // G while

@@ -263,25 +263,38 @@ def test_arrange_order_known_answers():
     assert list(got[:4]) == [0, 128, 2, 130] and list(got[64:68]) == [64, 192, 66, 194]
 
 
-def test_pack_arrangement_permutes_sub_ranges_only():
+def test_pack_arrangement_permutes_blocks_only():
+    """Each (term, tile) sub-range is rearranged in blocks of ARRANGE_BLOCK postings
+    from its start: a block of more than 64 postings is a permutation of itself in
+    the deal order of its own docs, a shorter one (a sub-range's tail) and every
+    short sub-range stay in slot order.  vocab 12 and 4096-doc tiles give
+    sub-ranges of about 1800 postings: two blocks each, the second one partial."""
     rng = np.random.default_rng(11)
     csr = random_csr(rng, 30000, 12, dtype=np.float16, dup_rate=0.05)
     ix = O.build_index(csr.indptr, csr.indices, csr.data, 30000, 12)
     tl = 12
     plain, arr = O.pack_postings(ix, tl, arrange=False), O.pack_postings(ix, tl)
-    moved = 0
+    moved, blocks, tails = 0, 0, 0
     edges = np.arange(((30000 + (1 << tl) - 1) >> tl) + 1, dtype=np.int64) << tl
     covered = np.zeros(len(plain), dtype=bool)
     for t in range(12):
         o, L = int(ix["offsets"][t]), int(ix["lengths"][t])
-        b = np.searchsorted(ix["doc_ids"][o:o + L], edges)
+        docs = ix["doc_ids"][o:o + L].astype(np.int64)
+        b = np.searchsorted(docs, edges)
         for lo, hi in zip(b[:-1], b[1:]):
             a, z = o + lo, o + hi
             assert np.array_equal(np.sort(arr[a:z]), np.sort(plain[a:z]))
-            if hi - lo > 64:
-                covered[a:z] = True
-                moved += int(np.count_nonzero(arr[a:z] != plain[a:z]))
+            for c in range(int(lo), int(hi), O.ARRANGE_BLOCK):
+                e = min(c + O.ARRANGE_BLOCK, int(hi))
+                if e - c > 64:
+                    want = plain[o + c:o + e][O.arrange_order(docs[c:e])]
+                    assert np.array_equal(arr[o + c:o + e], want)
+                    covered[o + c:o + e] = True
+                    moved += int(np.count_nonzero(arr[o + c:o + e] != plain[o + c:o + e]))
+                    blocks += 1
+                    tails += e - c < O.ARRANGE_BLOCK
     assert np.array_equal(arr[~covered], plain[~covered]) and moved > 0
+    assert blocks > tails > 0
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 17, 64, 1000])
