@@ -974,15 +974,28 @@ __global__ void __launch_bounds__(1024) k_heavy_terms(const int32_t *__restrict_
 // kHeavyTerms bytes, low = wq & 127 and high = wq >> 7 (arithmetic), for wq the
 // packed copy's integer weight of (d, heavy[h]) (pack_word_of) and 0 where doc d
 // lacks term h.  Every |wq| <= 16383 fits: low in [0, 127], high in [-128, 127].
-// One workgroup per kHeadFillDocs docs: per heavy term, a lane finds the term's
-// postings of those docs (binary search of the ascending list), the wave writes
-// their limbs into the block's rows staged in LDS, and the workgroup writes the
-// rows out whole (a byte scatter straight into the rows would cost a write
-// transaction per byte).  The lists hold each doc at most once (checked by the
-// caller); rows past n_docs stay zero.
-constexpr int kHeadFillDocs = 256;
-constexpr int kHeadRow = 2 * kHeavyTerms;  // bytes per row
-static_assert(kHeadFillDocs * kHeadRow <= 64 * 1024, "head fill stage fits 64 KiB of LDS");
+// One workgroup per kHeadFillBlocks consecutive blocks of kHeadFillDocs docs,
+// taken one after the other: per heavy term, a lane finds the term's postings
+// of the block (they start where the previous block's ended; their end is
+// searched within the block's width, which bounds it when the list holds each
+// doc at most once, and over the rest of the list otherwise), the waves write
+// their limbs into the block's rows staged in LDS (kHeadStrideWords words apart,
+// an odd number, so lanes on consecutive docs write distinct banks), and the
+// workgroup writes the rows out whole (a byte scatter straight into the rows
+// would cost a write transaction per byte), clearing the stage behind it.  The
+// block's postings of all heavy terms are taken as one flat range (an exclusive
+// scan of the per-term counts; a thread finds its posting's term by binary search
+// of it), kHeadFillUnroll per thread with their loads in flight together.
+// Rows past n_docs stay zero.  One block per workgroup with two full binary
+// searches per term and 128-byte rows in LDS (a 32-way bank conflict on every
+// byte write) took 2.25 ms at C3.
+constexpr int kHeadRow = 2 * kHeavyTerms;            // bytes per row
+constexpr int kHeadRowWords = kHeadRow / 4;
+constexpr int kHeadStrideWords = kHeadRowWords + 1;  // LDS row stride, odd
+constexpr int kHeadFillDocs = 32768 / kHeadRow;      // docs per block: 256 for 64 heavy terms
+constexpr int kHeadFillBlocks = 4;                   // blocks per workgroup
+constexpr int kHeadFillUnroll = 8;                   // postings per thread loaded together
+static_assert(kHeadFillDocs % 16 == 0 && kHeavyTerms <= 256, "head fill block shape");
 
 // the first position in doc[lo, hi) (ascending) holding a doc >= d
 __device__ __forceinline__ int64_t lower_doc(const int32_t *__restrict__ doc, int64_t lo, int64_t hi, int64_t d) {
@@ -999,40 +1012,95 @@ __global__ void __launch_bounds__(256)
     k_head_fill(const int32_t *__restrict__ doc, const void *__restrict__ w, const int64_t *__restrict__ offsets,
                 const int32_t *__restrict__ lengths, const int32_t *__restrict__ heavy, int32_t shift, int64_t n_docs,
                 int64_t n_rows, int8_t *__restrict__ head) {
-    __shared__ __align__(16) int8_t stage[kHeadFillDocs * kHeadRow];
+    __shared__ uint32_t stage[kHeadFillDocs * kHeadStrideWords];
     __shared__ int64_t s_lo[kHeavyTerms], s_hi[kHeavyTerms];
+    __shared__ uint32_t s_pre[kHeavyTerms], s_total;
     const int tid = threadIdx.x, lane = gs_lane(), wave = tid >> 6;
-    const int64_t d0 = (int64_t)blockIdx.x * kHeadFillDocs;
-    const int64_t d1 = min(d0 + kHeadFillDocs, n_docs);
-    for (int i = tid; i < kHeadFillDocs * kHeadRow / 16; i += blockDim.x)
-        reinterpret_cast<uint4 *>(stage)[i] = make_uint4(0, 0, 0, 0);
-    for (int h = tid; h < kHeavyTerms; h += blockDim.x) {
-        const int32_t t = heavy[h];
-        int64_t lo = 0, hi = 0;
-        if (t >= 0 && d0 < d1) {
-            const int64_t o = offsets[t], e = o + lengths[t];
-            lo = lower_doc(doc, o, e, d0);
-            hi = lower_doc(doc, lo, e, d1);
+    int8_t *stage8 = reinterpret_cast<int8_t *>(stage);
+    for (int i = tid; i < kHeadFillDocs * kHeadStrideWords; i += blockDim.x) stage[i] = 0u;
+    // thread h < kHeavyTerms follows heavy term h: [lo, e) its postings from the block on
+    int32_t t = -1;
+    int64_t lo = 0, e = 0;
+    if (tid < kHeavyTerms) {
+        t = heavy[tid];
+        if (t >= 0) {
+            lo = offsets[t];
+            e = lo + lengths[t];
         }
-        s_lo[h] = lo;
-        s_hi[h] = hi;
     }
-    __syncthreads();
     const auto *wall = reinterpret_cast<const typename gs_weight<WT>::store_t *>(w);
-    for (int h = wave; h < kHeavyTerms; h += blockDim.x / 64) {
-        for (int64_t i = s_lo[h] + lane; i < s_hi[h]; i += 64) {
-            const int32_t d = doc[i];  // in [d0, d1): the range above
-            // the packed word's weight half: uint8 0..255, or int16 rint(w 2^shift)
-            const int32_t wq = (int32_t)(int16_t)(pack_word_of<WT>(d, wall[i], 0u, shift) >> 16);
-            int8_t *row = stage + (int64_t)(d - d0) * kHeadRow;
-            row[h] = (int8_t)(wq & 127);
-            row[kHeavyTerms + h] = (int8_t)(wq >> 7);
+    const int64_t first = (int64_t)blockIdx.x * (kHeadFillBlocks * kHeadFillDocs);
+    for (int k = 0; k < kHeadFillBlocks; ++k) {
+        const int64_t d0 = first + (int64_t)k * kHeadFillDocs;
+        if (d0 >= n_rows) break;
+        const int64_t d1 = min(d0 + kHeadFillDocs, n_docs);
+        if (tid < kHeavyTerms) {
+            int64_t hi = lo;
+            if (t >= 0 && d0 < d1) {
+                if (k == 0) lo = lower_doc(doc, lo, e, d0);
+                const int64_t cap = min(e, lo + (d1 - d0));
+                hi = lower_doc(doc, lo, cap, d1);
+                if (hi == cap && cap < e && (int64_t)doc[cap] < d1) hi = lower_doc(doc, cap, e, d1);  // repeated docs
+            }
+            s_lo[tid] = lo;
+            s_hi[tid] = hi;
+            lo = hi;
         }
+        __syncthreads();
+        // the block's postings of all heavy terms in one flat range: term h's at
+        // [s_pre[h], s_pre[h] + s_hi[h] - s_lo[h])
+        if (wave == 0) {
+            uint32_t carry = 0;
+            for (int c = 0; c < kHeavyTerms; c += 64) {
+                const uint32_t v = (uint32_t)(s_hi[c + lane] - s_lo[c + lane]);
+                const uint32_t inc = gs_wave_incl_scan(v);
+                s_pre[c + lane] = carry + inc - v;
+                carry += __shfl(inc, 63, 64);
+            }
+            if (lane == 0) s_total = carry;
+        }
+        __syncthreads();
+        const uint32_t total = s_total;
+        for (uint32_t f0 = 0; f0 < total; f0 += 256u * kHeadFillUnroll) {
+            int32_t dv[kHeadFillUnroll], hv[kHeadFillUnroll];
+            typename gs_weight<WT>::store_t wv[kHeadFillUnroll];
+#pragma unroll
+            for (int u = 0; u < kHeadFillUnroll; ++u) {  // every load in flight before any is used
+                const uint32_t f = f0 + (uint32_t)(u * 256 + tid);
+                hv[u] = -1;
+                if (f < total) {
+                    int h = 0;  // the last term whose range starts at or before f (a non-empty one)
+#pragma unroll
+                    for (int step = kHeavyTerms / 2; step > 0; step >>= 1)
+                        if (s_pre[h + step] <= f) h += step;
+                    const int64_t i = s_lo[h] + (int64_t)(f - s_pre[h]);
+                    hv[u] = h;
+                    dv[u] = doc[i];  // in [d0, d1): the range above
+                    wv[u] = wall[i];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kHeadFillUnroll; ++u) {
+                const int h = hv[u];
+                if (h >= 0) {
+                    // the packed word's weight half: uint8 0..255, or int16 rint(w 2^shift)
+                    const int32_t wq = (int32_t)(int16_t)(pack_word_of<WT>(dv[u], wv[u], 0u, shift) >> 16);
+                    int8_t *row = stage8 + (int64_t)(dv[u] - d0) * (4 * kHeadStrideWords);
+                    row[h] = (int8_t)(wq & 127);
+                    row[kHeavyTerms + h] = (int8_t)(wq >> 7);
+                }
+            }
+        }
+        __syncthreads();
+        const int rows = (int)min<int64_t>(kHeadFillDocs, n_rows - d0);
+        uint32_t *out = reinterpret_cast<uint32_t *>(head + d0 * kHeadRow);
+        for (int i = tid; i < rows * kHeadRowWords; i += blockDim.x) {
+            const int r = i / kHeadRowWords, a = r * kHeadStrideWords + (i - r * kHeadRowWords);
+            out[i] = stage[a];
+            stage[a] = 0u;
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    const int64_t rows = min<int64_t>(kHeadFillDocs, n_rows - d0);
-    uint4 *out = reinterpret_cast<uint4 *>(head + d0 * kHeadRow);
-    for (int64_t i = tid; i < rows * kHeadRow / 16; i += blockDim.x) out[i] = reinterpret_cast<const uint4 *>(stage)[i];
 }
 
 // rank[t] = h for t = heavy[h], -1 for every other term
@@ -1478,7 +1546,8 @@ extern "C" int gs_head_fill(const int32_t *doc_ids_d, const void *weights_d, int
     k_head_rank<<<gs_blocks(vocab, 256), 256, 0, s>>>(vocab, head_rank_d);
     k_head_rank_set<<<1, kHeavyTerms, 0, s>>>(heavy_d, vocab, head_rank_d);
     GS_CHECK_LAUNCH();
-    const int64_t nb = (n_rows + kHeadFillDocs - 1) / kHeadFillDocs;  // every row written, zero past n_docs
+    const int64_t per_wg = (int64_t)kHeadFillBlocks * kHeadFillDocs;
+    const int64_t nb = (n_rows + per_wg - 1) / per_wg;  // every row written, zero past n_docs
     if (nb == 0) return GS_OK;
     GS_REQUIRE(nb < (1ll << 31), "too many head rows");
     switch (wtype) {
