@@ -170,20 +170,26 @@ __device__ __forceinline__ int64_t rs_tile(int64_t nblocks) {
     return x * q + (x < r ? x : r) + (p >> 3);
 }
 
-// Digit counts of one tile, per wave in LDS (waves do not contend on hot digits)
-// and summed at the end.  A whole, 16-byte aligned tile is read as four uint4
-// per thread, all in flight together (the order of the keys does not matter).
+// Digit counts of one tile in LDS, kRsHistCopies copies per wave (lane l adds
+// into copy l mod kRsHistCopies; the copies kRsHistStride words apart, so one
+// digit's counters sit in different banks), summed at the end: a hot digit (C3's
+// second pass: 46% of the term ids have high byte 0) is contended by 64 /
+// kRsHistCopies lanes of a wave instead of 64 (2.7 ms with one copy per wave,
+// against 1.0 ms for the evenly spread first digit).  A whole, 16-byte aligned
+// tile is read as four uint4 per thread, all in flight together (the order of
+// the keys does not matter).
+constexpr int kRsHistCopies = 8;
+constexpr int kRsHistStride = 257;
 __global__ void __launch_bounds__(kRsThreads) k_rs_hist(const uint32_t *__restrict__ key, int64_t n, int shift,
                                                         uint32_t *__restrict__ hist, int64_t nblocks) {
-    constexpr int kWaves = kRsThreads / 64;
-    __shared__ uint32_t h[kWaves][256];
-    const int tid = threadIdx.x, wave = tid >> 6;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) h[w][tid] = 0;
+    constexpr int kCopies = kRsThreads / 64 * kRsHistCopies;
+    __shared__ uint32_t h[kCopies * kRsHistStride];
+    const int tid = threadIdx.x, lane = gs_lane(), wave = tid >> 6;
+    for (int i = tid; i < kCopies * kRsHistStride; i += kRsThreads) h[i] = 0;
     __syncthreads();
     const int64_t tile = rs_tile(nblocks);
     const int64_t base = tile * kRsTile;
-    uint32_t *hw = h[wave];
+    uint32_t *hw = h + (wave * kRsHistCopies + (lane & (kRsHistCopies - 1))) * kRsHistStride;
     if (n - base >= kRsTile && ((uintptr_t)(key + base) & 15u) == 0) {
         static_assert(kRsTile == kRsThreads * 16, "four uint4 per thread");
         const uint4 *k4 = reinterpret_cast<const uint4 *>(key + base);
@@ -206,7 +212,7 @@ __global__ void __launch_bounds__(kRsThreads) k_rs_hist(const uint32_t *__restri
     __syncthreads();
     uint32_t c = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) c += h[w][tid];
+    for (int w = 0; w < kCopies; ++w) c += h[w * kRsHistStride + tid];
     hist[(int64_t)tid * nblocks + tile] = c;
 }
 
@@ -273,7 +279,7 @@ __global__ void __launch_bounds__(1024) k_scan_down(uint32_t *__restrict__ data,
 // (the scanned digit-major histogram).  FINAL (the last pass of the index
 // build): the entry of term k at sorted position pos goes to padded slot
 // pos + delta[k], as its doc id and weight.
-template <bool FINAL, int WT>
+template <bool FINAL, int WT, bool MASK_RANK>
 __global__ void __launch_bounds__(kRsThreads, 4)
     k_rs_scatter(const uint32_t *__restrict__ key_in, const uint32_t *__restrict__ doc_in,
                  const void *__restrict__ code_in, int src_code_bytes, int64_t n, int shift, int bits,
@@ -286,6 +292,7 @@ __global__ void __launch_bounds__(kRsThreads, 4)
     __shared__ uint32_t g_run[256];          // global position of this block's run of each digit
     __shared__ uint32_t l_off[256];          // start of each digit's run in the staged order
     __shared__ uint32_t wcnt[kWaves][256];   // per wave: digits seen, then the wave's offset in the run
+    __shared__ uint64_t peers_of[kWaves][256];  // per wave: the lanes of a round holding each digit
     __shared__ uint32_t sh[17];
     const int tid = threadIdx.x, wave = tid >> 6, lane = gs_lane();
     const int64_t tile = rs_tile(nblocks);
@@ -304,29 +311,56 @@ __global__ void __launch_bounds__(kRsThreads, 4)
         }
     }
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) wcnt[w][tid] = 0;
+    for (int w = 0; w < kWaves; ++w) {
+        wcnt[w][tid] = 0;
+        peers_of[w][tid] = 0;
+    }
     {
         const int64_t idx = (int64_t)tid * nblocks + tile;
         g_run[tid] = scanned[idx];
     }
     __syncthreads();
-    // 2. wave-local stable ranks (lp = rank among the wave's entries of that digit)
+    // 2. wave-local stable ranks (lp = rank among the wave's entries of that
+    // digit): the running count of the digit in the wave plus the lane's rank
+    // among the round's lanes holding it.  MASK_RANK: those lanes are found by
+    // ORing their bits into the digit's mask in LDS -- for digits that rarely
+    // repeat within a round (the index build's first pass: consecutive CSR
+    // entries are different terms); else by matching the digit's bits across the
+    // wave with ballots, for digits a round shares (a term id's top byte, 46% of
+    // C3's postings have high byte 0; a sorted list's doc-id bytes above the
+    // lowest), whose lanes would serialize on one LDS atomic: C3's index build
+    // 6.72 -> 6.54 ms with the mask in its first pass, the doc-major copy's
+    // passes 8.3 -> 9.0 ms with it.  Keys are below 2^(shift + bits).
 #pragma unroll
     for (int r = 0; r < kRsRounds; ++r) {
         const bool valid = wbase + r * 64 + lane < cnt;
         const uint32_t dig = (k[r] >> shift) & 255u;
-        uint64_t peers = __ballot(valid);
-        for (int b = 0; b < bits; ++b) {
-            const bool bit = (dig >> b) & 1u;
-            const uint64_t m = __ballot(bit);
-            peers &= bit ? m : ~m;
-        }
-        const uint32_t rank = __popcll(peers & gs_lanemask_lt());
+        uint64_t peers = 0;
         uint32_t seen = 0;
-        if (valid) seen = wcnt[wave][dig];
+        if (!MASK_RANK) {
+            peers = __ballot(valid);
+            for (int b = 0; b < bits; ++b) {
+                const bool bit = (dig >> b) & 1u;
+                const uint64_t m = __ballot(bit);
+                peers &= bit ? m : ~m;
+            }
+            if (valid) seen = wcnt[wave][dig];
+        } else {
+            if (valid) atomicOr(&peers_of[wave][dig], 1ull << lane);
+            gs_wave_sync();
+            if (valid) {
+                peers = peers_of[wave][dig];
+                seen = wcnt[wave][dig];
+            }
+        }
         gs_wave_sync();
+        const uint32_t rank =
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(peers >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)peers, 0u));
         lp[r] = seen + rank;
-        if (valid && rank == 0) wcnt[wave][dig] = seen + (uint32_t)__popcll(peers);
+        if (valid && rank == 0) {
+            wcnt[wave][dig] = seen + (uint32_t)__popcll(peers);
+            if (MASK_RANK) peers_of[wave][dig] = 0;
+        }
         gs_wave_sync();
     }
     __syncthreads();
@@ -402,9 +436,14 @@ __global__ void __launch_bounds__(kRsThreads, 4)
     for (int i = 0; i < kRsRounds; ++i) {
         const uint32_t v = s_buf[i * kRsThreads + tid];
         if (i * kRsThreads + tid < cnt) {
-            if (!FINAL)
-                code_out[dst[i]] = v;
-            else if (WT == GS_W_F32)
+            if (!FINAL) {  // the next pass reads the codes at their own width
+                if (WT == GS_W_F32)
+                    code_out[dst[i]] = v;
+                else if (WT == GS_W_F16)
+                    reinterpret_cast<uint16_t *>(code_out)[dst[i]] = (uint16_t)v;
+                else
+                    reinterpret_cast<uint8_t *>(code_out)[dst[i]] = (uint8_t)v;
+            } else if (WT == GS_W_F32)
                 reinterpret_cast<uint32_t *>(final_w)[dst[i]] = v;
             else if (WT == GS_W_F16)
                 reinterpret_cast<uint16_t *>(final_w)[dst[i]] = (uint16_t)v;
@@ -1243,17 +1282,18 @@ static int index_fill_impl(const int64_t *indptr_d, const int32_t *indices_d, co
             k_scan_down<<<(unsigned)p.nparts, 1024, 0, s>>>(hist, p.hist_n, parts);
             GS_CHECK_LAUNCH();
             if (last) {
-                k_rs_scatter<true, WT><<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(
+                k_rs_scatter<true, WT, false><<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(
                     key_in, doc_in, code_in, code_bytes, nnz, shift, bits, hist, p.nblocks, nullptr, nullptr,
                     nullptr, delta, doc_ids_d, weights_d);
             } else {
-                k_rs_scatter<false, WT><<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(
-                    key_in, doc_in, code_in, code_bytes, nnz, shift, bits, hist, p.nblocks, kb[cur], db[cur],
-                    cb[cur], nullptr, nullptr, nullptr);
+                // the lowest digit of the term ids of a CSR's consecutive entries rarely repeats
+                auto scatter = pass == 0 ? k_rs_scatter<false, WT, true> : k_rs_scatter<false, WT, false>;
+                scatter<<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(key_in, doc_in, code_in, code_bytes, nnz, shift,
+                                                                   bits, hist, p.nblocks, kb[cur], db[cur], cb[cur],
+                                                                   nullptr, nullptr, nullptr);
                 key_in = kb[cur];
                 doc_in = db[cur];
                 code_in = cb[cur];
-                code_bytes = 4;
                 cur ^= 1;
             }
             GS_CHECK_LAUNCH();
@@ -1457,7 +1497,7 @@ extern "C" int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, 
             k_scan_reduce<<<(unsigned)p.nparts, 1024, 0, s>>>(l.hist, p.hist_n, l.parts);
             k_scan_parts<<<1, 1024, 0, s>>>(l.parts, p.nparts);
             k_scan_down<<<(unsigned)p.nparts, 1024, 0, s>>>(l.hist, p.hist_n, l.parts);
-            k_rs_scatter<false, GS_W_F32><<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(
+            k_rs_scatter<false, GS_W_F32, false><<<(unsigned)p.nblocks, kRsThreads, 0, s>>>(
                 l.kb[cur], l.tb[cur], l.cb[cur], 4, nnz, shift, bits, l.hist, p.nblocks, l.kb[cur ^ 1],
                 l.tb[cur ^ 1], l.cb[cur ^ 1], nullptr, nullptr, nullptr);
             GS_CHECK_LAUNCH();
