@@ -1327,6 +1327,15 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
     gs_v4i ql[KB], qh[KB];
     int r;
     load_q(0, ql, qh, r);
+    constexpr int kHeadPiecesPerThread = 16 * kHeadBlock / 8 / 512;
+    static_assert(kHeadPiecesPerThread * 512 == 16 * kHeadBlock / 8, "whole pieces per thread");
+    int st_off[kHeadPiecesPerThread], out_off[kHeadPiecesPerThread];
+#pragma unroll
+    for (int j = 0; j < kHeadPiecesPerThread; ++j) {
+        const int i = tid + j * 512, row = i / (kHeadBlock / 8), col = (i % (kHeadBlock / 8)) * 8;
+        st_off[j] = row * kHeadStageRow + col;
+        out_off[j] = row * kHeadBlock + col;
+    }
     for (int rb = 0, buf = 0; rb < Bpad; rb += 16, buf ^= 1) {
         gs_v4i nl[KB], nh[KB];
 #pragma unroll
@@ -1353,8 +1362,9 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
                 const uint32_t h0 = ((uint32_t)c00[i] + ((uint32_t)cm[i] << 7) + ((uint32_t)c11[i] << 14)) << r;
                 const uint32_t h1 =
                     ((uint32_t)c00[i + 1] + ((uint32_t)cm[i + 1] << 7) + ((uint32_t)c11[i + 1] << 14)) << r;
-                w[i >> 1] = ((uint32_t)((int32_t)h0 >> kHeadShift) & 0xFFFFu) |
-                            ((uint32_t)((int32_t)h1 >> kHeadShift) << 16);
+                // floor(h / 2^16) of both, packed: the high half-words of h0 and h1 (one v_perm_b32)
+                static_assert(kHeadShift == 16, "the coarse sums are the high half-words");
+                w[i >> 1] = __builtin_amdgcn_perm(h1, h0, 0x07060302u);
             }
             const int d = (wave * CPW + c) * 16 + 4 * (lane >> 4);
             *reinterpret_cast<uint2 *>(st + (lane & 15) * kHeadStageRow + d) = make_uint2(w[0], w[1]);
@@ -1362,11 +1372,11 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
         // the stage is complete; the other one's copy-out (one block back) ended
         // before any wave got here, since it precedes this barrier in every wave
         __syncthreads();
-        for (int i = tid; i < 16 * kHeadBlock / 8; i += blockDim.x) {
-            const int row = i / (kHeadBlock / 8), col = (i % (kHeadBlock / 8)) * 8;
-            reinterpret_cast<uint4 *>(ob + (int64_t)(rb + row) * kHeadBlock)[col / 8] =
-                *reinterpret_cast<const uint4 *>(st + row * kHeadStageRow + col);
-        }
+        // 16-byte pieces tid and tid + 512 of the 16 rows (offsets fixed per thread)
+#pragma unroll
+        for (int j = 0; j < kHeadPiecesPerThread; ++j)
+            *reinterpret_cast<uint4 *>(ob + (int64_t)rb * kHeadBlock + out_off[j]) =
+                *reinterpret_cast<const uint4 *>(st + st_off[j]);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
             ql[kb] = nl[kb];
