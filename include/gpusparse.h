@@ -201,12 +201,13 @@ int gs_forward_fill(const int32_t *doc_ids_d, const void *weights_d, int32_t wty
  * the int16 rint(w * 2^w_shift) (clamped to +-32767; w_shift from gs_pack_shift
  * keeps every |value| <= 8191).  Padding slots (doc id < 0) hold 0.
  * With tile_bounds_d (gs_tile_bounds for this tile_log2; offsets_d, vocab and
- * n_docs of the index) the words of each (term, tile) sub-range of more than 64
- * postings are reordered so that each 64-posting group aligned to the sub-range's
- * start spreads its docs over the 64 residues mod 64 (the LDS banks of their
- * score words): sorted by (doc mod 64, doc), the k-th goes to group k mod G at
- * position k / G while all G groups have room there, then to the first G - 1.
- * With tile_bounds_d NULL the words stay in slot order.
+ * n_docs of the index) each (term, tile) sub-range is cut into blocks of 1024
+ * postings from its start, and the words of each block of more than 64 postings
+ * are reordered so that each 64-posting group aligned to the block's start
+ * spreads its docs over the 64 residues mod 64 (the LDS banks of their score
+ * words): sorted by (doc mod 64, doc), the k-th goes to group k mod G at
+ * position k / G while all G groups of the block have room there, then to the
+ * first G - 1.  With tile_bounds_d NULL the words stay in slot order.
  * tile_log2 <= 14; w_shift in [-200, 200] (ignored for GS_W_U8). */
 int gs_pack_postings(const int32_t *doc_ids_d, const void *weights_d, int32_t wtype, int64_t n_slots,
                      const int64_t *offsets_d, const int32_t *tile_bounds_d, int32_t vocab, int64_t n_docs,
