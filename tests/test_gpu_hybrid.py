@@ -79,10 +79,14 @@ def zipf_queries(rng, n, vocab, dtype, max_len=25, s=1.1):
 # ------------------------------------------------------------------ the dense head copy
 
 
-@pytest.mark.parametrize("dtype,n_docs", [(np.float32, 5000), (np.float16, 1537), (np.uint8, 700)])
+@pytest.mark.parametrize("dtype,n_docs", [(np.float32, 5000), (np.float16, 1537), (np.uint8, 700), (np.float16, 1500),
+                                         (np.float32, 300)])
 def test_head_copy_matches_oracle(device, dtype, n_docs):
     """gs_head_fill against oracle.head_limbs, byte for byte, rows up to the
-    last 512-doc block (zero past the docs), and the heavy-rank table."""
+    last 512-doc block (zero past the docs), and the heavy-rank table.  A
+    workgroup takes four 256-doc blocks: 1500 and 300 docs end their rows half
+    way through the last workgroup's blocks, 1537 and 700 leave a block without
+    docs."""
     from gpusparse.index import build_head
     rng = np.random.default_rng(n_docs)
     csr = zipf_csr(rng, n_docs, 400, dtype)

@@ -125,6 +125,35 @@ def test_packed_copy_matches_oracle(device, seed, dtype, tile_log2, vocab):
     assert np.array_equal(pk.words.cpu().numpy(), O.pack_postings(ref, tile_log2))
 
 
+@pytest.mark.parametrize("tile_log2", [12, 14])
+def test_packed_copy_block_boundaries(device, tile_log2):
+    """Bit for bit against the oracle, with (term, tile) sub-ranges sized around
+    the 1024-posting blocks of the bank-aware order: tails of 1, 63, 64 and 65
+    postings after whole blocks, single blocks just above 64 postings, and
+    sub-ranges filling a whole tile (docs at random, one term per size, two
+    tiles)."""
+    from gpusparse.index import build_packed
+    T = 1 << tile_log2
+    sizes = [65, 127, 1024, 1025, 1087, 1088, 1089, 2047, 2113, T - 1, T]
+    print(f"packed copy block boundaries tile_log2={tile_log2} sizes={sizes}", flush=True)
+    rng = np.random.default_rng(tile_log2)
+    rows, cols = [], []
+    for t, n in enumerate(sizes):
+        for j, m in enumerate((n, sizes[-1 - t])):  # tile 0 gets n postings, tile 1 another size
+            d = j * T + rng.choice(T, size=m, replace=False)
+            rows.append(d)
+            cols.append(np.full(m, t))
+    import scipy.sparse as sp
+    r, c = np.concatenate(rows), np.concatenate(cols)
+    w = rng.lognormal(-0.5, 0.8, size=len(r)).astype(np.float32)
+    m = sp.csr_matrix((w, (r, c)), shape=(2 * T, len(sizes)))
+    m.sort_indices()
+    csr = CSR(m.indptr.astype(np.int64), m.indices.astype(np.int32), m.data.astype(np.float16), m.shape)
+    ix = gs.build_from_csr(csr, device)
+    pk = build_packed(ix, tile_log2)
+    assert np.array_equal(pk.words.cpu().numpy(), O.pack_postings(oracle_index(csr), tile_log2))
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, np.uint8])
 def test_search_without_packed_copy(device, dtype):
     """The scorer reads the index arrays when the packed copy is absent (no room
