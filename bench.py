@@ -114,18 +114,19 @@ def traffic_file(cfg_name, hybrid=False):
     return os.path.join(ROOT, "profiles", f"traffic_k_score_union_{'hybrid_' if hybrid else ''}{cfg_name}.json")
 
 
-def measured_traffic(cfg_name, n_docs, tile_log2, hybrid):
+def measured_traffic(cfg_name, n_docs, tile_log2, hybrid, batch, k):
     """The committed rocprofv3 PMC measurement of this workload (HBM bytes per
     launch of the fused scorer and, for the hybrid search, of the heavy-term
     kernel: FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), when
-    it was taken on this workload and scorer; None otherwise."""
+    it was taken on this workload (collection, tile size, batch size, k) and
+    scorer; None otherwise."""
     try:
         with open(traffic_file(cfg_name, hybrid)) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
     if t.get("config") != cfg_name or t.get("n_docs") != n_docs or t.get("tile_log2") != tile_log2 or \
-            bool(t.get("hybrid", False)) != bool(hybrid):
+            bool(t.get("hybrid", False)) != bool(hybrid) or t.get("batch") != batch or t.get("k") != k:
         return None
     return t
 
@@ -177,8 +178,9 @@ def summarize_traffic(d, cfg_name, n_docs, tile_log2, copy_bytes):
     rf, rw = dispatches("f", ("k_rs_hist", "k_rs_scatter")), dispatches("w", ("k_rs_hist", "k_rs_scatter"))
     radix = [{"kernel": a[0], "fetch_bytes": round(a[1] * 1024 * fs), "write_bytes": round(b[1] * 1024 * ws)}
              for a, b in zip(rf, rw) if a[0] == b[0]]
+    from gpusparse import synth
     out = {"config": cfg_name, "n_docs": n_docs, "tile_log2": tile_log2, "kernel": "k_score_union",
-           "hybrid": hybrid,
+           "hybrid": hybrid, "batch": synth.CONFIGS[cfg_name].queries.n_rows, "k": synth.CONFIGS[cfg_name].k,
            "fetch_kib_per_launch": f, "write_kib_per_launch": w, "copy_bytes": copy_bytes,
            "copy_fetch_kib": cf, "copy_write_kib": cw, "fetch_scale": fs, "write_scale": ws,
            "fetch_bytes_per_launch": f * 1024 * fs, "write_bytes_per_launch": w * 1024 * ws,
@@ -399,7 +401,7 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
     avg_ms = float(np.mean(kern_ms))
     adds_per_s = post_launch / (avg_ms * 1e-3)
     lds = lds_peak()
-    tr = measured_traffic(cfg_name, N, a.tile_log2, plan["hybrid"])
+    tr = measured_traffic(cfg_name, N, a.tile_log2, plan["hybrid"], int(qt.shape[0]), k)
     phys = None if tr is None else tr.get("traffic_bytes_per_launch")
     # the hybrid scorer's algorithmic bytes: coarse sums of the main launch's
     # tiles, and the tail words once per (group of consecutive queries, term)
