@@ -966,7 +966,10 @@ __global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const
         // share its SIMDs: serving the waves that are further along first keeps
         // the workgroups apart, so that one's emission and set-up overlap the
         // other's adds.  (Lowering it instead, 3, 2, 1, 0, evened out the waves
-        // of a workgroup but drew the two workgroups into step.)
+        // of a workgroup but drew the two workgroups into step.)  The hybrid
+        // search's adds, a smaller part of its work in many short chunks, stay
+        // at priority 0 with no per-chunk bookkeeping: C3 scoring 5.30-5.35 vs
+        // 5.52-5.58 ms with the raising (5.48 with the levels counted but not set).
         const int my_total = (total - wave + NW - 1) / NW;  // chunks of this wave in the batch
         // level = floor(4 done / my_total), i.e. level >= L once done >= ceil(L
         // my_total / 4); only the next boundary is compared per chunk
@@ -974,6 +977,7 @@ __global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const
         int level = 0, next_at = quarter(1);
         __builtin_amdgcn_s_setprio(0);
         auto progress = [&](int done) {
+            if constexpr (HD) return;
             if (done < next_at) return;
             while (level < 3 && done >= quarter(level + 1)) ++level;
             next_at = level < 3 ? quarter(level + 1) : 0x7FFFFFFF;
