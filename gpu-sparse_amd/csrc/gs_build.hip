@@ -1579,6 +1579,11 @@ extern "C" int gs_head_fill(const int32_t *doc_ids_d, const void *weights_d, int
     GS_REQUIRE(n_docs >= 0 && n_rows >= n_docs, "head rows %lld fewer than the %lld docs", (long long)n_rows,
                (long long)n_docs);
     GS_REQUIRE(n_rows % 16 == 0, "head rows %lld not a multiple of 16", (long long)n_rows);
+    // gs_search's k_head_scores reads whole GS_HEAD_BLOCK-row blocks up to the
+    // last doc's block
+    GS_REQUIRE(n_rows >= (n_docs + GS_HEAD_BLOCK - 1) / GS_HEAD_BLOCK * GS_HEAD_BLOCK,
+               "head rows %lld fewer than the %lld docs rounded up to GS_HEAD_BLOCK (%d)", (long long)n_rows,
+               (long long)n_docs, GS_HEAD_BLOCK);
     GS_REQUIRE(wtype >= GS_W_F32 && wtype <= GS_W_U8, "unknown weight type %d", wtype);
     GS_REQUIRE(wtype == GS_W_U8 || (w_shift >= -200 && w_shift <= 200), "w_shift %d outside [-200, 200]", w_shift);
     GS_REQUIRE(doc_ids_d && weights_d && offsets_d && lengths_d && heavy_d && head_d && head_rank_d,

@@ -43,6 +43,12 @@ def test_argument_errors_map_to_python_exceptions():
     rc = L.gs_search(ctypes.byref(idx), None, None, 1, 1, 1, None, None, None, None, None, 0, None)
     with pytest.raises(ValueError):
         _lib.check(rc, "gs_search")
+    # the heavy-term rows must cover the last doc's whole GS_HEAD_BLOCK block,
+    # which the search reads; rejected before any pointer is used
+    n_docs = _lib.HEAD_BLOCK + 1
+    rc = L.gs_head_fill(None, None, 1, None, None, 8, None, 0, n_docs, n_docs + 15, None, None, None)
+    with pytest.raises(ValueError, match="rounded up to GS_HEAD_BLOCK"):
+        _lib.check(rc, "gs_head_fill")
 
 
 def test_pack_shift_matches_oracle():
