@@ -221,7 +221,7 @@ int gs_heavy_terms(const int32_t *lengths_d, int32_t vocab, int32_t *heavy_d, vo
 /* Dense copy of the heavy terms' weights for the hybrid search (no counterpart in
  * the reference: an operand of gs_search's int8 matrix products).  head_d int8
  * [n_rows][2][GS_HEAVY_TERMS], n_rows >= n_docs rounded up to GS_HEAD_BLOCK
- * (gs_search reads that many rows): row d holds, for h < GS_HEAVY_TERMS, the packed
+ * (gs_search reads that many rows; GS_EINVAL otherwise): row d holds, for h < GS_HEAVY_TERMS, the packed
  * copy's integer weight wq of (d, heavy_d[h]) -- the uint8 weight, or
  * rint(w * 2^w_shift) clamped to +-32767 -- as two limbs, wq & 127 at [d][0][h]
  * and wq >> 7 (arithmetic) at [d][1][h]; 0 where doc d lacks the term.  The
