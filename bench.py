@@ -1,11 +1,12 @@
 """Benchmark of the exact SPLADE search path on one MI355X.
 
-Default workload (BASELINE.json's metric): config C3 -- 8.8M synthetic docs
+Default workload (the headline metric): config C3 -- 8.8M synthetic docs
 (~1.06e9 postings, fp16 posting weights, fp32 accumulation), batches of 512
-queries, k = 1000.  A step is one ``search`` of one 512-query batch: fused
-LDS-tile scoring with threshold selection, candidate selection, fp64 rescoring
-and the status check.  Inputs (index and query batch) are resident in HBM before
-the timed region.
+queries, k = 1000.  A step is one ``search`` of one 512-query batch: the heavy
+terms' coarse sums (int8 matrix products), LDS-tile scoring of the other terms
+with threshold selection, candidate selection, fp64 rescoring and the status
+check.  Inputs (index and query batch) are resident in HBM before the timed
+region.
 
 Prints one JSON line.  ``value`` is queries/s with the results left in HBM (as
 the reference's benchmarks time it); ``queries_per_s_incl_d2h`` adds the

@@ -11,7 +11,7 @@ bench.py starts this file as a fresh child process that never touches a GPU:
     taskset -c <cpus> python3 oracle/cpu_baseline.py --dir D --cores C --k K --queries Q
 
 with OMP/MKL/OPENBLAS/NUMEXPR/RAYON_NUM_THREADS = C in its environment before
-the interpreter starts (the pinning of BASELINE.md's CPU plan, after
+the interpreter starts (the thread pinning the reference's CPU baselines use,
 baselines/seismic_k_calibration.py:50-53,99-117).  D holds the host copy of the
 index and the query batch as .npy files.  It prints one JSON line: wall
 seconds, CPU seconds of the whole process (getrusage: every thread), their
