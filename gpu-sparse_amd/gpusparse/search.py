@@ -3,8 +3,10 @@
 ``search(index, query_batch, k)`` is the batched retrieval call: scores and doc
 ids of the k best documents per query, ordered by score descending, ties by doc
 id ascending.  ``triton_fused_score`` (src/triton_kernel.py:159-200) keeps the
-reference's name and signature.  Both run the fused LDS-tile pipeline of
-``gs_search`` and finish the rare rows it flags with the dense path
+reference's name and signature.  Both run the fused pipeline of ``gs_search``
+(for float indexes whose heavy lists hold each doc once, the hybrid search: the
+heavy terms as int8 matrix products, the others added in LDS score tiles; else
+every term added in LDS) and finish the rare rows it flags with the dense path
 (``gs_search_dense``), or run the dense path directly when the full
 ``[B, num_docs]`` score rows are small.
 
