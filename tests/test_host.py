@@ -129,3 +129,14 @@ def test_dropin_modules_import():
         assert importlib.import_module("triton_kernel").triton_fused_score is gpusparse.triton_fused_score
     finally:
         sys.path.remove(d)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 ends with status 2 and a message,
+    before anything touches a device."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 2
+    assert "measures one GPU" in r.stderr and r.stdout == ""
