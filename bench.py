@@ -79,7 +79,7 @@ def parse():
                     help="skip the extra workloads (batch curve, k = 10, C5) after the headline")
     ap.add_argument("--path", default="fused", choices=["fused", "dense", "atomic"])
     ap.add_argument("--scorer", default="auto", choices=["auto", "hybrid", "lds"],
-                    help="fused scorer: hybrid (heavy terms as int8 MFMA products, 512-doc tiles), lds (LDS adds "
+                    help="fused scorer: hybrid (heavy terms as int8 MFMA products, 16384-doc tiles), lds (LDS adds "
                          "for every term) or auto (hybrid when the index allows it and no tile size is named)")
     ap.add_argument("--inflight", type=int, default=2,
                     help="batches in flight: batch i is queued before batch i - D's status is read (1: one at a time)")
@@ -357,15 +357,15 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
     posting (a (query, posting) pair of a valid query term), so the LDS-atomic
     issue rate bounds it, not HBM (each posting is fetched once per doc tile and
     query group and added to every query of the group holding its term).
-    Hybrid search: the heavy terms' part of every (query, doc) sum arrives as an
-    int16 coarse sum, and the other ("tail") terms are added in LDS, about a
+    Hybrid search: the heavy terms' part of every (query, doc) sum arrives as a
+    12-bit coarse sum, and the other ("tail") terms are added in LDS, about a
     tenth of the scored postings.  The scorer then streams its inputs: per
-    launch it reads the coarse sums of its tiles (2 B per (query, doc)) and, per
+    launch it reads the coarse sums of its tiles (1.5 B per (query, doc)) and, per
     query group and tile, the packed words of the group's tail terms (4 B per
     posting and group holding the term); those algorithmic bytes over its time,
     against the HBM peak, are its roofline, with the LDS-atomic rate of its adds
     beside it.  The heavy-term kernel reads the heavy terms' int8 doc rows (128 B
-    per doc) once and writes one int16 coarse sum per (query slot, doc):
+    per doc) once and writes one 12-bit coarse sum per (query slot, doc):
     HBM-bound; its int8 MFMA work (4 limb products of the heavy terms per (slot,
     doc)) is given beside it."""
     import numpy as np
@@ -412,7 +412,8 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
     for g0 in range(0, B, G):
         t = qt_h[g0:g0 + G][in_lds[g0:g0 + G]]
         word_reads += int(per_term[np.unique(t)].sum())
-    hd_bytes = 2 * B * docs_main + 4 * word_reads
+    coarse_bytes = 3 * B * docs_main // 2  # 12 bits per (query, doc)
+    hd_bytes = coarse_bytes + 4 * word_reads
     head = None
     head_ms = 0.0
     if plan["hybrid"] and timing.get("phases"):
@@ -421,16 +422,16 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
         rows = (N + HEAD_BLOCK - 1) // HEAD_BLOCK * HEAD_BLOCK
         cols_h = ((n_tiles << a.tile_log2) + HEAD_BLOCK - 1) // HEAD_BLOCK * HEAD_BLOCK
         n_heavy = _lib.heavy_term_count()  # lists taken as int8 matrix products
-        hbytes = rows * 2 * n_heavy + Bpad * cols_h * 2 + Bpad * 2 * n_heavy + B * 4
+        hbytes = rows * 2 * n_heavy + Bpad * cols_h * 3 // 2 + Bpad * 2 * n_heavy + B * 4
         ops = 4 * 2 * n_heavy * Bpad * rows
         hphys = None if tr is None else tr.get("head_traffic_bytes_per_launch")
-        head = {"kernel": f"k_head_scores (the {n_heavy} heavy terms as int8 MFMA limb products; int16 coarse sums "
+        head = {"kernel": f"k_head_scores (the {n_heavy} heavy terms as int8 MFMA limb products; 12-bit coarse sums "
                           "written block-major, the LDS slices' start)",
                 "bound": "hbm", "achieved": round(hbytes / (head_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(hbytes / (head_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                 "bytes_per_launch": hbytes, "traffic": hphys,
-                "bytes_note": "algorithmic: heavy int8 doc rows read once (128 B per doc) + one int16 coarse sum "
-                              "written per (query slot, doc) + query limbs",
+                "bytes_note": "algorithmic: heavy int8 doc rows read once (128 B per doc) + one 12-bit coarse sum "
+                              "(1.5 B) written per (query slot, doc) + query limbs",
                 "ms": round(head_ms, 3),
                 "mfma_int8": {"ops_per_launch": ops, "achieved": round(ops / (head_ms * 1e-3) / 1e12, 1),
                               "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
@@ -449,8 +450,8 @@ def scorer_roofline(a, index, qt, T, k, hyb, timing, cfg_name):
         roof = {"bound": "hbm", "achieved": round(hd_bytes / (avg_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(hd_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                 "traffic": phys, "bytes_per_launch": hd_bytes,
-                "bytes_note": "algorithmic: int16 coarse heavy-term sum per (query, doc) of the launch's tiles "
-                              f"({2 * B * docs_main} B) + 4 B packed word per tail posting and group holding its "
+                "bytes_note": "algorithmic: 12-bit coarse heavy-term sum (1.5 B) per (query, doc) of the launch's "
+                              f"tiles ({coarse_bytes} B) + 4 B packed word per tail posting and group holding its "
                               f"term ({4 * word_reads} B)",
                 "lds_atomic": lds_roof}
     else:

@@ -44,9 +44,11 @@ namespace {
 using namespace gs;
 
 constexpr int kRescoreCap = 16384;   // candidates rescored per query before the dense fallback
-constexpr int kHeadShift = 16;       // bits of the heavy-term sums dropped in their coarse copy
+constexpr int kHeadShift = 20;       // bits of the heavy-term sums dropped in their coarse copy (12 bits left)
 constexpr int kHeadBlock = GS_HEAD_BLOCK;  // docs per workgroup of k_head_scores
+constexpr int kHscRow = kHeadBlock * 3 / 2;  // bytes of one (doc block, slot) row of 12-bit coarse sums
 typedef uint32_t gs_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gs_u32x2 __attribute__((ext_vector_type(2)));
 constexpr int64_t kSeedMinDocs = 4096;    // fewest docs of the default first tiles scored with tau = 0
 constexpr int64_t kSeedDocs = 32768;      // most docs of the default first tiles scored with tau = 0
 constexpr int kDefaultCandCap = 65536;      // fewest candidate slots per query of the default cap
@@ -601,7 +603,7 @@ struct UnionArgs {
     const uint32_t *mfix;
     int32_t cap, k;
     int32_t local_k;  // > 0: threshold each slot at its tile's local k-th score too (seed launch)
-    const int16_t *hsc;  // HD: coarse heavy-term sums, block-major (k_head_scores), the slices' start
+    const uint8_t *hsc;  // HD: 12-bit coarse heavy-term sums, block-major rows (k_head_scores), the slices' start
     int64_t hsc_ld;      // slots per 512-doc block of hsc
 };
 
@@ -820,15 +822,19 @@ __global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const
     const pk_t *pkd = reinterpret_cast<const pk_t *>(a.pk);
 
     // The first tile's slices are set while the term loads are in flight: zero,
-    // or the coarse heavy-term sums c (int16) as c * 2^kHeadShift.  Those come
-    // as 8-doc (16-byte) pieces of the block-major k_head_scores output, at most
-    // kHeadPieces per thread (G * tile = 16 Ki docs), loaded for the next tile
-    // before the current tile's emission.
+    // or the 12-bit coarse heavy-term sums c as c * 2^kHeadShift.  Those come as
+    // 8-doc pieces of the block-major k_head_scores rows (8 high bytes and 4
+    // bytes of low nibbles), at most kHeadPieces per thread (G * tile = 16 Ki
+    // docs), loaded for the next tile before the current tile's emission.  (A
+    // thread's 8 docs are 32 bytes of its slice, as with 16-bit sums: 16-doc
+    // pieces, 64 bytes per thread, doubled the bank conflicts of the slices'
+    // set-up.)
     constexpr int kHeadPieces = (int)(kUnionTileLds / 4 / 8 / kUnionThreads);
-    uint4 hp[HD ? kHeadPieces : 1];
+    uint2 hp[HD ? kHeadPieces : 1];
+    uint32_t hn[HD ? kHeadPieces : 1];
     auto load_head = [&](int tile) {
         if constexpr (HD) {
-            const int per_log2 = a.tile_log2 - 3;
+            const int per_log2 = a.tile_log2 - 3;  // 8-doc pieces per slot of a tile
             const int64_t doc0 = (int64_t)tile << a.tile_log2;
 #pragma unroll
             for (int u = 0; u < kHeadPieces; ++u) {
@@ -836,11 +842,14 @@ __global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const
                 if (i < (nq << per_log2)) {
                     const int g = i >> per_log2;
                     const int64_t d = doc0 + ((int64_t)(i & ((1 << per_log2) - 1)) << 3);
-                    // read once: a non-temporal load keeps the L2 for the posting words
+                    const uint8_t *rp = a.hsc + ((d / kHeadBlock) * a.hsc_ld + grp * a.G + g) * kHscRow;
+                    const int o = (int)(d % kHeadBlock);
+                    // read once: non-temporal loads keep the L2 for the posting words
                     // (scoring 5.57 vs 5.65 ms at C3)
-                    const gs_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const gs_u32x4 *>(
-                        a.hsc + ((d / kHeadBlock) * a.hsc_ld + grp * a.G + g) * kHeadBlock + d % kHeadBlock));
-                    hp[u] = make_uint4(v.x, v.y, v.z, v.w);
+                    const gs_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const gs_u32x2 *>(rp + o));
+                    hp[u] = make_uint2(v.x, v.y);
+                    hn[u] = __builtin_nontemporal_load(
+                        reinterpret_cast<const uint32_t *>(rp + kHeadBlock + (o >> 1)));
                 }
             }
         } else {
@@ -850,14 +859,26 @@ __global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const
     auto zero_slices = [&]() {
         uint4 *z = reinterpret_cast<uint4 *>(acc);
         if constexpr (HD) {
-            static_assert(kHeadShift == 16, "slices take the coarse sums' bits in place");
+            // c * 2^20 = (high byte << 24) | (low nibble << 20): per doc one
+            // v_perm_b32 placing the high byte at byte 3 and the nibble's byte at
+            // byte 2 (shifted up by 4 for the even doc's low nibble), and one and
+            // clearing the other nibble (bits 16..19)
+            static_assert(kHeadShift == 20, "slices take the coarse sums' bits in place");
 #pragma unroll
             for (int u = 0; u < kHeadPieces; ++u) {
                 const int i = tid + u * kUnionThreads;
                 if (i < (nq << (a.tile_log2 - 3))) {
-                    const uint4 v = hp[u];
-                    z[2 * i] = make_uint4(v.x << 16, v.x & 0xFFFF0000u, v.y << 16, v.y & 0xFFFF0000u);
-                    z[2 * i + 1] = make_uint4(v.z << 16, v.z & 0xFFFF0000u, v.w << 16, v.w & 0xFFFF0000u);
+                    const uint32_t hw[2] = {hp[u].x, hp[u].y};
+                    const uint32_t nw = hn[u], nl = nw << 4;
+#pragma unroll
+                    for (int q4 = 0; q4 < 2; ++q4) {  // docs 4 q4 .. 4 q4 + 3 of the piece
+                        const uint32_t j0 = 2u * (uint32_t)q4;  // their nibbles' bytes j0, j0 + 1
+                        z[2 * i + q4] = make_uint4(
+                            __builtin_amdgcn_perm(hw[q4], nl, 0x04000C0Cu | (j0 << 16)) & 0xFFF00000u,
+                            __builtin_amdgcn_perm(hw[q4], nw, 0x05000C0Cu | (j0 << 16)) & 0xFFF00000u,
+                            __builtin_amdgcn_perm(hw[q4], nl, 0x06000C0Cu | ((j0 + 1) << 16)) & 0xFFF00000u,
+                            __builtin_amdgcn_perm(hw[q4], nw, 0x07000C0Cu | ((j0 + 1) << 16)) & 0xFFF00000u);
+                    }
                 }
             }
         } else {
@@ -1266,35 +1287,43 @@ __global__ void __launch_bounds__(kUnionThreads, HD ? 4 : 2) k_score_union(const
 // per 64 heavy terms in each, every one an exact int32 sum (|.| <= 2 * 256 * 128
 // * 128 = 2^23 for the middle one over 256 terms); the combination H is exact in
 // wrapping 32-bit arithmetic because it fits int32.  The slices start from
-// floor(H / 2^16) * 2^16, which is below H by less than 2^16: the margin grows
-// by 2^16 (k_query_prep_hybrid), so every doc that can reach the top k is still
-// rescored in fp64, and the answers stay exact.
+// floor(H / 2^20) * 2^20, which is below H by less than 2^20: the margin grows
+// by 2^20 (k_query_prep_hybrid), so every doc that can reach the top k is still
+// rescored in fp64, and the answers stay exact.  (|H| < 2^31, so floor(H / 2^20)
+// takes 12 bits: bits 20..31 of H, the slice's start being H & 0xFFF00000.)
 
 
 typedef int32_t gs_v4i __attribute__((ext_vector_type(4)));
 
-// Coarse heavy-term sums of every (slot, doc): floor(H(s, d) / 2^16) as int16
-// (|H| < 2^31), block-major -- out[(b * Bpad + s) * 512 + (d mod 512)] for doc d
-// of 512-doc block b -- so that each workgroup writes one contiguous run, slots
-// 0..Bpad-1 (slots past B hold zero limbs); blocks past the head rows (docs
-// past the collection) hold zeros.  Eight waves, each holding its 4 blocks of
-// 16 docs as the A operands (per 64 heavy terms: lane = doc lane % 16, terms
-// 16 (lane / 16) .. + 15, two limbs) for every block of 16 slots (B operands:
-// the query limbs, same lane layout, loaded one block ahead).  A lane's 4
-// outputs are 4 consecutive docs of one slot (rows 4 (lane / 16) + i, column
-// lane % 16 of the 16x16 product); they go to an LDS stage of the 16 slots'
-// rows (double-buffered, rows padded so that the 16 rows of a store fall in
-// different banks), which the workgroup then writes out as 16-byte pieces, one
-// contiguous 16 KiB run per block of slots.  (Each wave writing its own 64 docs
-// of the rows, with no workgroup barrier, measured slower; so did int8 coarse
-// sums with a per-query shift: half the bytes, but their wider margin costs the
-// scorer and the rescoring more than the writes save.)
+// Coarse heavy-term sums of every (slot, doc): c = floor(H(s, d) / 2^20), 12
+// bits (|H| < 2^31), in rows of kHscRow bytes per (512-doc block b, slot s),
+// block-major -- row b * Bpad + s at byte (b * Bpad + s) * kHscRow -- so that
+// each workgroup writes one contiguous run, slots 0..Bpad-1 (slots past B hold
+// zero limbs).  A row holds its 512 docs' high bytes (bits 4..11 of c; doc d mod
+// 512 at byte d mod 512), then their low nibbles (bits 0..3 of c), two per
+// byte: doc d mod 512 at byte 512 + (d mod 512) / 2, in the low nibble for even
+// d.  Blocks past the head rows (docs past the collection) hold zeros.
+//
+// Eight waves, each holding its 4 blocks of 16 docs as the A operands (per 64
+// heavy terms: lane = doc lane % 16, terms 16 (lane / 16) .. + 15, two limbs)
+// for every block of 16 slots (B operands: the query limbs, same lane layout,
+// loaded one block ahead).  A lane's 4 outputs are 4 consecutive docs of one
+// slot (rows 4 (lane / 16) + i, column lane % 16 of the 16x16 product); their
+// high half-words (bits 16..31 of H) go to an LDS stage of the 16 slots' rows
+// (double-buffered, rows padded so that the 16 rows of a store fall in
+// different banks).  The workgroup then writes the rows out, 8 docs per thread
+// and step as 8 high bytes and 4 bytes of nibbles: one contiguous 12 KiB run
+// per block of slots.  (Packing the 12 bits before the stage held the kernel at
+// 84 VGPRs, two workgroups per CU instead of three.  Each wave writing its own
+// 64 docs of the rows, with no workgroup barrier, measured slower; so did int8
+// coarse sums with a per-query shift: fewer bytes, but their wider margin costs
+// the scorer and the rescoring more than the writes save.)
 constexpr int kHeadStageRow = kHeadBlock + 16;  // int16 per staged row (bank padding)
 
 __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ head, int64_t head_rows,
                                                      const int8_t *__restrict__ alimb,
                                                      const int32_t *__restrict__ hshift, int32_t B, int32_t Bpad,
-                                                     int16_t *__restrict__ out) {
+                                                     uint8_t *__restrict__ out) {
     constexpr int HT = kHeavyTerms;
     constexpr int KB = HT / 64;               // 64-term blocks of the products
     constexpr int CPW = kHeadBlock / 16 / 8;  // blocks of 16 docs per wave
@@ -1302,9 +1331,9 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
     const int lane = gs_lane(), tid = threadIdx.x;
     const int wave = gs_uniform(tid >> 6);
     const int64_t doc0 = (int64_t)blockIdx.x * kHeadBlock;
-    int16_t *ob = out + (int64_t)blockIdx.x * Bpad * kHeadBlock;
+    uint8_t *ob = out + (int64_t)blockIdx.x * Bpad * kHscRow;
     if (doc0 >= head_rows) {  // docs past the collection
-        for (int64_t i = tid; i < (int64_t)Bpad * kHeadBlock / 8; i += blockDim.x)
+        for (int64_t i = tid; i < (int64_t)Bpad * kHscRow / 16; i += blockDim.x)
             reinterpret_cast<uint4 *>(ob)[i] = make_uint4(0, 0, 0, 0);
         return;
     }
@@ -1331,15 +1360,9 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
     gs_v4i ql[KB], qh[KB];
     int r;
     load_q(0, ql, qh, r);
+    // 8-doc pieces of the 16 staged rows: piece i = row * (kHeadBlock / 8) + col / 8
     constexpr int kHeadPiecesPerThread = 16 * kHeadBlock / 8 / 512;
     static_assert(kHeadPiecesPerThread * 512 == 16 * kHeadBlock / 8, "whole pieces per thread");
-    int st_off[kHeadPiecesPerThread], out_off[kHeadPiecesPerThread];
-#pragma unroll
-    for (int j = 0; j < kHeadPiecesPerThread; ++j) {
-        const int i = tid + j * 512, row = i / (kHeadBlock / 8), col = (i % (kHeadBlock / 8)) * 8;
-        st_off[j] = row * kHeadStageRow + col;
-        out_off[j] = row * kHeadBlock + col;
-    }
     for (int rb = 0, buf = 0; rb < Bpad; rb += 16, buf ^= 1) {
         gs_v4i nl[KB], nh[KB];
 #pragma unroll
@@ -1366,8 +1389,7 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
                 const uint32_t h0 = ((uint32_t)c00[i] + ((uint32_t)cm[i] << 7) + ((uint32_t)c11[i] << 14)) << r;
                 const uint32_t h1 =
                     ((uint32_t)c00[i + 1] + ((uint32_t)cm[i + 1] << 7) + ((uint32_t)c11[i + 1] << 14)) << r;
-                // floor(h / 2^16) of both, packed: the high half-words of h0 and h1 (one v_perm_b32)
-                static_assert(kHeadShift == 16, "the coarse sums are the high half-words");
+                // the high half-words of h0 and h1 (one v_perm_b32): bits 16..31
                 w[i >> 1] = __builtin_amdgcn_perm(h1, h0, 0x07060302u);
             }
             const int d = (wave * CPW + c) * 16 + 4 * (lane >> 4);
@@ -1376,11 +1398,27 @@ __global__ void __launch_bounds__(512) k_head_scores(const int8_t *__restrict__ 
         // the stage is complete; the other one's copy-out (one block back) ended
         // before any wave got here, since it precedes this barrier in every wave
         __syncthreads();
-        // 16-byte pieces tid and tid + 512 of the 16 rows (offsets fixed per thread)
+        // 8-doc pieces tid and tid + 512 of the 16 rows.  c = bits 20..31 of H =
+        // bits 4..15 of the staged half-word: its high byte, and its bits 4..7
+        // as the low nibble, two docs per byte (the even doc's in the low
+        // nibble).  Buffer stores into this block of slots' 12 KiB run take
+        // 32-bit lane offsets: with 64-bit addresses the kernel held 92 VGPRs
+        // (two workgroups per CU), and spilled one of them at 80.
+        static_assert(kHeadShift == 20, "the coarse sums are bits 20..31");
+        const auto rs = gs_rsrc(ob + (int64_t)rb * kHscRow, 16 * kHscRow);
 #pragma unroll
-        for (int j = 0; j < kHeadPiecesPerThread; ++j)
-            *reinterpret_cast<uint4 *>(ob + (int64_t)rb * kHeadBlock + out_off[j]) =
-                *reinterpret_cast<const uint4 *>(st + st_off[j]);
+        for (int j = 0; j < kHeadPiecesPerThread; ++j) {
+            const uint32_t i = (uint32_t)(tid + j * 512);
+            const uint32_t row = i / (kHeadBlock / 8), col = (i % (kHeadBlock / 8)) * 8;
+            // docs col + 2k and col + 2k + 1 in word k
+            const uint4 u = *reinterpret_cast<const uint4 *>(st + row * kHeadStageRow + col);
+            const gs_u32x2 hv = {__builtin_amdgcn_perm(u.y, u.x, 0x07050301u),
+                                 __builtin_amdgcn_perm(u.w, u.z, 0x07050301u)};
+            auto nib2 = [](uint32_t v) { return ((v >> 4) & 0x0Fu) | ((v >> 16) & 0xF0u); };
+            const uint32_t nb = nib2(u.x) | (nib2(u.y) << 8) | (nib2(u.z) << 16) | (nib2(u.w) << 24);
+            __builtin_amdgcn_raw_buffer_store_b64(hv, rs, (int)(row * kHscRow + col), 0, 0);  // 8 high bytes
+            __builtin_amdgcn_raw_buffer_store_b32(nb, rs, (int)(row * kHscRow + kHeadBlock + col / 2), 0, 0);
+        }
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
             ql[kb] = nl[kb];
@@ -2017,7 +2055,7 @@ struct SearchPlan {
     int64_t hsc_ld;   // docs of the coarse heavy-term sums per slot: the tiles' docs rounded up to whole 512-doc blocks
     int8_t *alimb;
     int32_t *hshift;
-    int16_t *hsc;
+    uint8_t *hsc;
     int S, cap, rcap, unroll, G, n_groups, ecap, gt_np, tiles_per_wg;
     int32_t *u_term, *u_ebeg, *u_count;
     uint2 *e_sw;
@@ -2149,7 +2187,7 @@ SearchPlan plan_search(const gs_index *ix, int32_t B, int32_t T, int32_t k, cons
     if (p.hyb) {
         p.alimb = ar.take<int8_t>((size_t)p.Bpad * 2 * kHeavyTerms);
         p.hshift = ar.take<int32_t>((size_t)B);
-        p.hsc = ar.take<int16_t>((size_t)p.Bpad * (size_t)p.hsc_ld);
+        p.hsc = ar.take<uint8_t>((size_t)p.Bpad * (size_t)(p.hsc_ld / kHeadBlock) * kHscRow);
     }
     return p;
 }

@@ -282,7 +282,7 @@ int gs_search(const gs_index *index, const int32_t *q_terms_d, const void *q_wei
  * GS_ENOSPC, with a message, when the search needs more scratch than that
  * (gs_search_workspace reports the need): e.g. B = 512, T = 107, k = 1000 fits
  * with cand_cap <= 32768, and B <= 256 fits at the default caps (the hybrid search
- * needs 2 bytes more per query slot and doc, for its coarse heavy-term sums).  The scratch
+ * needs 1.5 bytes more per query slot and doc, for its coarse heavy-term sums).  The scratch
  * keeps the last call's contents; every call clears what it needs cleared.
  * The first call on each device looks up the array's device address
  * (hipGetSymbolAddress): make it outside stream capture.  Later calls record
